@@ -1,0 +1,288 @@
+// Encoder INT8 producer: per-frame GroupNorm(32) statistics, then a two-pass
+// norm / SiLU / causal + reflect pad recompute that writes padded INT8 directly
+// (opt/encoder_int8_norm.py:16-110, opt/encoder_fused_temporal_norm.py:12-51,
+// opt/encoder_fused_norm_bias.py:14-39, opt/encoder_int8_norm_recompute.py:11-48).
+//
+// x: fp16 NDHWC [D, H, W, C] (batch one, C in {128, 256}).  Output q: int8 NDHWC
+// [D+2, H+2, W+2, C], frames 0 and 1 zero, spatial reflect padding of 1.
+//
+// Launch sequence (all on the caller's stream, no host synchronisation):
+//   gn_partial   grid (chunks, D): per 256-pixel chunk and group, avg and M2
+//   gn_merge     grid D x 32 threads: Chan merge of the chunks -> (mean, rstd);
+//                also clears the absmax word
+//   norm_pack<0> every padded element's norm/SiLU value -> atomic absmax
+//   norm_pack<1> same values -> int8 with the per-tensor scale; writes the scale
+//
+// Fixed reduction order (shared with the CPU oracle): a chunk has PL = 256/(C/8)
+// pixel lanes; lane pl owns pixels pl, pl+PL, ...; per pixel the group's
+// channels are summed left to right and added to the lane's running sum; the
+// lanes combine by the halving tree off = PL/2 .. 1; chunks merge sequentially.
+#include "h3v_common.hpp"
+#include "h3v_abi.hpp"
+
+namespace h3v {
+namespace {
+
+constexpr int kGroups = 32;
+constexpr int kChunk = 256;
+constexpr int kNT = 256;
+
+__device__ __forceinline__ void load8(const uint16_t* p, float* v) {
+    u16x8 a = *reinterpret_cast<const u16x8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = h2f(a[e]);
+}
+
+// C channels, cg = C/32 channels per group, TPP = C/8 threads per pixel.
+template <int C, bool PRE_BIAS>
+__global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
+                                                  int hw, int nchunk, float* __restrict__ part_avg,
+                                                  float* __restrict__ part_m2) {
+    constexpr int CG = C / kGroups;
+    constexpr int TPP = C / 8;
+    constexpr int PL = kNT / TPP;
+    constexpr int STEPS = kChunk / PL;
+    constexpr int GPT = 8 / CG;                 // groups inside one thread's 8 channels
+    __shared__ float red[PL][kGroups];
+    __shared__ float avg_s[kGroups];
+
+    const int j = blockIdx.x, t = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int cv = tid % TPP, pl = tid / TPP;
+    const int p0 = j * kChunk;
+    const int npix = hw - p0 < kChunk ? hw - p0 : kChunk;
+    const uint16_t* base = x + ((int64_t)t * hw + p0) * C + cv * 8;
+
+    float pb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pb[e] = PRE_BIAS ? h2f(pre_bias[cv * 8 + e]) : 0.0f;
+    auto load = [&](int p, float* v) {
+        load8(base + (int64_t)p * C, v);
+        if constexpr (PRE_BIAS) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
+        }
+    };
+
+    float ls[GPT];
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi) ls[gi] = 0.0f;
+    for (int s = 0; s < STEPS; ++s) {
+        int p = pl + s * PL;
+        if (p >= npix) break;
+        float v[8];
+        load(p, v);
+#pragma unroll
+        for (int gi = 0; gi < GPT; ++gi) {
+            float ps = v[gi * CG];
+#pragma unroll
+            for (int i = 1; i < CG; ++i) ps = ps + v[gi * CG + i];
+            ls[gi] = ls[gi] + ps;
+        }
+    }
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi) red[pl][cv * GPT + gi] = ls[gi];
+    __syncthreads();
+    if (tid < kGroups) {
+        for (int off = PL / 2; off >= 1; off >>= 1)
+            for (int i = 0; i < off; ++i) red[i][tid] = red[i][tid] + red[i + off][tid];
+        avg_s[tid] = red[0][tid] / (float)(npix * CG);
+    }
+    __syncthreads();
+
+    float a[GPT], lm[GPT];
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi) { a[gi] = avg_s[cv * GPT + gi]; lm[gi] = 0.0f; }
+    for (int s = 0; s < STEPS; ++s) {
+        int p = pl + s * PL;
+        if (p >= npix) break;
+        float v[8];
+        load(p, v);
+#pragma unroll
+        for (int gi = 0; gi < GPT; ++gi) {
+            float dv = v[gi * CG] - a[gi];
+            float pm = dv * dv;
+#pragma unroll
+            for (int i = 1; i < CG; ++i) {
+                dv = v[gi * CG + i] - a[gi];
+                pm = pm + dv * dv;
+            }
+            lm[gi] = lm[gi] + pm;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int gi = 0; gi < GPT; ++gi) red[pl][cv * GPT + gi] = lm[gi];
+    __syncthreads();
+    if (tid < kGroups) {
+        for (int off = PL / 2; off >= 1; off >>= 1)
+            for (int i = 0; i < off; ++i) red[i][tid] = red[i][tid] + red[i + off][tid];
+        int64_t dst = ((int64_t)t * nchunk + j) * kGroups + tid;
+        part_avg[dst] = avg_s[tid];
+        part_m2[dst] = red[0][tid];
+    }
+}
+
+// One thread per (frame, group): sequential merge over chunks as in _merge.
+__global__ void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2, int hw, int nchunk,
+                         int cg, float eps, float* __restrict__ stats, uint32_t* __restrict__ amax_bits) {
+    const int t = blockIdx.x, g = threadIdx.x;
+    if (t == 0 && g == 0) *amax_bits = 0u;
+    if (g >= kGroups) return;
+    const float total = (float)(hw * cg);
+    const float* pa = part_avg + (int64_t)t * nchunk * kGroups + g;
+    const float* pm = part_m2 + (int64_t)t * nchunk * kGroups + g;
+    float san = 0.0f;
+    for (int j = 0; j < nchunk; ++j) {
+        int cnt = hw - j * kChunk < kChunk ? hw - j * kChunk : kChunk;
+        san = san + pa[(int64_t)j * kGroups] * (float)(cnt * cg);
+    }
+    const float mean = san / total;
+    float sv = 0.0f;
+    for (int j = 0; j < nchunk; ++j) {
+        int cnt = hw - j * kChunk < kChunk ? hw - j * kChunk : kChunk;
+        float dl = pa[(int64_t)j * kGroups] - mean;
+        float nj = (float)(cnt * cg);
+        sv = sv + (pm[(int64_t)j * kGroups] + (nj * dl) * dl);
+    }
+    float var = sv / total;
+    if (var < 0.0f) var = 0.0f;
+    stats[(t * kGroups + g) * 2] = mean;
+    stats[(t * kGroups + g) * 2 + 1] = rsqrt_rn(var + eps);
+}
+
+__device__ __forceinline__ int reflect(int i, int n) { return i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i); }
+
+// PASS 0: absmax of all padded values.  PASS 1: int8 with the per-tensor scale.
+template <int C, bool PRE_BIAS, int PASS>
+__global__ __launch_bounds__(kNT) void norm_pack(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
+                                                 const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+                                                 const float* __restrict__ stats, int d, int h, int w,
+                                                 uint32_t* __restrict__ amax_bits, int8_t* __restrict__ q,
+                                                 float* __restrict__ scale) {
+    constexpr int CG = C / kGroups;
+    constexpr int TPP = C / 8;
+    const int hp = h + 2, wp = w + 2;
+    const int64_t nvec = (int64_t)(d + 2) * hp * wp * TPP;
+    float s = 0.0f;
+    if constexpr (PASS == 1) {
+        s = e3_scale(__builtin_bit_cast(float, *amax_bits));
+        if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
+    }
+    float amax = 0.0f;
+    const int64_t stride = (int64_t)gridDim.x * kNT;
+    for (int64_t vi = (int64_t)blockIdx.x * kNT + threadIdx.x; vi < nvec; vi += stride) {
+        const int cv = (int)(vi % TPP);
+        const int64_t pix = vi / TPP;
+        const int jj = (int)(pix % wp);
+        const int64_t r = pix / wp;
+        const int ii = (int)(r % hp);
+        const int tp = (int)(r / hp);
+        const int t = tp - 2;
+        float z[8];
+        if (t >= 0) {
+            const int si = reflect(ii - 1, h), sj = reflect(jj - 1, w);
+            float v[8];
+            load8(x + (((int64_t)t * h + si) * w + sj) * C + cv * 8, v);
+            float gm[8], bt[8];
+            load8(gamma + cv * 8, gm);
+            load8(beta + cv * 8, bt);
+            if constexpr (PRE_BIAS) {
+                float pb[8];
+                load8(pre_bias + cv * 8, pb);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int g = (cv * 8 + e) / CG;
+                const float mean = stats[(t * kGroups + g) * 2];
+                const float rstd = stats[(t * kGroups + g) * 2 + 1];
+                float zz = rt16(((v[e] - mean) * rstd) * gm[e] + bt[e]);
+                z[e] = rt16(silu(zz));
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) z[e] = 0.0f;
+        }
+        if constexpr (PASS == 0) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(z[e]));
+        } else {
+            uint32_t lo = pack4(e3_quant(z[0], s), e3_quant(z[1], s), e3_quant(z[2], s), e3_quant(z[3], s));
+            uint32_t hi = pack4(e3_quant(z[4], s), e3_quant(z[5], s), e3_quant(z[6], s), e3_quant(z[7], s));
+            *reinterpret_cast<uint2*>(q + vi * 8) = make_uint2(lo, hi);
+        }
+    }
+    if constexpr (PASS == 0) {
+        __shared__ float red[kNT / 64];
+        amax = wave_max(amax);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float m = red[0];
+            for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
+            atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
+        }
+    }
+}
+
+template <int C, bool PB>
+void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta, float eps,
+                int d, int h, int w, int8_t* q, float* scale, float* stats, float* part, uint32_t* amax_bits,
+                hipStream_t stream) {
+    const int hw = h * w;
+    const int nchunk = (hw + kChunk - 1) / kChunk;
+    float* part_avg = part;
+    float* part_m2 = part + (int64_t)d * nchunk * kGroups;
+    hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
+                       part_m2);
+    hipLaunchKernelGGL(gn_merge, dim3(d), dim3(64), 0, stream, part_avg, part_m2, hw, nchunk, C / kGroups, eps, stats,
+                       amax_bits);
+    const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
+    int64_t want = (nvec + kNT - 1) / kNT;
+    unsigned blocks = (unsigned)(want > 16384 ? 16384 : want);
+    hipLaunchKernelGGL((norm_pack<C, PB, 0>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
+                       w, amax_bits, q, scale);
+    hipLaunchKernelGGL((norm_pack<C, PB, 1>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
+                       w, amax_bits, q, scale);
+}
+
+}  // namespace
+}  // namespace h3v
+
+using namespace h3v;
+
+extern "C" {
+
+int64_t h3v_gn_norm_pack_workspace_floats(int d, int h, int w) {
+    if (d <= 0 || h <= 0 || w <= 0) return -1;
+    int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
+    return 2 * (int64_t)d * nchunk * kGroups;
+}
+
+int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta,
+                        float eps, int c, int d, int h, int w, int8_t* q, float* scale, float* stats,
+                        float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
+    const char* what = "h3v_gn_norm_pack_i8";
+    H3V_REQUIRE(x && gamma && beta && q && scale && stats && workspace && amax_scratch, "%s: null pointer argument",
+                what);
+    H3V_REQUIRE(c == 128 || c == 256, "%s: C must be 128 or 256 (got %d)", what, c);
+    H3V_REQUIRE(d >= 1 && h >= 2 && w >= 2, "%s: requires D >= 1 and H, W >= 2", what);
+    H3V_REQUIRE((int64_t)c * (d + 2) * (h + 2) * (w + 2) < ((int64_t)1 << 31), "%s: padded output exceeds int32 index range",
+                what);
+    H3V_REQUIRE(eps > 0.0f, "%s: eps must be positive", what);
+    H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(beta, 16) && (!pre_bias || aligned(pre_bias, 16)) &&
+                    aligned(q, 8),
+                "%s: x, gamma, beta, pre_bias need 16-byte and q 8-byte alignment", what);
+    if (c == 128) {
+        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+    } else {
+        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+    }
+    return launch_status(what);
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Shared device helpers for the H3 VAE INT8 hot-path kernels (gfx950 / CDNA4).
+//
+// Numerics contract: every kernel is compiled with -ffp-contract=off, so a*b+c
+// is two roundings unless written as __builtin_fmaf.  Division and sqrtf are
+// IEEE correctly rounded (hipcc default -fhip-fp32-correctly-rounded-divide-sqrt).
+// FP16 conversion is round-to-nearest-even with subnormals kept.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace h3v {
+
+typedef _Float16 f16;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }
+__device__ __forceinline__ float rt16(float f) { return (float)(f16)f; }
+
+// exp(x) by Cody-Waite reduction and a degree-7 Taylor polynomial in Horner
+// form:  n = rint(x*log2 e),  r = (x - n*LN2_HI) - n*LN2_LO,  exp(x) = 2^n * P(r).
+// LN2_HI has 15 significant bits so n*LN2_HI is exact; |r| <= 0.35 keeps the
+// truncation error below 6e-9 relative; measured error <= 1.2 ulp.
+__device__ __forceinline__ float exp_f32(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.972084045410156f) return 0.0f;
+    const float LOG2E = 0x1.715476p+0f;
+    const float LN2_HI = 0x1.62e4p-1f;
+    const float LN2_LO = 0x1.7f7d1cp-20f;
+    float n = __builtin_rintf(x * LOG2E);
+    float r = x - n * LN2_HI;
+    r = r - n * LN2_LO;
+    float p = 0x1.a01a02p-13f;
+    p = p * r + 0x1.6c16c2p-10f;
+    p = p * r + 0x1.111112p-7f;
+    p = p * r + 0x1.555556p-5f;
+    p = p * r + 0x1.555556p-3f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    return __builtin_amdgcn_ldexpf(p, (int)n);
+}
+
+// SiLU written as the reference writes it: z / (1 + exp(-z)).
+__device__ __forceinline__ float silu(float z) { return z / (1.0f + exp_f32(-z)); }
+
+// 1/sqrt as two correctly rounded operations.
+__device__ __forceinline__ float rsqrt_rn(float x) { return 1.0f / __builtin_sqrtf(x); }
+
+// Row scale of the comfy-kitchen row quantizer: max(amax * fp32(1/127), 1e-30).
+__device__ __forceinline__ float q1_scale(float amax) {
+    float s = amax * (1.0f / 127.0f);
+    return s >= 1.0e-30f ? s : 1.0e-30f;
+}
+
+// One element of the row quantizer, d = fp32(fp16(scale)):
+// v = fp16(a / d); v = rint(v); NaN -> -128; clamp [-128, 127].
+__device__ __forceinline__ int q1_quant(float a, float d) {
+    float v = rt16(a / d);
+    v = __builtin_rintf(v);
+    if (v != v) return -128;
+    v = __builtin_fminf(127.0f, __builtin_fmaxf(-128.0f, v));
+    return (int)v;
+}
+
+// Per-tensor scale of the encoder activation quantizer: amax * fp32(1/127), 0 -> 1.
+__device__ __forceinline__ float e3_scale(float amax) {
+    float s = amax * (1.0f / 127.0f);
+    return s > 0.0f ? s : 1.0f;
+}
+
+// Encoder activation rounding: half away from zero as floor(t + 0.5), clamp +-127.
+__device__ __forceinline__ int e3_quant(float v, float s) {
+    float t = v / s;
+    float r = t >= 0.0f ? __builtin_floorf(t + 0.5f) : -__builtin_floorf(-t + 0.5f);
+    r = __builtin_fminf(127.0f, __builtin_fmaxf(-127.0f, r));
+    return (int)r;
+}
+
+// Pack four int8 values (low byte first) into one 32-bit word.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) |
+           ((uint32_t)(c & 0xff) << 16) | ((uint32_t)(d & 0xff) << 24);
+}
+
+// Wave-wide (64 lanes) max of a non-negative float.
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off >= 1; off >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace h3v

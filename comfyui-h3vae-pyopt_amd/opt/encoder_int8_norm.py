@@ -1,0 +1,49 @@
+"""INT8 producer for the batch-one H3 encoder prefix.
+
+Mirror of opt/encoder_int8_norm.py in fishelegs/ComfyUI-H3VAE-PyOpt
+(``quantized_temporal_norm_pad``, :77-110).  One call of
+``h3v_gn_norm_pack_i8`` runs per-frame GroupNorm(32) statistics, then two
+recompute passes of norm / FP16 round / SiLU / FP16 round / causal + reflect
+padding: the first finds the absmax, the second writes padded INT8 directly.
+No full-sized FP16 intermediate is allocated.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _hip
+
+
+def _validate(x, weight, bias, pre_bias):
+    if x.ndim != 5 or x.device.type != "cuda":
+        raise ValueError("INT8 norm producer requires a CUDA rank-5 input")
+    b, c, d, h, w = x.shape
+    if b != 1 or x.dtype != torch.float16 or c not in (128, 256) or d < 1 or min(h, w) < 2:
+        raise ValueError("INT8 norm producer requires batch-one FP16 C=128/256, D>=1, H/W>=2")
+    if c * (d + 2) * (h + 2) * (w + 2) >= 2**31:
+        raise ValueError("Padded output exceeds int32 index range")
+    for parameter in (weight, bias) + (() if pre_bias is None else (pre_bias,)):
+        if (parameter is None or parameter.shape != (c,) or parameter.dtype != x.dtype
+                or parameter.device != x.device or not parameter.is_contiguous()):
+            raise ValueError("Expected contiguous FP16 channel vectors on input device")
+
+
+def quantized_temporal_norm_pad(x, weight, bias, eps, *, pre_bias=None, return_stats=False):
+    """-> (q int8 [1, C, D+2, H+2, W+2] channels-last-3d, scale fp32 scalar)."""
+    _validate(x, weight, bias, pre_bias)
+    _hip.require_gfx950(x.device, "INT8 norm producer")
+    _, c, d, h, w = x.shape
+    x = x.contiguous(memory_format=torch.channels_last_3d)
+    qy = torch.empty((1, c, d + 2, h + 2, w + 2), device=x.device, dtype=torch.int8,
+                     memory_format=torch.channels_last_3d)
+    scale = torch.empty((), device=x.device, dtype=torch.float32)
+    stats = torch.empty((d, 32, 2), device=x.device, dtype=torch.float32)
+    nws = int(_hip.lib().h3v_gn_norm_pack_workspace_floats(d, h, w))
+    workspace = torch.empty((nws,), device=x.device, dtype=torch.float32)
+    scratch = torch.empty((1,), device=x.device, dtype=torch.int32)
+    _hip.call("h3v_gn_norm_pack_i8", _hip.ptr(x), _hip.ptr(pre_bias), _hip.ptr(weight), _hip.ptr(bias), float(eps),
+              c, d, h, w, _hip.ptr(qy), _hip.ptr(scale), _hip.ptr(stats), _hip.ptr(workspace), _hip.ptr(scratch),
+              _hip.stream(x.device))
+    if return_stats:
+        return qy, scale, stats
+    return qy, scale

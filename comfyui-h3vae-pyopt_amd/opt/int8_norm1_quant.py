@@ -1,0 +1,60 @@
+"""Residual / norm1 / INT8-QKV fusion.
+
+Mirror of opt/int8_norm1_quant.py in fishelegs/ComfyUI-H3VAE-PyOpt.
+``residual_qkv`` (:126-162) runs ``h3v_residual_norm1_quant`` in place on
+``h`` (raw = fma(o, g, h); h <- fp16(raw); the published W16 reduction tree
+for sum(raw^2); n = fp16((h * inv) * w); row quantization) followed by the
+INT8 QKV GEMM ``h3v_gemm_i8_dequant``.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _hip
+from ._checks import ROW_WIDTHS
+from .int8_swiglu_fused import prequantized_linear
+
+_EPS = 1.0e-5
+
+
+def produce_norm1(h, o, g, w, eps=_EPS):
+    """In-place h producer -> (q int8 [M, K], s fp32 [M, 1])."""
+    k = h.shape[-1]
+    m = h.numel() // k
+    q = torch.empty((m, k), device=h.device, dtype=torch.int8)
+    scale = torch.empty((m, 1), device=h.device, dtype=torch.float32)
+    _hip.call("h3v_residual_norm1_quant", _hip.ptr(h), _hip.ptr(o), _hip.ptr(g), _hip.ptr(w), float(eps), m, k,
+              _hip.ptr(h), _hip.ptr(q), _hip.ptr(scale), _hip.stream(h.device))
+    return q, scale
+
+
+def residual_qkv_impl(h, o, g, w, qw, ws, bias):
+    """In-place H producer followed by the INT8 QKV GEMM."""
+    k = h.shape[-1] if h.ndim else 0
+    tensors = (h, o, g, w, qw, ws) + (() if bias is None else (bias,))
+    if (h.ndim < 2 or k not in ROW_WIDTHS or h.numel() == 0 or o.shape != h.shape or g.shape != (k,)
+            or w.shape != (k,) or qw.ndim != 2 or qw.shape[1] != k or ws.shape != (qw.shape[0],)
+            or h.dtype != torch.float16 or o.dtype != torch.float16 or g.dtype != torch.float16
+            or w.dtype != torch.float16 or qw.dtype != torch.int8 or ws.dtype != torch.float32
+            or any(t.device != h.device or not t.is_contiguous() for t in tensors)
+            or (bias is not None and (bias.shape != (qw.shape[0],) or bias.dtype != torch.float16))):
+        raise ValueError(f"expected contiguous [..., K] FP16 inputs (K in {ROW_WIDTHS}) and INT8 QKV [N, K]")
+    if torch.is_grad_enabled():
+        raise RuntimeError("norm1 fusion requires inference/no_grad")
+    _hip.require_gfx950(h.device, "norm1 fusion")
+    if h.data_ptr() == o.data_ptr():
+        raise ValueError("residual H and FFN output must have distinct storage")
+    q, scale = produce_norm1(h, o, g, w)
+    return prequantized_linear(q, scale, qw, ws, bias).reshape(*h.shape[:-1], qw.shape[0])
+
+
+@torch.library.custom_op("h3vae_norm1::residual_qkv", mutates_args=("h",))
+def residual_qkv(h: torch.Tensor, o: torch.Tensor, g: torch.Tensor, w: torch.Tensor, qw: torch.Tensor,
+                 ws: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    return residual_qkv_impl(h, o, g, w, qw, ws, bias)
+
+
+@residual_qkv.register_fake
+def _fake_residual_qkv(h, o, g, w, qw, ws, bias):
+    del o, g, w, ws, bias
+    return h.new_empty((*h.shape[:-1], qw.shape[0]))

@@ -1,0 +1,160 @@
+/*
+ * h3vae_hip.h -- C ABI of libh3vae_hip.so, the MI355X (gfx950) kernels of the
+ * H3 video-VAE INT8 hot path.
+ *
+ * Conventions shared by every entry point:
+ *   - plain device pointers and sizes; fp16 tensors are passed as uint16_t
+ *     bit patterns, int8 as int8_t, scales as float;
+ *   - `stream` is a hipStream_t (NULL = the default stream); work is queued
+ *     asynchronously, nothing synchronises the host;
+ *   - no entry point allocates memory: scratch space is passed in by the caller;
+ *   - return 0 on success or an H3V_E* code; h3v_last_error() then holds the
+ *     message for the calling thread.  Shape, alignment and contract checks
+ *     run before anything is queued.
+ *
+ * Each declaration names the reference interface it replaces
+ * (fishelegs/ComfyUI-H3VAE-PyOpt, file:line).
+ */
+#ifndef H3VAE_HIP_H
+#define H3VAE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define H3V_ABI_VERSION 1
+
+#define H3V_OK 0
+#define H3V_EINVAL 1   /* shape / dtype / alignment / contract violation */
+#define H3V_ELAUNCH 2  /* the HIP runtime rejected a launch */
+
+#ifndef __HIP_PLATFORM_AMD__
+typedef struct ihipStream_t* hipStream_t;
+#endif
+
+/* ABI version of the loaded library (H3V_ABI_VERSION). */
+int h3v_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* h3v_last_error(void);
+
+/* ---- row quantization (comfy-kitchen 0.2.34 contract) -------------------
+ * Replaces the reference's restated CK row quantizer
+ * (opt/int8_ffn_up_fused.py:91-104 `quantize_act`, and the dynamic
+ * activation quant inside CK int8_linear, opt/kitchen_int8.py:20-37).
+ * x: fp16 [rows, cols]; q: int8 [rows, cols]; scale: fp32 [rows].
+ *   s = max(amax * fp32(1/127), 1e-30); d = fp16(s);
+ *   q = clamp(rint(fp16(x / d)), -128, 127), NaN -> -128.              */
+int h3v_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* q, float* scale,
+                  hipStream_t stream);
+
+/* SiLU(gate) * up then row quantization of x: fp16 [rows, 2*cols] = [gate | up].
+ * Replaces opt/int8_swiglu_fused.py:22-38 (`quant`) / :52-65 (`quantize_swiglu`). */
+int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* q, float* scale,
+                         hipStream_t stream);
+
+/* ---- INT8 GEMMs (int32 accumulation on MFMA) ---------------------------
+ * acc[m, n] = sum_k a[m, k] * w[n, k]; a: int8 [m, k], w: int8 [n, k], both
+ * row-major.  Dequant epilogue:
+ *   out = fp16(bias ? fma(fp32(acc) * a_scale[m], w_scale[n], fp32(bias[n]))
+ *                   : (fp32(acc) * a_scale[m]) * w_scale[n])
+ * Replaces the CK CUTLASS GEMM behind prequantized_linear
+ * (opt/int8_swiglu_fused.py:78-107, cutlass_int8_dequant). */
+int h3v_gemm_i8_dequant(const int8_t* a, const float* a_scale, const int8_t* w, const float* w_scale,
+                        const uint16_t* bias, uint16_t* out, int64_t m, int64_t n, int64_t k,
+                        hipStream_t stream);
+
+/* FFN-up GEMM with the paired SwiGLU epilogue.  w: int8 [2n, k] with gate rows
+ * 0..n-1 and up rows n..2n-1; w_scale, bias: [2n].  act: fp16 [m, n] =
+ *   fp16(silu(g) * u), g, u = fp32(fp16(dequant(acc of gate / up row))).
+ * Replaces opt/int8_ffn_up_fused.py:50-89 (`up_swiglu`). */
+int h3v_gemm_i8_swiglu(const int8_t* a, const float* a_scale, const int8_t* w, const float* w_scale,
+                       const uint16_t* bias, uint16_t* act, int64_t m, int64_t n, int64_t k,
+                       hipStream_t stream);
+
+/* Raw int32 accumulators of the same GEMM (exactness checks; tl.dot with
+ * out_dtype=int32 in opt/int8_ffn_up_fused.py:68-72). acc: int32 [m, n]. */
+int h3v_gemm_i8_i32(const int8_t* a, const int8_t* w, int32_t* acc, int64_t m, int64_t n, int64_t k,
+                    hipStream_t stream);
+
+/* ---- encoder convolution -----------------------------------------------
+ * Valid conv3d as implicit GEMM.  qx: int8 NDHWC [batch, d, h, w, cin] (already
+ * padded); qw: int8 [cout, kd*kh*kw*cin] with k = (kd, kh, kw, c), c fastest;
+ * x_scale: one fp32 on the device; w_scale: fp32 [cout]; bias: fp16 [cout] or
+ * NULL; out: fp16 NDHWC [batch, do, ho, wo, cout], do = (d-kd)/sd+1 etc.
+ * causal_skip != 0 promises that input frames 0 and 1 are zero (the fused
+ * producer's causal planes); taps that only read them are skipped (exact).
+ * Replaces _conv3d_from_quantized + implicit_conv3d_kernel
+ * (opt/encoder_int8.py:509-588, opt/encoder_int8_pipeline.py:15-119). */
+int h3v_conv3d_i8(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                  const uint16_t* bias, uint16_t* out, int batch, int cin, int d, int h, int w, int cout,
+                  int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip, hipStream_t stream);
+
+/* Raw int32 accumulators of the same convolution (exactness checks). */
+int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,
+                      int w, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                      hipStream_t stream);
+
+/* Per-tensor dynamic activation quant of a contiguous fp16 tensor of n
+ * elements: scale = amax * fp32(1/127) (0 -> 1), q = clamp(half-away(x/scale),
+ * +-127).  amax_scratch: one uint32 of device scratch.
+ * Replaces quantize_activation_tensor (opt/encoder_int8.py:384-426). */
+int h3v_tensor_quant_i8(const uint16_t* x, int64_t n, int8_t* q, float* scale, uint32_t* amax_scratch,
+                        hipStream_t stream);
+
+/* Float count of the workspace h3v_gn_norm_pack_i8 needs for a [d, h, w] input. */
+int64_t h3v_gn_norm_pack_workspace_floats(int d, int h, int w);
+
+/* Fused GroupNorm(32) / SiLU / causal + reflect pad / INT8 producer.
+ * x: fp16 NDHWC [d, h, w, c] (batch one, c in {128, 256}); pre_bias: fp16 [c]
+ * or NULL (v = fp16(v + pre_bias) first); gamma, beta: fp16 [c].
+ * q: int8 NDHWC [d+2, h+2, w+2, c]; scale: one fp32; stats: fp32 [d, 32, 2]
+ * (mean, rstd); workspace: h3v_gn_norm_pack_workspace_floats() floats;
+ * amax_scratch: one uint32.
+ * Replaces quantized_temporal_norm_pad (opt/encoder_int8_norm.py:77-110)
+ * with _partial/_partial_bias/_merge and recompute_pack. */
+int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta,
+                        float eps, int c, int d, int h, int w, int8_t* q, float* scale, float* stats,
+                        float* workspace, uint32_t* amax_scratch, hipStream_t stream);
+
+/* ---- decoder row producers (row width k in {1024, 2048, 4096}) ---------
+ * norm1: raw = fma(o, g, h); h_out = fp16(raw) (h_out may equal h: in place);
+ * ss = published W16 tree of raw^2; inv = 1/sqrt(ss/k + eps);
+ * n = fp16((fp32(h_out) * inv) * w); (q, scale) = row quantization of n.
+ * Replaces residual_norm_quant via _produce_norm1 (opt/int8_norm1_quant.py:113-123). */
+int h3v_residual_norm1_quant(const uint16_t* h, const uint16_t* o, const uint16_t* g, const uint16_t* w, float eps,
+                             int64_t m, int64_t k, uint16_t* h_out, int8_t* q, float* scale, hipStream_t stream);
+
+/* norm2: as norm1 with the plain tree of rounded squares.
+ * Replaces residual_quant (opt/int8_norm_quant.py:22-69). */
+int h3v_residual_rms_quant(const uint16_t* x, const uint16_t* a, const uint16_t* g, const uint16_t* w, float eps,
+                           int64_t m, int64_t k, uint16_t* h_out, int8_t* q, float* scale, hipStream_t stream);
+
+/* Block-0 RMSNorm: out = fp16((x * inv) * gamma), W16 tree of x^2.
+ * Replaces rms_fp16_x2_w16 (opt/decoder_block0_norm.py:39-95). */
+int h3v_rms_fp16(const uint16_t* x, const uint16_t* gamma, float eps, int64_t m, int64_t k, uint16_t* out,
+                 hipStream_t stream);
+
+/* Final residual + LayerNorm: raw = fma(o, gate, h);
+ * out = fp16(fma((raw - mean) * inv, gamma, beta)).
+ * Replaces final_residual_ln_w8 (opt/decoder_final_norm.py:35-86). */
+int h3v_residual_layernorm(const uint16_t* h, const uint16_t* o, const uint16_t* gate, const uint16_t* gamma,
+                           const uint16_t* beta, float eps, int64_t m, int64_t k, uint16_t* out,
+                           hipStream_t stream);
+
+/* ---- attention input ---------------------------------------------------
+ * QK RMSNorm (no affine) + rotate-half RoPE on the first rot_dim dims.
+ * qkv: fp16 [tokens, heads, 3*head_dim] (per head [q | k | v]);
+ * cosv, sinv: fp16 [tokens, rot_dim]; q, k: fp16 [tokens, heads, head_dim].
+ * head_dim must be 64 and rot_dim 48.
+ * Replaces qk_rope / _qk_rope (opt/decoder_fused_qk_rope.py:12-54). */
+int h3v_qk_rope(const uint16_t* qkv, const uint16_t* cosv, const uint16_t* sinv, int64_t tokens, int heads,
+                int head_dim, int rot_dim, float eps, uint16_t* q, uint16_t* k, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3VAE_HIP_H */

@@ -1,0 +1,203 @@
+"""GPU parity: row quantizers and INT8 GEMMs (through the C ABI) vs the CPU oracle.
+
+Integer outputs (int8 codes, int32 accumulators) and the fp16 epilogues must
+match bit for bit: the kernels and the oracle implement the same IEEE
+operation sequence.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_bitwise, bits16, np_
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _gen(seed=20261002):
+    return torch.Generator().manual_seed(seed)
+
+
+def _row_quant_gpu(ops, x):
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty(x.shape[0], dtype=torch.float32, device=DEV)
+    xd = x.to(DEV)
+    ops.hip.call("h3v_row_quant", ops.hip.ptr(xd), x.shape[0], x.shape[1], ops.hip.ptr(q), ops.hip.ptr(s),
+                 ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    return np_(q), np_(s)
+
+
+@pytest.mark.parametrize("m,k", [(1, 2048), (17, 2048), (129, 1024), (7188, 2048), (33, 8192), (5, 5), (3, 40),
+                                 (2, 16384)])
+def test_row_quant_matches_oracle(ops, oracle, m, k):
+    gen = _gen(m * 31 + k)
+    x = torch.randn(m, k, generator=gen).half()
+    if m > 2:
+        x[1] = 0                                    # zero row: q=-128, s=1e-30
+        x[2] = x[2] * 2.0 ** -20                    # rows whose fp16 scale is subnormal / zero
+    if m > 4:
+        x[3, 0] = 65504.0
+        x[4] = torch.tensor(2.0 ** -24).half()
+    q, s = _row_quant_gpu(ops, x)
+    rq, rs = oracle.row_quant(x.numpy())
+    assert_bitwise(q, rq, "q")
+    assert_bitwise(s.view(np.uint32), rs.view(np.uint32), "scale")
+    if m > 2:
+        assert (q[1] == -128).all() and s[1] == np.float32(1e-30)
+
+
+@pytest.mark.parametrize("m,k", [(1, 8192), (17, 4096), (129, 8192), (4, 5)])
+def test_swiglu_row_quant_matches_oracle(ops, oracle, m, k):
+    gen = _gen(k + m)
+    x = (torch.randn(m, 2 * k, generator=gen) * 3).half()
+    q = torch.empty((m, k), dtype=torch.int8, device=DEV)
+    s = torch.empty(m, dtype=torch.float32, device=DEV)
+    xd = x.to(DEV)
+    ops.hip.call("h3v_swiglu_row_quant", ops.hip.ptr(xd), m, k, ops.hip.ptr(q), ops.hip.ptr(s), ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    rq, rs = oracle.swiglu_row_quant(x.numpy())
+    assert_bitwise(np_(q), rq, "q")
+    assert_bitwise(np_(s).view(np.uint32), rs.view(np.uint32), "scale")
+
+
+def _i32_gpu(ops, a, w):
+    m, k = a.shape
+    n = w.shape[0]
+    acc = torch.empty((m, n), dtype=torch.int32, device=DEV)
+    ad, wd = a.to(DEV), w.to(DEV)
+    ops.hip.call("h3v_gemm_i8_i32", ops.hip.ptr(ad), ops.hip.ptr(wd), ops.hip.ptr(acc), m, n, k, ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    return np_(acc)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (17, 6144, 2048), (129, 512, 1024), (300, 200, 192),
+                                   (256, 256, 64), (5, 7, 33), (2, 3, 5)])
+def test_gemm_int32_accumulators_exact(ops, oracle, m, n, k):
+    gen = _gen(m + n + k)
+    a = torch.randint(-128, 128, (m, k), generator=gen, dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=gen, dtype=torch.int8)
+    got = _i32_gpu(ops, a, w)
+    want = a.numpy().astype(np.int64) @ w.numpy().astype(np.int64).T
+    assert np.array_equal(got, want)
+
+
+def test_gemm_int32_full_size_sampled_rows(ops):
+    """H3 QKV shape M=7188, N=6144, K=2048: every tile position, rows sampled across all M tiles."""
+    gen = _gen(7)
+    m, n, k = 7188, 6144, 2048
+    a = torch.randint(-128, 128, (m, k), generator=gen, dtype=torch.int8)
+    w = torch.randint(-128, 128, (n, k), generator=gen, dtype=torch.int8)
+    got = _i32_gpu(ops, a, w)
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), np.arange(m - 20, m), np.arange(0, 256, 7)]))
+    want = a.numpy()[rows].astype(np.int64) @ w.numpy().astype(np.int64).T
+    assert np.array_equal(got[rows], want)
+    # and a column checksum over all rows (checksum of checksums)
+    col = w.numpy().astype(np.int64)[:: 61]
+    assert np.array_equal(got[:, ::61].astype(np.int64).sum(0), (a.numpy().astype(np.int64).sum(0) @ col.T))
+
+
+@pytest.mark.parametrize("m,n,k,with_bias", [(1, 6144, 2048, True), (17, 2048, 2048, False), (129, 1024, 4096, True),
+                                             (300, 200, 192, True), (5, 7, 33, False)])
+def test_gemm_dequant_matches_oracle(ops, oracle, m, n, k, with_bias):
+    gen = _gen(m * 3 + n)
+    a = torch.randint(-128, 128, (m, k), generator=gen, dtype=torch.int8)
+    w = torch.randint(-31, 32, (n, k), generator=gen, dtype=torch.int8)
+    sx = (torch.rand(m, generator=gen) * 0.02 + 0.001).float()
+    sw = (torch.rand(n, generator=gen) * 0.02 + 0.001).float()
+    bias = torch.randn(n, generator=gen).half() if with_bias else None
+    out = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) if t is not None else None for t in (a, sx, w, sw, bias)]
+    ops.hip.call("h3v_gemm_i8_dequant", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(out), m, n, k, ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    want = oracle.gemm_dequant(oracle.gemm_acc(a.numpy(), w.numpy()), sx.numpy(), sw.numpy(),
+                               None if bias is None else bias.numpy())
+    assert_bitwise(np_(out), want, "out")
+
+
+@pytest.mark.parametrize("rows,bias", [(1, None), (17, True), (129, True)])
+def test_swiglu_gemm_matches_oracle(ops, oracle, rows, bias):
+    """Reference fixture tests/test_int8_ffn_up_fused_gpu.py:21-33 (K2048, 16384 weight rows)."""
+    gen = _gen(rows)
+    w = torch.randint(-31, 32, (16384, 2048), generator=gen, dtype=torch.int8)
+    ws = (torch.rand(16384, generator=gen) * 0.02 + 0.001).float()
+    q = torch.randint(-31, 32, (rows, 2048), generator=gen, dtype=torch.int8)
+    scale = (torch.rand(rows, 1, generator=gen) * 0.02 + 0.001).float()
+    b = torch.randn(16384, generator=gen).half() if bias else None
+    act = torch.empty((rows, 8192), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) if t is not None else None for t in (q, scale, w, ws, b)]
+    ops.hip.call("h3v_gemm_i8_swiglu", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(act), rows, 8192, 2048,
+                 ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    want = oracle.gemm_swiglu(oracle.gemm_acc(q.numpy(), w.numpy()), scale.numpy(), ws.numpy(),
+                              None if b is None else b.numpy())
+    assert_bitwise(np_(act), want, "act")
+    # fused (GEMM+SwiGLU then row quant) == unfused (dequant GEMM then SwiGLU+quant)
+    hidden = oracle.gemm_dequant(oracle.gemm_acc(q.numpy(), w.numpy()), scale.numpy(), ws.numpy(),
+                                 None if b is None else b.numpy())
+    rq, rs = oracle.swiglu_row_quant(hidden)
+    gq, gs = _row_quant_gpu(ops, act.cpu())
+    assert_bitwise(gq, rq, "requant q")
+    assert_bitwise(gs.view(np.uint32), rs.view(np.uint32), "requant scale")
+
+
+@pytest.mark.parametrize("magnitude", [0.0, 2.0 ** -14, 1.0])
+def test_swiglu_gemm_zero_input_bias_contract(ops, oracle, magnitude):
+    """Reference fixture tests/test_int8_ffn_up_fused_gpu.py:35-46."""
+    q = torch.zeros((3, 2048), dtype=torch.int8)
+    s = torch.ones((3, 1), dtype=torch.float32)
+    w = torch.zeros((16384, 2048), dtype=torch.int8)
+    ws = torch.ones(16384, dtype=torch.float32)
+    b = torch.full((16384,), magnitude, dtype=torch.float16)
+    act = torch.empty((3, 8192), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) for t in (q, s, w, ws, b)]
+    ops.hip.call("h3v_gemm_i8_swiglu", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(act), 3, 8192, 2048,
+                 ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    gq, gs = _row_quant_gpu(ops, act.cpu())
+    rq, rs = oracle.swiglu_row_quant(np.full((3, 16384), magnitude, np.float16))
+    assert_bitwise(gq, rq, "q")
+    assert_bitwise(gs.view(np.uint32), rs.view(np.uint32), "s")
+    if magnitude == 0.0:
+        assert (gq == -128).all() and (gs == np.float32(1e-30)).all()
+
+
+def _tensor_quant_gpu(ops, x):
+    xd = x.to(DEV).contiguous()
+    q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
+    s = torch.empty((), dtype=torch.float32, device=DEV)
+    scratch = torch.empty(1, dtype=torch.int32, device=DEV)
+    ops.hip.call("h3v_tensor_quant_i8", ops.hip.ptr(xd), x.numel(), ops.hip.ptr(q), ops.hip.ptr(s),
+                 ops.hip.ptr(scratch), ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    return np_(q), np.float32(s.item())
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 5, 7, 11), (1, 128, 11, 66, 66), (1, 256, 19, 130, 130), (7,)])
+def test_tensor_quant_matches_oracle(ops, oracle, shape):
+    gen = _gen(sum(shape))
+    x = torch.randn(*shape, generator=gen).half()
+    q, s = _tensor_quant_gpu(ops, x)
+    rs = oracle.tensor_scale(x.numpy())
+    assert np.float32(s).view(np.uint32) == rs.view(np.uint32)
+    assert_bitwise(q, oracle.tensor_quant(x.numpy(), rs), "q")
+
+
+def test_tensor_quant_reference_kats(ops):
+    """Reference tests/test_encoder_int8_gpu.py:57-72: extremes and half-away rounding."""
+    for maximum in [0.0, 2 ** -24, 2 ** -14, 0.5, 127.0, 65504.0]:
+        x = torch.full((9,), maximum, dtype=torch.float16)
+        x[0] = -maximum
+        q, s = _tensor_quant_gpu(ops, x)
+        expect_s = np.float32(maximum) * np.float32(1.0 / 127.0) if maximum else np.float32(1.0)
+        assert s == expect_s
+        if maximum:
+            assert q[0] == -127 and (q[1:] == 127).all()
+        else:
+            assert (q == 0).all()
+    x = torch.tensor([-127.0, -0.5, -1.5, 0.0, 0.5, 1.5, 127.0], dtype=torch.float16)
+    q, s = _tensor_quant_gpu(ops, x)
+    assert s == 1.0
+    assert q.tolist() == [-127, -1, -2, 0, 1, 2, 127]
