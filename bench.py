@@ -1,0 +1,387 @@
+"""Benchmark: the H3 VAE INT8 hot path of one full-clip encode + decode on one MI355X.
+
+One step = the INT8 hot path of encoding and decoding a synthetic
+1x3x124x768x1344 clip at tile 256 (tile batch 4), with random-init H3-shaped
+weights resident in HBM:
+
+* encode: 28 spatial tiles x 8 clips of 17 frames = 224 prefix calls, each
+  running the 8 INT8 residual convolutions of encoder stages 0-1 as fused
+  GroupNorm/SiLU/pad/quant producer + causal-skipping INT8 conv
+  (stage 0: 4 x C128 @ 17x256x256; stage 1: 128->256 and 3 x 256->256 @ 17x128x128);
+* decode: 49 decoder calls of 4 tiles (M = 4 x 1797 = 7188 tokens, width
+  2048), 36 blocks each: norm1 producer + QKV GEMM (block 0: RMSNorm + row
+  quant + GEMM), QK-RMSNorm-RoPE, attention-out row quant + GEMM, norm2
+  producer, FFN-up SwiGLU GEMM, requant, FFN-down GEMM; final residual LayerNorm.
+
+The FP16 layers outside the INT8 path (conv_in, downsample and suffix convs,
+scaled-dot-product attention, output projection, blending) are not part of
+the step.  Kernels are called through the C ABI on preallocated buffers.
+
+Prints one JSON line (rank 0, N=1).  `--gpus N` with N > 1 exits: this build
+measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+INT8_PEAK_TOPS = 5033.2  # 256 CU x 8192 int8 ops/clk x 2.4 GHz (dense)
+HBM_PEAK_GBS = 8000.0
+
+# H3 shapes
+ENC_CALLS = 224            # 28 tiles x 8 clips
+DEC_CALLS = 49             # 7 temporal chunks x 28 tiles / batch 4
+DEC_BLOCKS = 36
+DEC_M = 4 * 1797
+DEC_D = 2048
+DEC_HEADS = 32
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--enc-calls", type=int, default=ENC_CALLS, help=argparse.SUPPRESS)
+    p.add_argument("--dec-calls", type=int, default=DEC_CALLS, help=argparse.SUPPRESS)
+    return p.parse_args()
+
+
+class Workload:
+    """Preallocated synthetic inputs, weights and scratch for the hot path."""
+
+    def __init__(self, torch, hip, seed=20261002):
+        self.torch, self.hip = torch, hip
+        dev = self.dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev).manual_seed(seed)
+        f16, i8, f32 = torch.float16, torch.int8, torch.float32
+
+        def randn(*shape, scale=1.0):
+            return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * scale).to(f16)
+
+        def randi8(*shape, lo=-127, hi=128):
+            return torch.randint(lo, hi, shape, generator=g, device=dev, dtype=i8)
+
+        # ---------------- encoder (stage 0 @256^2 C128, stage 1 @128^2) ----------------
+        t = 17
+        self.enc_layers = []   # (cin, cout, h, w)
+        self.enc_layers += [(128, 128, 256, 256)] * 4
+        self.enc_layers += [(128, 256, 128, 128)] + [(256, 256, 128, 128)] * 3
+        self.enc_w = []
+        for cin, cout, h, w in self.enc_layers:
+            qw = randi8(cout, 27 * cin)
+            ws = (torch.rand(cout, generator=g, device=dev) * 2e-4 + 1e-5).to(f32)
+            bias = randn(cout, scale=0.1)
+            gamma = (1 + 0.1 * torch.randn(cin, generator=g, device=dev)).to(f16)
+            beta = randn(cin, scale=0.1)
+            self.enc_w.append((qw, ws, bias, gamma, beta))
+        self.x0 = randn(t, 256, 256, 128)                         # NDHWC stage-0 input
+        self.x1 = randn(t, 128, 128, 128)                         # stage-1 input (after the FP16 downsample)
+        self.a0 = torch.empty((t, 256, 256, 128), device=dev, dtype=f16)
+        self.a1 = torch.empty((t, 256, 256, 128), device=dev, dtype=f16)
+        self.b0 = torch.empty((t, 128, 128, 256), device=dev, dtype=f16)
+        self.b1 = torch.empty((t, 128, 128, 256), device=dev, dtype=f16)
+        self.q = torch.empty((t + 2) * 258 * 258 * 128, device=dev, dtype=i8)
+        self.qscale = torch.empty(1, device=dev, dtype=f32)
+        self.stats = torch.empty((t, 32, 2), device=dev, dtype=f32)
+        nws = int(hip.lib().h3v_gn_norm_pack_workspace_floats(t, 256, 256))
+        self.gn_ws = torch.empty(nws, device=dev, dtype=f32)
+        self.amax = torch.empty(1, device=dev, dtype=torch.int32)
+        self.t = t
+
+        # ---------------- decoder (36 blocks, width 2048) ----------------
+        m, d = DEC_M, DEC_D
+        self.blocks = []
+        for _ in range(DEC_BLOCKS):
+            blk = {
+                "g1": (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16),
+                "g2": (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16),
+                "scale1": randn(d, scale=0.1), "scale2": randn(d, scale=0.1),
+                "qkv": randi8(6144, d), "qkv_s": (torch.rand(6144, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
+                "qkv_b": randn(6144, scale=0.02),
+                "out": randi8(d, d), "out_s": (torch.rand(d, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
+                "out_b": randn(d, scale=0.02),
+                "up": randi8(16384, d), "up_s": (torch.rand(16384, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
+                "up_b": randn(16384, scale=0.02),
+                "down": randi8(d, 8192), "down_s": (torch.rand(d, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
+                "down_b": randn(d, scale=0.02),
+            }
+            self.blocks.append(blk)
+        self.ln_g = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16)
+        self.ln_b = randn(d, scale=0.02)
+        self.tokens0 = randn(m, d)
+        self.attn_y = randn(m, d)                     # stand-in for the SDPA output
+        cos_sin = torch.rand(m, 48, generator=g, device=dev) * 6.283
+        self.cos, self.sin = cos_sin.cos().to(f16), cos_sin.sin().to(f16)
+        self.h = torch.empty((m, d), device=dev, dtype=f16)
+        self.h2 = torch.empty((m, d), device=dev, dtype=f16)
+        self.normed = torch.empty((m, d), device=dev, dtype=f16)
+        self.o = torch.empty((m, d), device=dev, dtype=f16)
+        self.attn = torch.empty((m, d), device=dev, dtype=f16)
+        self.qx = torch.empty((m, 8192), device=dev, dtype=i8)
+        self.sx = torch.empty(m, device=dev, dtype=f32)
+        self.qkv = torch.empty((m, 6144), device=dev, dtype=f16)
+        self.rq = torch.empty((m, DEC_HEADS, 64), device=dev, dtype=f16)
+        self.rk = torch.empty((m, DEC_HEADS, 64), device=dev, dtype=f16)
+        self.act = torch.empty((m, 8192), device=dev, dtype=f16)
+        self.final = torch.empty((m, d), device=dev, dtype=f16)
+        self.conv_events = None
+
+    # -- raw C-ABI helpers ---------------------------------------------------------------
+    def _p(self, t):
+        return self.hip.ptr(t)
+
+    def norm_conv(self, x, layer, out, h, w, stream, pre_bias=None):
+        cin, cout, _, _ = self.enc_layers[layer]
+        qw, ws, bias, gamma, beta = self.enc_w[layer]
+        call, p = self.hip.call, self._p
+        t = self.t
+        call("h3v_gn_norm_pack_i8", p(x), p(pre_bias), p(gamma), p(beta), 1e-6, cin, t, h, w, p(self.q),
+             p(self.qscale), p(self.stats), p(self.gn_ws), p(self.amax), stream)
+        ev = self.conv_events is not None and cin == 128 and cout == 128
+        if ev:
+            e0, e1 = self.torch.cuda.Event(enable_timing=True), self.torch.cuda.Event(enable_timing=True)
+            e0.record()
+        call("h3v_conv3d_i8", p(self.q), p(self.qscale), p(qw), p(ws), p(bias), p(out), 1, cin, t + 2, h + 2, w + 2,
+             cout, 3, 3, 3, 1, 1, 1, 1, stream)
+        if ev:
+            e1.record()
+            self.conv_events.append((e0, e1))
+
+    def encode_call(self, stream):
+        """One prefix call: 8 fused norm + INT8 conv layers (stage 0 then stage 1)."""
+        b = [w[2] for w in self.enc_w]
+        self.norm_conv(self.x0, 0, self.a0, 256, 256, stream)
+        self.norm_conv(self.a0, 1, self.a1, 256, 256, stream, pre_bias=b[0])
+        self.norm_conv(self.a1, 2, self.a0, 256, 256, stream)
+        self.norm_conv(self.a0, 3, self.a1, 256, 256, stream, pre_bias=b[2])
+        self.norm_conv(self.x1, 4, self.b0, 128, 128, stream)
+        self.norm_conv(self.b0, 5, self.b1, 128, 128, stream, pre_bias=b[4])
+        self.norm_conv(self.b1, 6, self.b0, 128, 128, stream)
+        self.norm_conv(self.b0, 7, self.b1, 128, 128, stream, pre_bias=b[6])
+
+    def decode_call(self, stream):
+        """One B4 decoder call: 36 blocks of the INT8 path + the final LayerNorm."""
+        call, p = self.hip.call, self._p
+        m, d = DEC_M, DEC_D
+        h, h2 = self.h, self.h2
+        self.h.copy_(self.tokens0)
+        for i, blk in enumerate(self.blocks):
+            if i == 0:
+                call("h3v_rms_fp16", p(h), p(blk["g1"]), 9.999999747378752e-06, m, d, p(self.normed), stream)
+                call("h3v_row_quant", p(self.normed), m, d, p(self.qx), p(self.sx), stream)
+            else:
+                # h <- fp16(h + o * scale2_prev), norm1, row quant (in place on h)
+                call("h3v_residual_norm1_quant", p(h), p(self.o), p(self.blocks[i - 1]["scale2"]), p(blk["g1"]),
+                     1e-5, m, d, p(h), p(self.qx), p(self.sx), stream)
+            call("h3v_gemm_i8_dequant", p(self.qx), p(self.sx), p(blk["qkv"]), p(blk["qkv_s"]), p(blk["qkv_b"]),
+                 p(self.qkv), m, 6144, d, stream)
+            call("h3v_qk_rope", p(self.qkv), p(self.cos), p(self.sin), m, DEC_HEADS, 64, 48, 1e-6, p(self.rq),
+                 p(self.rk), stream)
+            # attention itself (SDPA) is outside the INT8 path; its output is a resident stand-in
+            call("h3v_row_quant", p(self.attn_y), m, d, p(self.qx), p(self.sx), stream)
+            call("h3v_gemm_i8_dequant", p(self.qx), p(self.sx), p(blk["out"]), p(blk["out_s"]), p(blk["out_b"]),
+                 p(self.attn), m, d, d, stream)
+            call("h3v_residual_rms_quant", p(h), p(self.attn), p(blk["scale1"]), p(blk["g2"]), 1e-5, m, d, p(h2),
+                 p(self.qx), p(self.sx), stream)
+            call("h3v_gemm_i8_swiglu", p(self.qx), p(self.sx), p(blk["up"]), p(blk["up_s"]), p(blk["up_b"]),
+                 p(self.act), m, 8192, d, stream)
+            call("h3v_row_quant", p(self.act), m, 8192, p(self.qx), p(self.sx), stream)
+            call("h3v_gemm_i8_dequant", p(self.qx), p(self.sx), p(blk["down"]), p(blk["down_s"]), p(blk["down_b"]),
+                 p(self.o), m, d, 8192, stream)
+            h, h2 = h2, h
+        call("h3v_residual_layernorm", p(h), p(self.o), p(self.blocks[-1]["scale2"]), p(self.ln_g), p(self.ln_b),
+             9.999999747378752e-06, m, d, p(self.final), stream)
+
+
+def enc_ops_per_call():
+    """Useful (non-causal-zero) and dense INT8 ops of the 8 convs of one prefix call."""
+    useful = dense = 0
+    t = 17
+    for cin, cout, h, w in [(128, 128, 256, 256)] * 4 + [(128, 256, 128, 128)] + [(256, 256, 128, 128)] * 3:
+        per_frame = 2 * h * w * cout * 27 * cin
+        dense += t * per_frame
+        useful += t * per_frame - per_frame * (2 + 1) // 3     # frame 0 skips 2 of 3 taps, frame 1 skips 1
+    return useful, dense
+
+
+def dec_ops_per_call():
+    m, d = DEC_M, DEC_D
+    return 2 * m * DEC_BLOCKS * (6144 * d + d * d + 16384 * d + d * 8192)
+
+
+def cpu_baseline(budget_s: float):
+    """The CPU oracle on a bounded sample of the same work, extrapolated by op count."""
+    import numpy as np
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(20261002)
+    # sample 1: a stage-0 fused layer (norm producer + conv) on 3 frames of 64x256 pixels
+    x = rng.standard_normal((3, 64, 256, 128)).astype(np.float16)
+    gamma = np.ones(128, np.float16)
+    beta = np.zeros(128, np.float16)
+    qw = rng.integers(-127, 128, (128, 3456)).astype(np.int8)
+    ws = np.full(128, 1e-4, np.float32)
+    bias = np.zeros(128, np.float16)
+    # sample 2: one decoder block's GEMM work on 64 of 7188 rows
+    mrow = 64
+    a = rng.integers(-127, 128, (mrow, DEC_D)).astype(np.int8)
+    wq = rng.integers(-127, 128, (6144, DEC_D)).astype(np.int8)
+    wu = rng.integers(-127, 128, (16384, DEC_D)).astype(np.int8)
+    wd = rng.integers(-127, 128, (DEC_D, 8192)).astype(np.int8)
+    wo = rng.integers(-127, 128, (DEC_D, DEC_D)).astype(np.int8)
+    sx = np.full(mrow, 1e-2, np.float32)
+    t_enc = t_dec = 0.0
+    n_enc = n_dec = 0
+    start = time.perf_counter()
+    while time.perf_counter() - start < budget_s or n_enc == 0 or n_dec == 0:
+        t0 = time.perf_counter()
+        oracle.norm_conv3d(x, gamma, beta, 1e-6, qw, ws, bias)      # out: [3, 64, 256, 128]
+        t_enc += time.perf_counter() - t0
+        n_enc += 1
+        t0 = time.perf_counter()
+        qkv = oracle.gemm_dequant(oracle.gemm_acc(a, wq), sx, np.full(6144, 1e-3, np.float32))
+        oracle.gemm_dequant(oracle.gemm_acc(a, wo), sx, np.full(DEC_D, 1e-3, np.float32))
+        act = oracle.gemm_swiglu(oracle.gemm_acc(a, wu), sx, np.full(16384, 1e-3, np.float32))
+        q2, s2 = oracle.row_quant(act)
+        oracle.gemm_dequant(oracle.gemm_acc(q2, wd), s2, np.full(DEC_D, 1e-3, np.float32))
+        del qkv
+        t_dec += time.perf_counter() - t0
+        n_dec += 1
+    enc_sample_ops = 3 * 64 * 256 * 2 * 128 * 3456          # dense conv ops of the sample (3 frames)
+    dec_sample_ops = 2 * mrow * (6144 * DEC_D + DEC_D * DEC_D + 16384 * DEC_D + DEC_D * 8192)
+    useful, dense = enc_ops_per_call()
+    enc_total = ENC_CALLS * dense
+    dec_total = DEC_CALLS * dec_ops_per_call()
+    enc_s = (t_enc / n_enc) * enc_total / enc_sample_ops
+    dec_s = (t_dec / n_dec) * dec_total / dec_sample_ops
+    return {
+        "value": round(enc_s + dec_s, 1),
+        "unit": "s (extrapolated)",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"CPU oracle (C, OpenMP {threads} threads): {n_enc}x one fused stage-0 norm+conv on a "
+                   f"3x64x256x128 input ({enc_sample_ops / 1e9:.1f} GOP) and {n_dec}x one decoder block's four "
+                   f"INT8 GEMMs + SwiGLU + requant on {mrow} of 7188 rows ({dec_sample_ops / 1e9:.1f} GOP); "
+                   f"extrapolated by op count to the full step (encode {enc_s:.0f} s + decode {dec_s:.0f} s)"),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the H3 hot path runs per GPU and multi-GPU sharding is not "
+              "part of this build (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    import importlib
+    hip = importlib.import_module(f"{pkg.__name__}._hip")
+    hip.require_gfx950("cuda:0", "bench")
+    wl = Workload(torch, hip)
+    stream = hip.stream(wl.dev)
+    enc_calls, dec_calls = args.enc_calls, args.dec_calls
+
+    def step(timings=None):
+        t0 = time.perf_counter()
+        for _ in range(enc_calls):
+            wl.encode_call(stream)
+        if timings is not None:
+            torch.cuda.synchronize()
+            timings["enc"] += time.perf_counter() - t0
+            t0 = time.perf_counter()
+        for _ in range(dec_calls):
+            wl.decode_call(stream)
+        if timings is not None:
+            torch.cuda.synchronize()
+            timings["dec"] += time.perf_counter() - t0
+
+    def log(msg):
+        print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+    with torch.inference_mode():
+        for i in range(args.warmup):
+            step()
+            torch.cuda.synchronize()
+            log(f"warmup step {i + 1}/{args.warmup} done")
+        split = {"enc": 0.0, "dec": 0.0}
+        step(split)                      # one extra untimed step for the encode/decode split
+        log(f"split step: encode {split['enc']:.3f} s, decode {split['dec']:.3f} s")
+        wl.conv_events = []
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        log(f"timed {args.steps} steps: {elapsed / args.steps:.3f} s/step")
+        conv_ms = [e0.elapsed_time(e1) for e0, e1 in wl.conv_events]
+        wl.conv_events = None
+
+    sec_per_step = elapsed / args.steps
+    useful, dense = enc_ops_per_call()
+    enc_ops = enc_calls * useful
+    dec_ops = dec_calls * dec_ops_per_call()
+    conv_avg_s = sum(conv_ms) / len(conv_ms) / 1e3
+    conv_useful = 17 * 2 * 256 * 256 * 128 * 27 * 128 - 3 * 2 * 256 * 256 * 128 * 9 * 128
+    achieved = conv_useful / conv_avg_s / 1e12
+    result = {
+        "metric": "H3 VAE encode/decode s @768x1344x124 tile256; INT8 MFMA % of peak",
+        "value": round(sec_per_step, 4),
+        "unit": "s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec_per_step * 1e3, 2),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded random int8 weights of H3 shape, random fp16 activations, resident in HBM)",
+        "config": {
+            "workload": "h3vae_int8_hot_path_encode_decode_1x3x124x768x1344_tile256",
+            "encode_prefix_calls": enc_calls,
+            "encode_int8_convs": 8 * enc_calls,
+            "decode_calls": dec_calls,
+            "decode_blocks": DEC_BLOCKS,
+            "decode_tokens_per_call": DEC_M,
+            "excluded": "FP16 layers outside the INT8 path: conv_in, downsample/suffix convs, SDPA, output head",
+        },
+        "encode_s": round(split["enc"], 4),
+        "decode_s": round(split["dec"], 4),
+        "int8_tops_step": round((enc_ops + dec_ops) / sec_per_step / 1e12, 1),
+        "int8_mfma_frac_step": round((enc_ops + dec_ops) / sec_per_step / 1e12 / INT8_PEAK_TOPS, 4),
+        "roofline": {
+            "kernel": "gemm_i8_mfma<256,128,64,Conv,Dequant> (stage-0 conv C128->128, [1,128,19,258,258] int8)",
+            "bound": "mfma",
+            "achieved": round(achieved, 1),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / INT8_PEAK_TOPS, 4),
+            "traffic": None,
+            "launches_timed": len(conv_ms),
+            "avg_us": round(conv_avg_s * 1e6, 1),
+            "algorithmic_ops_per_launch": conv_useful,
+        },
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU oracle baseline sample")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -12,12 +12,13 @@
 // per-row and a per-k term.  With C a multiple of the K tile every K tile is one
 // tap and a contiguous channel slice.
 //
-// Tiling: BM x BN x 64 workgroup tile, 2 x 2 waves, each wave owning a
-// (BM/2) x (BN/2) block built from v_mfma_i32_32x32x32_i8.  Global -> register ->
-// LDS double buffering with one barrier per K step; LDS rows are padded to
-// 80 bytes so the 16-byte fragment reads of 8 consecutive lanes hit distinct
-// banks.  Workgroup ids are remapped so that each XCD (own L2) walks a
-// contiguous, M-grouped range of tiles.
+// Tiling: BM x BN x 64 workgroup tile of 8 waves (2 per SIMD), each owning a
+// 128 x 64 block built from v_mfma_i32_32x32x32_i8.  Operands stream
+// global -> LDS with LDS-DMA (global_load_lds_dwordx4) into a 4-stage ring,
+// three K steps ahead of the MFMAs; one barrier per K step.  LDS rows are
+// XOR-swizzled in 16-byte chunks so fragment reads are bank-conflict free.
+// Workgroup ids are remapped so that each XCD (own L2) walks a contiguous,
+// M-grouped range of tiles.
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
@@ -111,22 +112,62 @@ __device__ __forceinline__ float g1_value(int32_t acc, float sx, float sw, const
     return bias ? __builtin_fmaf(v, sw, h2f(bias[col])) : v * sw;
 }
 
-template <int BM, int BN, int BK, AMode AM, Epi EP>
-__global__ __launch_bounds__(256, 1) void gemm_i8_mfma(GemmParams p) {
-    constexpr int NT = 256;
-    constexpr int WGN = 2;
-    constexpr int WM = BM / 2, WN = BN / 2;
-    constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int LDS = BK + 16;        // padded row stride (bytes)
-    constexpr int CPR = BK / 16;        // 16-byte chunks per row
-    constexpr int RPP = NT / CPR;       // rows covered per pass of the block
-    constexpr int A_CH = BM / RPP, B_CH = BN / RPP;
-    static_assert(BM % RPP == 0 && BN % RPP == 0, "tile rows must be a multiple of rows per pass");
-    static_assert(EP != Epi::SwiGLU || (WN % 64) == 0, "SwiGLU pairs need 64-column wave tiles");
+// LDS-DMA helpers.  global_load_lds_dwordx4 writes lane i's 16 bytes to
+// M0 + 16*i, so one wave instruction fills 1 KB of LDS contiguously: 16 tile
+// rows of 64 bytes.  Lane i loads row i/4 and puts its 16-byte chunk in slot
+// i%4; the chunk it fetches is slot ^ swz(row) so that slot s of row r holds
+// k-chunk s ^ swz(r).  swz(r) = (r >> 1) & 3 makes the 16-byte fragment reads
+// of 8 consecutive rows hit distinct LDS banks (32 or 64 banks).
+typedef __attribute__((address_space(3))) void* lds_void_t;
+typedef const __attribute__((address_space(1))) void* gbl_void_t;
 
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    int8_t* sA = smem;
-    int8_t* sB = smem + 2 * BM * LDS;
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
+
+__device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
+    __builtin_amdgcn_global_load_lds((gbl_void_t)g, (lds_void_t)lds, 16, 0, 0);
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the release/acquire fences of __syncthreads(): those
+// would wait for every outstanding LDS-DMA load (vmcnt(0)) and drain the ring.
+// LDS reads issued before the barrier are completed explicitly (lgkmcnt(0)).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt((15 << 4) | (0 << 8) | 0xC00F);  // lgkmcnt(0) only
+    __builtin_amdgcn_s_barrier();
+}
+
+template <int LPS>
+__device__ __forceinline__ void wait_stage(int ahead) {
+    // wait until at most `ahead` later stages (LPS loads each) are still in flight
+    if (ahead >= 3) wait_vmcnt<3 * LPS>();
+    else if (ahead == 2) wait_vmcnt<2 * LPS>();
+    else if (ahead == 1) wait_vmcnt<LPS>();
+    else wait_vmcnt<0>();
+}
+
+// BM x BN x 64 workgroup tile, WGM x WGN waves of (BM/WGM) x (BN/WGN), NS-stage
+// LDS ring filled by LDS-DMA loads issued up to NS K steps ahead of the MFMAs.
+template <int BM, int BN, int WGM, int WGN, int NS, AMode AM, Epi EP>
+__global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
+    constexpr int BK = 64;
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int A_BYTES = BM * BK, STAGE = (BM + BN) * BK;
+    constexpr int A_PW = BM / 16 / NW, B_PW = BN / 16 / NW;   // 16-row groups per wave
+    constexpr int LPS = A_PW + B_PW;                          // DMA instructions per stage per wave
+    static_assert(A_PW * 16 * NW == BM && B_PW * 16 * NW == BN, "tile rows must split into 16-row groups per wave");
+    static_assert(EP != Epi::SwiGLU || (WN % 64) == 0, "SwiGLU pairs need 64-column wave tiles");
+    static_assert(NS >= 2 && NS <= 4, "LDS ring depth");
+
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -137,23 +178,23 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_mfma(GemmParams p) {
     grouped_tile(xcd_remap(blockIdx.x, gridDim.x), p.tiles_m, p.tiles_n, 8, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const int crow = tid / CPR;
-    const int ccol = (tid % CPR) * 16;
+    const int lrow = lane >> 2;
+    const int gchunk = ((lane & 3) ^ swz(lrow)) * 16;
 
-    int64_t abase[A_CH];
+    int64_t aoff[A_PW];
 #pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-        int m = m0 + crow + i * RPP;
+    for (int j = 0; j < A_PW; ++j) {
+        int m = m0 + (wave * A_PW + j) * 16 + lrow;
         m = m < p.M ? m : p.M - 1;
-        abase[i] = (AM == AMode::Gemm ? (int64_t)m * p.lda : conv_row_offset(p, m)) + ccol;
+        aoff[j] = (AM == AMode::Gemm ? (int64_t)m * p.lda : conv_row_offset(p, m)) + gchunk;
     }
-    const int8_t* bptr[B_CH];
+    const int8_t* bptr[B_PW];
 #pragma unroll
-    for (int i = 0; i < B_CH; ++i) {
-        int r = crow + i * RPP;
+    for (int j = 0; j < B_PW; ++j) {
+        int r = (wave * B_PW + j) * 16 + lrow;
         int wrow;
         if constexpr (EP == Epi::SwiGLU) {
-            // tile row r -> pair r/64, half (r/32)&1 (0 gate, 1 up), lane r&31
+            // tile row r -> pair r/64, half (r/32)&1 (0 gate, 1 up), column r&31
             int c = tn * (BN / 2) + (r >> 6) * 32 + (r & 31);
             c = c < p.N ? c : p.N - 1;
             wrow = ((r >> 5) & 1) ? p.N + c : c;
@@ -161,11 +202,22 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_mfma(GemmParams p) {
             int n = n0 + r;
             wrow = n < p.N ? n : p.N - 1;
         }
-        bptr[i] = p.b + (int64_t)wrow * p.K + ccol;
+        bptr[j] = p.b + (int64_t)wrow * p.K + gchunk;
     }
 
-    const int nkb = p.K / BK;
     const int kb0 = (AM == AMode::Conv) ? conv_first_kblock(p, m0, BM, BK) : 0;
+    const int nk = p.K / BK - kb0;
+
+    auto issue = [&](int it) {
+        const int kb = kb0 + it;
+        int8_t* sa = smem + (it % NS) * STAGE;
+        int8_t* sb = sa + A_BYTES;
+        const int64_t koff = (AM == AMode::Gemm) ? (int64_t)kb * BK : conv_k_offset(p, kb * BK);
+#pragma unroll
+        for (int j = 0; j < A_PW; ++j) lds_dma16(p.a + aoff[j] + koff, sa + (wave * A_PW + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < B_PW; ++j) lds_dma16(bptr[j] + (int64_t)kb * BK, sb + (wave * B_PW + j) * 1024);
+    };
 
     v16i acc[FM][FN];
 #pragma unroll
@@ -173,51 +225,75 @@ __global__ __launch_bounds__(256, 1) void gemm_i8_mfma(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
-    v4i ra[A_CH], rb[B_CH];
-    auto gload = [&](int kb) {
-        int64_t koff = (AM == AMode::Gemm) ? (int64_t)kb * BK : conv_k_offset(p, kb * BK);
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const v4i*>(p.a + abase[i] + koff);
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const v4i*>(bptr[i] + (int64_t)kb * BK);
-    };
-    auto sstore = [&](int buf) {
-        int8_t* a = sA + buf * BM * LDS + crow * LDS + ccol;
-        int8_t* b = sB + buf * BN * LDS + crow * LDS + ccol;
-#pragma unroll
-        for (int i = 0; i < A_CH; ++i) *reinterpret_cast<v4i*>(a + i * RPP * LDS) = ra[i];
-#pragma unroll
-        for (int i = 0; i < B_CH; ++i) *reinterpret_cast<v4i*>(b + i * RPP * LDS) = rb[i];
-    };
-
-    if (kb0 < nkb) {
-        gload(kb0);
-        sstore(0);
-    }
-    __syncthreads();
-
+    // fragment addressing: lane reads row (lane & 31) of a 32-row block, 16-byte
+    // k-chunk (lane >> 5) + 2*ks of the 64-byte K step
     const int frow = lane & 31;
-    const int fk = (lane >> 5) * 16;
-    for (int kb = kb0; kb < nkb; ++kb) {
-        const int buf = (kb - kb0) & 1;
-        if (kb + 1 < nkb) gload(kb + 1);
-        const int8_t* a_base = sA + buf * BM * LDS + (wm * WM + frow) * LDS + fk;
-        const int8_t* b_base = sB + buf * BN * LDS + (wn * WN + frow) * LDS + fk;
+    const int fhi = lane >> 5;
+    auto load_frags = [&](int it, int ks, v4i (&af)[FM], v4i (&bf)[FN]) {
+        const int8_t* sa = smem + (it % NS) * STAGE;
+        const int8_t* sb = sa + A_BYTES;
+        const int kc = fhi + 2 * ks;
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ++ks) {
-            v4i af[FM], bf[FN];
-#pragma unroll
-            for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const v4i*>(a_base + i * 32 * LDS + ks * 32);
-#pragma unroll
-            for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const v4i*>(b_base + j * 32 * LDS + ks * 32);
-#pragma unroll
-            for (int i = 0; i < FM; ++i)
-#pragma unroll
-                for (int j = 0; j < FN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < FM; ++i) {
+            const int r = wm * WM + i * 32 + frow;
+            af[i] = *reinterpret_cast<const v4i*>(sa + r * BK + ((kc ^ swz(r)) << 4));
         }
-        if (kb + 1 < nkb) sstore(buf ^ 1);
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+            const int r = wn * WN + j * 32 + frow;
+            bf[j] = *reinterpret_cast<const v4i*>(sb + r * BK + ((kc ^ swz(r)) << 4));
+        }
+    };
+    auto mfma_all = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
+    // Prologue: fill the whole ring, then wait for stage 0.
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+        if (s < nk) issue(s);
+    v4i a0[FM], b0[FN], a1[FM], b1[FN];
+    if (nk > 0) {
+        wait_stage<LPS>(nk - 1 < NS - 1 ? nk - 1 : NS - 1);
+        lds_barrier();
+        load_frags(0, 0, a0, b0);
+    }
+    // Per K step: MFMA the first half while reading the second half's fragments,
+    // then (behind the barrier that publishes the next stage) refill the freed
+    // ring slot and MFMA the second half while reading the next step's first
+    // half.  sched_group_barrier interleaves 2 MFMAs with 1 LDS read so the
+    // reads hide under the matrix pipeline.
+    constexpr int NFRAG = FM + FN;
+    constexpr int NMFMA = FM * FN;
+    for (int it = 0; it < nk; ++it) {
+        mfma_all(a0, b0);
+        load_frags(it, 1, a1, b1);
+#pragma unroll
+        for (int g = 0; g < NFRAG; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NFRAG, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const bool more = it + 1 < nk;
+        if (more) {
+            wait_stage<LPS>(nk - 2 - it < NS - 2 ? nk - 2 - it : NS - 2);
+            lds_barrier();
+            if (it + NS < nk) issue(it + NS);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_all(a1, b1);
+        // on the last step this re-reads a stale slot; the values are never used
+        load_frags(more ? it + 1 : it, 0, a0, b0);
+#pragma unroll
+        for (int g = 0; g < NFRAG; ++g) {
+            __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NFRAG, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Epilogue.  v_mfma 32x32 result layout: lane holds column lane&31 and rows
@@ -309,15 +385,21 @@ __global__ __launch_bounds__(256) void gemm_i8_generic(GemmParams p) {
 
 constexpr int kBK = 64;
 
-template <int BM, int BN, AMode AM, Epi EP>
+template <int BM, int BN, int WGM, int WGN, int NS, AMode AM, Epi EP>
 int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     int ncols = (EP == Epi::SwiGLU) ? 2 * p.N : p.N;
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (ncols + BN - 1) / BN;
     int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
     if (grid > 0x7fffffff) return fail(H3V_EINVAL, "%s: too many tiles", what);
-    size_t lds = (size_t)2 * (BM + BN) * (kBK + 16);
-    hipLaunchKernelGGL((gemm_i8_mfma<BM, BN, kBK, AM, EP>), dim3((unsigned)grid), dim3(256), lds, stream, p);
+    const size_t lds = (size_t)NS * (BM + BN) * kBK;   // LDS ring (at most 160 KB on gfx950)
+    static_assert((size_t)NS * (BM + BN) * kBK <= 163840, "LDS ring exceeds 160 KB");
+    auto kernel = &gemm_i8_mfma<BM, BN, WGM, WGN, NS, AM, EP>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, lds,
+                                        hipGetErrorString(attr));
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(WGM * WGN * 64), lds, stream, p);
     return launch_status(what);
 }
 
@@ -334,7 +416,7 @@ template <Epi EP>
 int run_gemm(GemmParams p, hipStream_t stream, const char* what) {
     bool tiled = p.K % kBK == 0 && p.lda % 16 == 0 && aligned(p.a, 16) && aligned(p.b, 16);
     if (!tiled) return launch_generic<AMode::Gemm, EP>(p, stream, what);
-    return launch_tiled<256, 256, AMode::Gemm, EP>(p, stream, what);
+    return launch_tiled<256, 256, 2, 4, 4, AMode::Gemm, EP>(p, stream, what);
 }
 
 template <Epi EP>
@@ -344,8 +426,8 @@ int run_conv(GemmParams p, hipStream_t stream, const char* what) {
         p.causal_skip = 0;  // the generic path always runs the full reduction
         return launch_generic<AMode::Conv, EP>(p, stream, what);
     }
-    if (p.N <= 128) return launch_tiled<256, 128, AMode::Conv, EP>(p, stream, what);
-    return launch_tiled<256, 256, AMode::Conv, EP>(p, stream, what);
+    if (p.N <= 128) return launch_tiled<512, 128, 4, 2, 4, AMode::Conv, EP>(p, stream, what);
+    return launch_tiled<256, 256, 2, 4, 4, AMode::Conv, EP>(p, stream, what);
 }
 
 int check_gemm_dims(const char* what, int64_t m, int64_t n, int64_t k) {

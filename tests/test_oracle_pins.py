@@ -1,0 +1,358 @@
+"""Pin the CPU oracle before trusting it (CPU only).
+
+Every oracle function is checked against something that does not restate its
+own formula: the reference's known-answer vectors, closed forms derived by
+hand from exact arithmetic, numpy's independent implementations (float16
+conversion, int64 matmul, float64 math) with stated error bounds, and
+structural invariants of the padding/packing.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+
+RNG = np.random.default_rng(20261002)
+
+
+# ---------------------------------------------------------------------------
+# binary16 conversion and exp
+# ---------------------------------------------------------------------------
+
+def test_h2f_exhaustive_against_numpy(oracle):
+    codes = np.arange(65536, dtype=np.uint16)
+    ref = codes.view(np.float16).astype(np.float32)
+    got = np.array([oracle.h2f(int(c)) for c in codes], np.float32)
+    nan = np.isnan(ref)
+    assert np.isnan(got[nan]).all()
+    assert np.array_equal(ref[~nan].view(np.uint32), got[~nan].view(np.uint32))
+
+
+def test_f2h_round_to_nearest_even_against_numpy(oracle):
+    bits = RNG.integers(0, 2 ** 32, size=100000, dtype=np.uint64).astype(np.uint32)
+    f = bits.view(np.float32)
+    f = f[np.isfinite(f)]
+    codes = np.arange(0, 0x7c00, dtype=np.uint16)
+    v = codes.view(np.float16).astype(np.float64)
+    mid = ((v[:-1] + v[1:]) / 2).astype(np.float32)            # exact ties
+    probe = np.concatenate([f, mid, -mid, np.nextafter(mid, np.float32(np.inf)),
+                            np.nextafter(mid, np.float32(0)), np.float32([65504, 65519.99, 65520, 1e9, 2.0 ** -25,
+                                                                          2.0 ** -26, 0.0, -0.0])])
+    with np.errstate(over="ignore"):
+        ref = probe.astype(np.float16).view(np.uint16)
+    got = np.array([oracle.f2h_bits(float(x)) for x in probe], np.uint16)
+    assert np.array_equal(ref, got)
+
+
+def test_exp_error_bound_and_special_values(oracle):
+    xs = np.linspace(-87.0, 88.7, 100001).astype(np.float32)
+    got = np.array([oracle.expf(float(x)) for x in xs], np.float64)
+    ref = np.exp(xs.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - ref) / ulp).max() <= 2.0
+    assert oracle.expf(0.0) == 1.0
+    assert oracle.expf(float("inf")) == float("inf")
+    assert oracle.expf(float("-inf")) == 0.0
+    assert math.isnan(oracle.expf(float("nan")))
+    assert oracle.expf(89.0) == float("inf")
+
+
+# ---------------------------------------------------------------------------
+# Q1 row quantizer (comfy-kitchen contract as restated by the reference)
+# ---------------------------------------------------------------------------
+
+def test_q1_zero_row_quirk(oracle):
+    """opt/kitchen_int8.py:131-133: an all-zero row gives q=-128, s=1e-30."""
+    q, s = oracle.row_quant(np.zeros((2, 64), np.float16))
+    assert (q == -128).all()
+    assert (s == np.float32(1e-30)).all()
+
+
+@pytest.mark.parametrize("e", [-6, 0, 3])
+def test_q1_closed_form_power_of_two_scale(oracle, e):
+    """amax = 127*2^e -> s = 2^e exactly (127 * fp32(1/127) rounds to 1), so q = rint(a * 2^-e), ties to even."""
+    base = np.array([127, 2.5, -2.5, 0.5, 1.5, -0.5, 3.5, 126.5, -127, 0, 64.5, -64.5], np.float64)
+    row = (base * 2.0 ** e).astype(np.float16)[None]
+    q, s = oracle.row_quant(row)
+    assert s[0] == np.float32(2.0 ** e)
+    assert q[0].tolist() == [127, 2, -2, 0, 2, 0, 4, 126, -127, 0, 64, -64]
+
+
+def test_q1_zero_divisor_saturates_and_nan(oracle):
+    """amax = 2^-24: s = 2^-24/127 rounds to fp16 0, so +x/0 -> 127, -x/0 -> -128, 0/0 -> NaN -> -128."""
+    row = np.array([[2.0 ** -24, -(2.0 ** -24), 0.0, 2.0 ** -24]], np.float16)
+    q, s = oracle.row_quant(row)
+    assert q[0].tolist() == [127, -128, -128, 127]
+    assert s[0] == np.float32(2.0 ** -24) * np.float32(1.0 / 127.0)
+    row = np.array([[1.0, np.nan, -1.0]], np.float16)
+    q, _ = oracle.row_quant(row)
+    assert q[0, 1] == -128 and q[0, 0] == 127 and q[0, 2] == -127
+
+
+def test_q1_dequant_error_bound(oracle):
+    x = (RNG.standard_normal((64, 1024)) * RNG.uniform(0.01, 100, (64, 1))).astype(np.float16)
+    q, s = oracle.row_quant(x)
+    d = s.astype(np.float16).astype(np.float64)[:, None]
+    err = np.abs(q.astype(np.float64) * d - x.astype(np.float64))
+    # rint(fp16(x/d)): fp16 spacing below 128 is at most 1/16, so |q*d - x| <= (1/2 + 1/32) d
+    assert (err <= (0.5 + 1.0 / 32) * d * (1 + 1e-6) + 1e-12).all()
+    assert np.abs(q).max() <= 127 and (np.abs(q).max(axis=1) >= 126).all()
+
+
+# ---------------------------------------------------------------------------
+# encoder per-tensor quantizer (reference KATs)
+# ---------------------------------------------------------------------------
+
+def test_e3_reference_half_away_vector(oracle):
+    """tests/test_encoder_int8_gpu.py:65-72 of the reference."""
+    x = np.array([-127.0, -0.5, -1.5, 0.0, 0.5, 1.5, 127.0], np.float16)
+    s = oracle.tensor_scale(x)
+    assert s == np.float32(1.0)
+    assert oracle.tensor_quant(x, s).tolist() == [-127, -1, -2, 0, 1, 2, 127]
+
+
+@pytest.mark.parametrize("maximum", [0.0, 2.0 ** -24, 2.0 ** -14, 0.5, 127.0, 65504.0])
+def test_e3_reference_extremes(oracle, maximum):
+    """tests/test_encoder_int8_gpu.py:57-64: [-m, m, ..., m] -> [-127, 127, ...]; zero tensor -> s = 1, q = 0."""
+    x = np.full(9, maximum, np.float16)
+    x[0] = -maximum
+    s = oracle.tensor_scale(x)
+    q = oracle.tensor_quant(x, s)
+    if maximum == 0:
+        assert s == 1.0 and (q == 0).all()
+    else:
+        assert s == np.float32(maximum) * np.float32(1.0 / 127.0)
+        assert q[0] == -127 and (q[1:] == 127).all()
+
+
+# ---------------------------------------------------------------------------
+# integer GEMM / conv accumulators and epilogues
+# ---------------------------------------------------------------------------
+
+def test_gemm_acc_matches_numpy_int64(oracle):
+    a = RNG.integers(-128, 128, (37, 200), dtype=np.int8)
+    w = RNG.integers(-128, 128, (53, 200), dtype=np.int8)
+    assert np.array_equal(oracle.gemm_acc(a, w), a.astype(np.int64) @ w.astype(np.int64).T)
+
+
+def test_dequant_zero_accumulator_is_bias_and_fp64_bound(oracle):
+    """Zero products leave exactly the bias (reference tests/test_encoder_int8.py:44-50)."""
+    bias = RNG.standard_normal(40).astype(np.float16)
+    out = oracle.gemm_dequant(np.zeros((3, 40), np.int32), np.ones(3, np.float32), np.ones(40, np.float32), bias)
+    assert np.array_equal(out.view(np.uint16), np.broadcast_to(bias, (3, 40)).view(np.uint16))
+    acc = RNG.integers(-2 ** 20, 2 ** 20, (64, 48)).astype(np.int32)
+    sx = RNG.uniform(1e-4, 1e-2, 64).astype(np.float32)
+    sw = RNG.uniform(1e-4, 1e-2, 48).astype(np.float32)
+    b = RNG.standard_normal(48).astype(np.float16)
+    got = oracle.gemm_dequant(acc, sx, sw, b).astype(np.float64)
+    ref = acc.astype(np.float64) * sx[:, None].astype(np.float64) * sw[None].astype(np.float64) + b.astype(np.float64)
+    ulp16 = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert (np.abs(got - ref) <= ulp16 * 0.5 + np.abs(ref) * 2e-7 + 1e-7).all()
+
+
+def test_swiglu_epilogue_equals_dequant_then_swiglu(oracle):
+    """Reference tests/test_int8_ffn_up_fused_gpu.py:21-33: fused == G1 then quantize_swiglu."""
+    acc = RNG.integers(-200000, 200000, (9, 64)).astype(np.int32)
+    sx = RNG.uniform(1e-4, 1e-3, 9).astype(np.float32)
+    sw = RNG.uniform(1e-3, 1e-2, 64).astype(np.float32)
+    b = RNG.standard_normal(64).astype(np.float16)
+    act = oracle.gemm_swiglu(acc, sx, sw, b)
+    hidden = oracle.gemm_dequant(acc, sx, sw, b)
+    q1, s1 = oracle.row_quant(act)
+    q2, s2 = oracle.swiglu_row_quant(hidden)
+    assert np.array_equal(q1, q2) and np.array_equal(s1, s2)
+    g = hidden[:, :32].astype(np.float64)
+    u = hidden[:, 32:].astype(np.float64)
+    ref = g / (1 + np.exp(-g)) * u
+    assert np.allclose(act.astype(np.float64), ref, rtol=2e-3, atol=1e-4)
+
+
+@pytest.mark.parametrize("magnitude", [0.0, 2.0 ** -14, 1.0])
+def test_swiglu_zero_input_bias_kat(oracle, magnitude):
+    """Reference tests/test_int8_ffn_up_fused_gpu.py:35-46: zero GEMM, bias only."""
+    acc = np.zeros((3, 16), np.int32)
+    b = np.full(16, magnitude, np.float16)
+    act = oracle.gemm_swiglu(acc, np.ones(3, np.float32), np.ones(16, np.float32), b)
+    q, s = oracle.row_quant(act)
+    m = np.float64(magnitude)
+    expect = np.float16(m / (1 + np.exp(-m)) * m)      # 2^-14: ~2^-29 underflows fp16 to zero
+    assert np.allclose(act.astype(np.float64), np.float64(expect), rtol=1e-3)
+    if expect == 0:
+        assert (q == -128).all() and (s == np.float32(1e-30)).all()
+    else:
+        assert (q == 127).all()
+
+
+def _conv_ref(qx, qw, kernel, stride):
+    """Independent int64 direct convolution via numpy slicing (NDHWC, [O, (kd,kh,kw,c)] weights)."""
+    b, d, h, w, c = qx.shape
+    o = qw.shape[0]
+    kd, kh, kw = kernel
+    sd, sh, sw = stride
+    wt = qw.reshape(o, kd, kh, kw, c).astype(np.int64)
+    do, ho, wo = (d - kd) // sd + 1, (h - kh) // sh + 1, (w - kw) // sw + 1
+    out = np.zeros((b, do, ho, wo, o), np.int64)
+    x = qx.astype(np.int64)
+    for a in range(kd):
+        for bb in range(kh):
+            for e in range(kw):
+                patch = x[:, a:a + sd * (do - 1) + 1:sd, bb:bb + sh * (ho - 1) + 1:sh, e:e + sw * (wo - 1) + 1:sw]
+                out += np.einsum("bdhwc,oc->bdhwo", patch, wt[:, a, bb, e])
+    return out
+
+
+@pytest.mark.parametrize("shape,o,kernel,stride", [((1, 5, 9, 11, 7), 19, (3, 3, 3), (1, 2, 2)),
+                                                   ((2, 4, 6, 6, 16), 8, (3, 3, 3), (1, 1, 1)),
+                                                   ((1, 5, 8, 10, 3), 4, (3, 1, 3), (2, 1, 2))])
+def test_conv_acc_matches_independent_reference(oracle, shape, o, kernel, stride):
+    qx = RNG.integers(-127, 128, shape, dtype=np.int8)
+    qw = RNG.integers(-127, 128, (o, kernel[0] * kernel[1] * kernel[2] * shape[-1]), dtype=np.int8)
+    got = oracle.conv3d_acc(qx, qw, kernel, stride)
+    assert np.array_equal(got, _conv_ref(qx, qw, kernel, stride))
+
+
+def test_conv_all_ones_kat_and_output_shape(oracle):
+    """Reference KAT: all-ones 128-channel 3x3x3 conv -> 27*128 = 3456; stride-2 shape (1,4,2,8,4)."""
+    acc = oracle.conv3d_acc(np.ones((1, 3, 10, 18, 128), np.int8), np.ones((128, 3456), np.int8), (3, 3, 3),
+                            (1, 1, 1))
+    assert (acc == 3456).all()
+    acc = oracle.conv3d_acc(np.zeros((1, 5, 8, 10, 3), np.int8), np.zeros((4, 27), np.int8), (3, 1, 3), (2, 1, 2))
+    assert acc.shape[1:4] == (2, 8, 4)
+
+
+def test_prepare_weight_shape_scale_and_error_bound(oracle):
+    """Reference tests/test_encoder_int8.py:20-30: [5,3,3,1,3] packs to (5, 27); scales positive."""
+    w = RNG.standard_normal((5, 3, 3, 1, 3)).astype(np.float32)
+    w[2] = 0
+    q, s = oracle.prepare_conv_weight(w)
+    assert q.shape == (5, 27) and (s > 0).all() and s[2] == 1.0 and (q[2] == 0).all()
+    assert np.abs(q).max() <= 127
+    packed = w.transpose(0, 2, 3, 4, 1).reshape(5, 27)
+    err = np.abs(q.astype(np.float64) * s[:, None] - packed)
+    assert (err <= 0.5 * s[:, None] * (1 + 1e-6)).all()
+
+
+# ---------------------------------------------------------------------------
+# encoder GroupNorm producer
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("c,d,h,w,pre", [(128, 2, 20, 30, False), (256, 3, 13, 19, True), (128, 1, 2, 3, True)])
+def test_gn_stats_against_float64(oracle, c, d, h, w, pre):
+    x = (RNG.standard_normal((d, h, w, c)) * 2 + 0.3).astype(np.float16)
+    pb = RNG.standard_normal(c).astype(np.float16) if pre else None
+    st = oracle.gn_stats(x, 1e-6, pb)
+    v = x.astype(np.float32)
+    if pre:
+        v = (v + pb.astype(np.float32)).astype(np.float16)
+    g = v.astype(np.float64).reshape(d, h * w, 32, c // 32)
+    mean = g.mean(axis=(1, 3))
+    var = g.var(axis=(1, 3))
+    assert np.allclose(st[..., 0], mean, rtol=1e-5, atol=1e-6)
+    assert np.allclose(st[..., 1], 1 / np.sqrt(var + 1e-6), rtol=1e-5)
+
+
+def test_norm_pack_structure_and_float64(oracle):
+    d, h, w, c = 3, 6, 7, 128
+    x = RNG.standard_normal((d, h, w, c)).astype(np.float16)
+    gamma = (1 + 0.2 * RNG.standard_normal(c)).astype(np.float16)
+    beta = (0.2 * RNG.standard_normal(c)).astype(np.float16)
+    st = oracle.gn_stats(x, 1e-6)
+    y, _, amax = oracle.norm_pack(x, gamma, beta, st)
+    assert y.shape == (d + 2, h + 2, w + 2, c)
+    assert (y[:2] == 0).all()                                    # causal zero planes
+    assert np.array_equal(y[2:, 0], y[2:, 2]) and np.array_equal(y[2:, -1], y[2:, -3])   # reflect rows
+    assert np.array_equal(y[2:, :, 0], y[2:, :, 2]) and np.array_equal(y[2:, :, -1], y[2:, :, -3])
+    assert amax == np.abs(y.astype(np.float32)).max()
+    mean = np.repeat(st[..., 0], c // 32, axis=1)[:, None, None, :].astype(np.float64)
+    rstd = np.repeat(st[..., 1], c // 32, axis=1)[:, None, None, :].astype(np.float64)
+    z = (x.astype(np.float64) - mean) * rstd * gamma.astype(np.float64) + beta.astype(np.float64)
+    z = z.astype(np.float16).astype(np.float64)
+    ref = z / (1 + np.exp(-z))
+    inner = y[2:, 1:-1, 1:-1].astype(np.float64)
+    assert np.allclose(inner, ref, rtol=2e-3, atol=2e-4)
+    s = oracle.scale_from_amax(amax)
+    _, q, _ = oracle.norm_pack(x, gamma, beta, st, scale=s, want_fp16=False)
+    assert np.array_equal(q, oracle.tensor_quant(y, s))         # pass 2 == E3 quant of pass-1 values
+
+
+# ---------------------------------------------------------------------------
+# decoder producers
+# ---------------------------------------------------------------------------
+
+def test_w16_tree_order_closed_form(oracle):
+    """The published W16 tree: lanes combine inside 32-lane groups first, then across groups.
+
+    Partials 2^24 (lane 0) and 1, 1 at lanes 1 and 17: the in-group level 16 adds
+    lanes 1 and 17 exactly (2) before lane 0 absorbs it -> 2^24 + 2.  Ones at lanes
+    1 and 33 (different groups) are each absorbed into 2^24 separately (ties to
+    even) -> 2^24.  A sequential sum gives 2^24 for the first case and a single
+    halving tree over all 512 partials gives 2^24 + 2 for the second.
+    """
+    x = np.zeros(2048, np.float32)
+    x[0], x[4], x[68] = 2.0 ** 12, 1.0, 1.0
+    assert oracle.tree_sumsq_w16(x) == np.float32(2.0 ** 24 + 2)
+    x = np.zeros(2048, np.float32)
+    x[0], x[4], x[132] = 2.0 ** 12, 1.0, 1.0
+    assert oracle.tree_sumsq_w16(x) == np.float32(2.0 ** 24)
+    # the per-lane fma chain: x0^2 + x1^2 with x1^2 absorbed by the fma
+    x = np.zeros(2048, np.float32)
+    x[0], x[1] = 2.0 ** 12, 1.0
+    assert oracle.tree_sumsq_w16(x) == np.float32(2.0 ** 24)    # fma(2^12,2^12,1) ties to even
+    v = RNG.standard_normal(2048).astype(np.float32)
+    assert np.isclose(oracle.tree_sumsq_w16(v), np.sum(v.astype(np.float64) ** 2), rtol=1e-6)
+    assert np.isclose(oracle.tree_sum_plain(v), np.sum(v.astype(np.float64)), rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("recipe", [0, 1])
+def test_residual_rms_quant_against_float64(oracle, recipe):
+    m, k = 33, 2048
+    h = RNG.standard_normal((m, k)).astype(np.float16)
+    o = RNG.standard_normal((m, k)).astype(np.float16)
+    g = (0.1 * RNG.standard_normal(k)).astype(np.float16)
+    w = (1 + 0.1 * RNG.standard_normal(k)).astype(np.float16)
+    h_out, q, s = oracle.residual_rms_quant(h, o, g, w, 1e-5, recipe)
+    raw = o.astype(np.float64) * g.astype(np.float64) + h.astype(np.float64)      # exact for fp16 inputs
+    assert np.array_equal(h_out.view(np.uint16), raw.astype(np.float32).astype(np.float16).view(np.uint16))
+    inv = 1 / np.sqrt((raw ** 2).mean(axis=1, keepdims=True) + 1e-5)
+    n = h_out.astype(np.float64) * inv * w.astype(np.float64)
+    d = s.astype(np.float16).astype(np.float64)[:, None]
+    assert np.allclose(s, np.abs(n).max(axis=1) / 127, rtol=2e-3)
+    assert (np.abs(q * d - n) <= 0.5 * d + 2e-3 * np.abs(n) + 1e-6).all()
+
+
+def test_rms_and_layernorm_against_float64(oracle):
+    m, k = 17, 1024
+    x = RNG.standard_normal((m, k)).astype(np.float16)
+    o = RNG.standard_normal((m, k)).astype(np.float16)
+    gate = (0.1 * RNG.standard_normal(k)).astype(np.float16)
+    gamma = (1 + 0.1 * RNG.standard_normal(k)).astype(np.float16)
+    beta = (0.1 * RNG.standard_normal(k)).astype(np.float16)
+    xd = x.astype(np.float64)
+    ref = xd / np.sqrt((xd ** 2).mean(1, keepdims=True) + 1e-5) * gamma.astype(np.float64)
+    assert np.allclose(oracle.rms_fp16(x, gamma, 1e-5).astype(np.float64), ref, rtol=2e-3, atol=2e-3)
+    raw = o.astype(np.float64) * gate.astype(np.float64) + xd
+    mu = raw.mean(1, keepdims=True)
+    ln = (raw - mu) / np.sqrt(raw.var(1, keepdims=True) + 1e-5) * gamma.astype(np.float64) + beta.astype(np.float64)
+    got = oracle.residual_layernorm(x, o, gate, gamma, beta, 1e-5).astype(np.float64)
+    assert np.allclose(got, ln, rtol=2e-3, atol=2e-3)
+
+
+def test_qk_rope_closed_forms(oracle):
+    """cos=1, sin=0 returns the normalised rows; cos=0, sin=1 is the exact rotate-half permutation."""
+    tokens, heads = 5, 3
+    x = RNG.standard_normal((1, tokens, heads * 192)).astype(np.float16)
+    ones = np.ones((1, tokens, 1, 48), np.float16)
+    zeros = np.zeros((1, tokens, 1, 48), np.float16)
+    q_id, k_id = oracle.qk_rope(x, ones, zeros, heads, 1e-6)
+    xr = x.reshape(tokens, heads, 3, 64).astype(np.float64)
+    for part, got in ((0, q_id), (1, k_id)):
+        v = xr[:, :, part]
+        ref = v / np.sqrt((v ** 2).mean(-1, keepdims=True) + 1e-6)
+        assert np.allclose(got[0].astype(np.float64), ref, rtol=2e-3, atol=2e-3)
+    q_rot, _ = oracle.qk_rope(x, zeros, ones, heads, 1e-6)
+    q0 = q_id[0].astype(np.float32)
+    want = q0.copy()
+    want[..., :24] = -q0[..., 24:48]
+    want[..., 24:48] = q0[..., :24]
+    assert np.array_equal(q_rot[0].astype(np.float32), want)
