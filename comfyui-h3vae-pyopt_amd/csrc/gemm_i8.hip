@@ -116,12 +116,14 @@ __device__ __forceinline__ float g1_value(int32_t acc, float sx, float sw, const
 // M0 + 16*i, so one wave instruction fills 1 KB of LDS contiguously: 16 tile
 // rows of 64 bytes.  Lane i loads row i/4 and puts its 16-byte chunk in slot
 // i%4; the chunk it fetches is slot ^ swz(row) so that slot s of row r holds
-// k-chunk s ^ swz(r).  swz(r) = (r >> 1) & 3 makes the 16-byte fragment reads
-// of 8 consecutive rows hit distinct LDS banks (32 or 64 banks).
+// k-chunk s ^ swz(r).  swz(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1) (bits 1-3 of the
+// row, so it is the same for a row's DMA lane and its reader) makes the 16-byte
+// fragment reads conflict free both for 8-lane groups on 32 banks and for
+// 16-lane groups on 64 banks (rows r, r+4, r+8, r+12 get distinct slots).
 typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef const __attribute__((address_space(1))) void* gbl_void_t;
 
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 3; }
+__device__ __forceinline__ int swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
 
 __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds((gbl_void_t)g, (lds_void_t)lds, 16, 0, 0);
@@ -249,7 +251,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
     };
 
     // Prologue: fill the whole ring, then wait for stage 0.
@@ -296,51 +298,87 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Epilogue.  v_mfma 32x32 result layout: lane holds column lane&31 and rows
-    // (r/4)*8 + (lane/32)*4 + r%4 for register r.
-    const int col_l = lane & 31;
-    const int row_l = (lane >> 5) * 4;
+    // Epilogue.  The MFMAs compute W * A^T blocks, so in the v_mfma 32x32 result
+    // layout lane l holds output row m = lane&31 of the block and, in register
+    // r, output column n = (r/4)*8 + (l/32)*4 + r%4: four consecutive columns per
+    // register quad, stored as one 8-byte (fp16) or 16-byte (int32) vector.
+    const int mrow = lane & 31;
+    const int ncol = (lane >> 5) * 4;
     if constexpr (EP == Epi::SwiGLU) {
         uint16_t* out = static_cast<uint16_t*>(p.out);
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i) {
+            const int row = m0 + wm * WM + i * 32 + mrow;
+            if (row >= p.M) continue;
+            const float sx = p.sx[(int64_t)row * p.sx_stride];
 #pragma unroll
             for (int j = 0; j < FN / 2; ++j) {
-                int c = tn * (BN / 2) + (wn * WN) / 2 + j * 32 + col_l;
-                if (c >= p.N) continue;
-                float swg = p.sw[c], swu = p.sw[p.N + c];
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + row_l + (r & 3);
-                    if (row >= p.M) continue;
-                    float sx = p.sx[(int64_t)row * p.sx_stride];
-                    float g = rt16(g1_value(acc[i][2 * j][r], sx, swg, p.bias, c));
-                    float u = rt16(g1_value(acc[i][2 * j + 1][r], sx, swu, p.bias, p.N + c));
-                    out[(int64_t)row * p.ldo + c] = f2h(silu(g) * u);
-                }
-            }
-    } else {
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int c0 = tn * (BN / 2) + (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
+                    if (c0 >= p.N) continue;
+                    u16x4 v;
 #pragma unroll
-        for (int i = 0; i < FM; ++i)
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-                int col = n0 + wn * WN + j * 32 + col_l;
-                if (col >= p.N) continue;
-                float sw = 0.0f;
-                if constexpr (EP == Epi::Dequant) sw = p.sw[col];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    int row = m0 + wm * WM + i * 32 + (r >> 2) * 8 + row_l + (r & 3);
-                    if (row >= p.M) continue;
-                    if constexpr (EP == Epi::Int32) {
-                        static_cast<int32_t*>(p.out)[(int64_t)row * p.ldo + col] = acc[i][j][r];
+                    for (int e = 0; e < 4; ++e) {
+                        const int c = c0 + e < p.N ? c0 + e : p.N - 1;
+                        float g = rt16(g1_value(acc[i][2 * j][q4 * 4 + e], sx, p.sw[c], p.bias, c));
+                        float u = rt16(g1_value(acc[i][2 * j + 1][q4 * 4 + e], sx, p.sw[p.N + c], p.bias, p.N + c));
+                        v[e] = f2h(silu(g) * u);
+                    }
+                    uint16_t* dst = out + (int64_t)row * p.ldo + c0;
+                    if (c0 + 4 <= p.N && (p.ldo & 3) == 0) {
+                        *reinterpret_cast<u16x4*>(dst) = v;
                     } else {
-                        float sx = p.sx[(int64_t)row * p.sx_stride];
-                        static_cast<uint16_t*>(p.out)[(int64_t)row * p.ldo + col] =
-                            f2h(g1_value(acc[i][j][r], sx, sw, p.bias, col));
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c0 + e < p.N) dst[e] = v[e];
                     }
                 }
             }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int row = m0 + wm * WM + i * 32 + mrow;
+            if (row >= p.M) continue;
+            float sx = 0.0f;
+            if constexpr (EP == Epi::Dequant) sx = p.sx[(int64_t)row * p.sx_stride];
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int c0 = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
+                    if (c0 >= p.N) continue;
+                    const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
+                    if constexpr (EP == Epi::Int32) {
+                        int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
+                        if (full) {
+                            v4i v = {acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
+                            *reinterpret_cast<v4i*>(dst) = v;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
+                        }
+                    } else {
+                        u16x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int c = c0 + e < p.N ? c0 + e : p.N - 1;
+                            v[e] = f2h(g1_value(acc[i][j][q4 * 4 + e], sx, p.sw[c], p.bias, c));
+                        }
+                        uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + c0;
+                        if (full) {
+                            *reinterpret_cast<u16x4*>(dst) = v;
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                if (c0 + e < p.N) dst[e] = v[e];
+                        }
+                    }
+                }
+            }
+        }
     }
 }
 

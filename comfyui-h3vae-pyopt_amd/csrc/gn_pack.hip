@@ -1,5 +1,5 @@
-// Encoder INT8 producer: per-frame GroupNorm(32) statistics, then a two-pass
-// norm / SiLU / causal + reflect pad recompute that writes padded INT8 directly
+// Encoder INT8 producer: per-frame GroupNorm(32) statistics, then a norm /
+// SiLU / causal + reflect pad recompute that writes padded INT8 directly
 // (opt/encoder_int8_norm.py:16-110, opt/encoder_fused_temporal_norm.py:12-51,
 // opt/encoder_fused_norm_bias.py:14-39, opt/encoder_int8_norm_recompute.py:11-48).
 //
@@ -7,11 +7,21 @@
 // [D+2, H+2, W+2, C], frames 0 and 1 zero, spatial reflect padding of 1.
 //
 // Launch sequence (all on the caller's stream, no host synchronisation):
-//   gn_partial   grid (chunks, D): per 256-pixel chunk and group, avg and M2
-//   gn_merge     grid D x 32 threads: Chan merge of the chunks -> (mean, rstd);
-//                also clears the absmax word
-//   norm_pack<0> every padded element's norm/SiLU value -> atomic absmax
-//   norm_pack<1> same values -> int8 with the per-tensor scale; writes the scale
+//   gn_init       clears the per-(frame, channel) max/min keys and the absmax word
+//   gn_partial    grid (chunks, D): per 256-pixel chunk and group, avg and M2;
+//                 per (frame, channel) max and min of the (pre-biased) input
+//   gn_merge      grid D: Chan merge of the chunks -> (mean, rstd); absmax
+//                 candidate from the per-channel extremes (below)
+//   norm_pack<0>  full absmax pass, only when the candidate cannot be proven exact
+//   norm_pack<1>  every padded value -> int8 with the per-tensor scale; writes the scale
+//
+// Absmax shortcut.  z = fp16(((v - mean) * rstd) * gamma + beta) is monotone in
+// v for each channel (every rounding step is monotone; the direction is the
+// sign of gamma), so the largest z of a (frame, channel) is z(vmax) or z(vmin)
+// exactly.  SiLU is increasing for z above its minimum (|SiLU| <= 0.2785 below
+// z = 0.43), so if the largest fp16(SiLU(zmax)) over all (frame, channel) is at
+// least 0.5, it is the absmax of the whole padded tensor and the full pass
+// exits at once; otherwise the full pass runs.  The result is bitwise the same.
 //
 // Fixed reduction order (shared with the CPU oracle): a chunk has PL = 256/(C/8)
 // pixel lanes; lane pl owns pixels pl, pl+PL, ...; per pixel the group's
@@ -26,6 +36,8 @@ namespace {
 constexpr int kGroups = 32;
 constexpr int kChunk = 256;
 constexpr int kNT = 256;
+constexpr int kMaxC = 256;
+constexpr float kShortcutFloor = 0.5f;
 
 __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     u16x8 a = *reinterpret_cast<const u16x8*>(p);
@@ -33,11 +45,31 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     for (int e = 0; e < 8; ++e) v[e] = h2f(a[e]);
 }
 
+// Order-preserving float <-> uint key (for atomic max / min of signed floats).
+__device__ __forceinline__ uint32_t fkey(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fval(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __builtin_bit_cast(float, u);
+}
+
+__global__ void gn_init(uint32_t* __restrict__ vmax, uint32_t* __restrict__ vmin, int n, uint32_t* __restrict__ amax) {
+    int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        vmax[i] = 0u;
+        vmin[i] = 0xffffffffu;
+    }
+    if (i == 0) *amax = 0u;
+}
+
 // C channels, cg = C/32 channels per group, TPP = C/8 threads per pixel.
 template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
                                                   int hw, int nchunk, float* __restrict__ part_avg,
-                                                  float* __restrict__ part_m2) {
+                                                  float* __restrict__ part_m2, uint32_t* __restrict__ vmax,
+                                                  uint32_t* __restrict__ vmin) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
     constexpr int PL = kNT / TPP;
@@ -45,6 +77,8 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     constexpr int GPT = 8 / CG;                 // groups inside one thread's 8 channels
     __shared__ float red[PL][kGroups];
     __shared__ float avg_s[kGroups];
+    __shared__ float mx_s[PL][C];
+    __shared__ float mn_s[PL][C];
 
     const int j = blockIdx.x, t = blockIdx.y;
     const int tid = threadIdx.x;
@@ -64,14 +98,21 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
         }
     };
 
-    float ls[GPT];
+    float ls[GPT], vmx[8], vmn[8];
 #pragma unroll
     for (int gi = 0; gi < GPT; ++gi) ls[gi] = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { vmx[e] = -__builtin_inff(); vmn[e] = __builtin_inff(); }
     for (int s = 0; s < STEPS; ++s) {
         int p = pl + s * PL;
         if (p >= npix) break;
         float v[8];
         load(p, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            vmx[e] = __builtin_fmaxf(vmx[e], v[e]);
+            vmn[e] = __builtin_fminf(vmn[e], v[e]);
+        }
 #pragma unroll
         for (int gi = 0; gi < GPT; ++gi) {
             float ps = v[gi * CG];
@@ -82,11 +123,25 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     }
 #pragma unroll
     for (int gi = 0; gi < GPT; ++gi) red[pl][cv * GPT + gi] = ls[gi];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        mx_s[pl][cv * 8 + e] = vmx[e];
+        mn_s[pl][cv * 8 + e] = vmn[e];
+    }
     __syncthreads();
     if (tid < kGroups) {
         for (int off = PL / 2; off >= 1; off >>= 1)
             for (int i = 0; i < off; ++i) red[i][tid] = red[i][tid] + red[i + off][tid];
         avg_s[tid] = red[0][tid] / (float)(npix * CG);
+    }
+    if (tid < C) {
+        float a = mx_s[0][tid], b = mn_s[0][tid];
+        for (int i = 1; i < PL; ++i) {
+            a = __builtin_fmaxf(a, mx_s[i][tid]);
+            b = __builtin_fminf(b, mn_s[i][tid]);
+        }
+        atomicMax(&vmax[t * C + tid], fkey(a));
+        atomicMin(&vmin[t * C + tid], fkey(b));
     }
     __syncthreads();
 
@@ -123,37 +178,95 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     }
 }
 
-// One thread per (frame, group): sequential merge over chunks as in _merge.
-__global__ void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2, int hw, int nchunk,
-                         int cg, float eps, float* __restrict__ stats, uint32_t* __restrict__ amax_bits) {
-    const int t = blockIdx.x, g = threadIdx.x;
-    if (t == 0 && g == 0) *amax_bits = 0u;
-    if (g >= kGroups) return;
+// One workgroup per frame.  Chunk partials are staged through LDS in batches;
+// the 32 group threads then merge them sequentially as in _merge.
+constexpr int kMergeBatch = 256;
+
+__global__ __launch_bounds__(kNT) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
+                                                const uint32_t* __restrict__ vmax, const uint32_t* __restrict__ vmin,
+                                                const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+                                                int hw, int nchunk, int c, float eps, float* __restrict__ stats,
+                                                uint32_t* __restrict__ amax_bits) {
+    __shared__ float sa[kMergeBatch * kGroups];
+    __shared__ float sm[kMergeBatch * kGroups];
+    __shared__ float mean_s[kGroups], rstd_s[kGroups];
+    __shared__ float red[kNT / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const int cg = c / kGroups;
     const float total = (float)(hw * cg);
-    const float* pa = part_avg + (int64_t)t * nchunk * kGroups + g;
-    const float* pm = part_m2 + (int64_t)t * nchunk * kGroups + g;
+    const float* pa = part_avg + (int64_t)t * nchunk * kGroups;
+    const float* pm = part_m2 + (int64_t)t * nchunk * kGroups;
+
+    // pass 1: mean = (sum_j avg_j * n_j) / N
     float san = 0.0f;
-    for (int j = 0; j < nchunk; ++j) {
-        int cnt = hw - j * kChunk < kChunk ? hw - j * kChunk : kChunk;
-        san = san + pa[(int64_t)j * kGroups] * (float)(cnt * cg);
+    for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
+        const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
+        __syncthreads();
+        for (int i = tid; i < nb * kGroups; i += kNT) sa[i] = pa[(int64_t)j0 * kGroups + i];
+        __syncthreads();
+        if (tid < kGroups) {
+            for (int j = 0; j < nb; ++j) {
+                int jj = j0 + j;
+                int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
+                san = san + sa[j * kGroups + tid] * (float)(cnt * cg);
+            }
+        }
     }
     const float mean = san / total;
+    // pass 2: var = (sum_j (m2_j + (n_j * d_j) * d_j)) / N
     float sv = 0.0f;
-    for (int j = 0; j < nchunk; ++j) {
-        int cnt = hw - j * kChunk < kChunk ? hw - j * kChunk : kChunk;
-        float dl = pa[(int64_t)j * kGroups] - mean;
-        float nj = (float)(cnt * cg);
-        sv = sv + (pm[(int64_t)j * kGroups] + (nj * dl) * dl);
+    for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
+        const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
+        __syncthreads();
+        for (int i = tid; i < nb * kGroups; i += kNT) {
+            sa[i] = pa[(int64_t)j0 * kGroups + i];
+            sm[i] = pm[(int64_t)j0 * kGroups + i];
+        }
+        __syncthreads();
+        if (tid < kGroups) {
+            for (int j = 0; j < nb; ++j) {
+                int jj = j0 + j;
+                int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
+                float dl = sa[j * kGroups + tid] - mean;
+                float nj = (float)(cnt * cg);
+                sv = sv + (sm[j * kGroups + tid] + (nj * dl) * dl);
+            }
+        }
     }
-    float var = sv / total;
-    if (var < 0.0f) var = 0.0f;
-    stats[(t * kGroups + g) * 2] = mean;
-    stats[(t * kGroups + g) * 2 + 1] = rsqrt_rn(var + eps);
+    if (tid < kGroups) {
+        float var = sv / total;
+        if (var < 0.0f) var = 0.0f;
+        const float rstd = rsqrt_rn(var + eps);
+        stats[(t * kGroups + tid) * 2] = mean;
+        stats[(t * kGroups + tid) * 2 + 1] = rstd;
+        mean_s[tid] = mean;
+        rstd_s[tid] = rstd;
+    }
+    __syncthreads();
+    // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map
+    float cand = 0.0f;
+    if (tid < c) {
+        const int g = tid / cg;
+        const float gm = h2f(gamma[tid]), bt = h2f(beta[tid]);
+        const float v = gm >= 0.0f ? fval(vmax[t * c + tid]) : fval(vmin[t * c + tid]);
+        const float z = rt16(((v - mean_s[g]) * rstd_s[g]) * gm + bt);
+        cand = __builtin_fabsf(rt16(silu(z)));
+    }
+    cand = wave_max(cand);
+    if ((tid & 63) == 0) red[tid >> 6] = cand;
+    __syncthreads();
+    if (tid == 0) {
+        float m = red[0];
+        for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
+        // every candidate is the |value| of a real element, so it never exceeds the true absmax
+        atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
+    }
 }
 
 __device__ __forceinline__ int reflect(int i, int n) { return i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i); }
 
-// PASS 0: absmax of all padded values.  PASS 1: int8 with the per-tensor scale.
+// PASS 0: absmax of all padded values (skipped when the candidate is exact).
+// PASS 1: int8 with the per-tensor scale.
 template <int C, bool PRE_BIAS, int PASS>
 __global__ __launch_bounds__(kNT) void norm_pack(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
                                                  const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
@@ -165,7 +278,9 @@ __global__ __launch_bounds__(kNT) void norm_pack(const uint16_t* __restrict__ x,
     const int hp = h + 2, wp = w + 2;
     const int64_t nvec = (int64_t)(d + 2) * hp * wp * TPP;
     float s = 0.0f;
-    if constexpr (PASS == 1) {
+    if constexpr (PASS == 0) {
+        if (__builtin_bit_cast(float, *amax_bits) >= kShortcutFloor) return;
+    } else {
         s = e3_scale(__builtin_bit_cast(float, *amax_bits));
         if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
     }
@@ -227,18 +342,26 @@ __global__ __launch_bounds__(kNT) void norm_pack(const uint16_t* __restrict__ x,
     }
 }
 
+int64_t workspace_floats(int d, int h, int w) {
+    int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
+    return 2 * (int64_t)d * nchunk * kGroups + 2 * (int64_t)d * kMaxC;
+}
+
 template <int C, bool PB>
 void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta, float eps,
-                int d, int h, int w, int8_t* q, float* scale, float* stats, float* part, uint32_t* amax_bits,
+                int d, int h, int w, int8_t* q, float* scale, float* stats, float* ws, uint32_t* amax_bits,
                 hipStream_t stream) {
     const int hw = h * w;
     const int nchunk = (hw + kChunk - 1) / kChunk;
-    float* part_avg = part;
-    float* part_m2 = part + (int64_t)d * nchunk * kGroups;
+    float* part_avg = ws;
+    float* part_m2 = ws + (int64_t)d * nchunk * kGroups;
+    uint32_t* vmax = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups);
+    uint32_t* vmin = vmax + (int64_t)d * kMaxC;
+    hipLaunchKernelGGL(gn_init, dim3((d * C + kNT - 1) / kNT), dim3(kNT), 0, stream, vmax, vmin, d * C, amax_bits);
     hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
-                       part_m2);
-    hipLaunchKernelGGL(gn_merge, dim3(d), dim3(64), 0, stream, part_avg, part_m2, hw, nchunk, C / kGroups, eps, stats,
-                       amax_bits);
+                       part_m2, vmax, vmin);
+    hipLaunchKernelGGL(gn_merge, dim3(d), dim3(kNT), 0, stream, part_avg, part_m2, vmax, vmin, gamma, beta, hw, nchunk,
+                       C, eps, stats, amax_bits);
     const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
     int64_t want = (nvec + kNT - 1) / kNT;
     unsigned blocks = (unsigned)(want > 16384 ? 16384 : want);
@@ -257,8 +380,7 @@ extern "C" {
 
 int64_t h3v_gn_norm_pack_workspace_floats(int d, int h, int w) {
     if (d <= 0 || h <= 0 || w <= 0) return -1;
-    int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
-    return 2 * (int64_t)d * nchunk * kGroups;
+    return workspace_floats(d, h, w);
 }
 
 int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta,
@@ -273,7 +395,7 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
                 what);
     H3V_REQUIRE(eps > 0.0f, "%s: eps must be positive", what);
     H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(beta, 16) && (!pre_bias || aligned(pre_bias, 16)) &&
-                    aligned(q, 8),
+                    aligned(q, 8) && aligned(workspace, 4),
                 "%s: x, gamma, beta, pre_bias need 16-byte and q 8-byte alignment", what);
     if (c == 128) {
         if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
