@@ -8,6 +8,9 @@ in FP32; dims 48..63 pass through.
 """
 from __future__ import annotations
 
+import copy
+import os
+
 import torch
 
 from .. import _hip
@@ -65,3 +68,24 @@ class FusedQKAttention(torch.nn.Module):
         v = qkv.view(b, n, a.heads, 3 * a.dim_head)[..., 2 * a.dim_head:]
         y = a.perform_attention(q, k, v, pack_info or {})
         return a.to_out(y.reshape(b, n, -1))
+
+
+def clone_with_qk_fusion(raw, rows=8):
+    """Copy the decoder's module containers with every attention wrapped in FusedQKAttention.
+
+    Weights are shared read-only and the original decoder is left intact
+    (reference opt/decoder_fused_qk_rope.py:76-89).
+    """
+    if raw.training or os.environ.get("MINIMAX_H3_VAE_DECODER_VIT_FP32_NORM", "1").lower() in ("0", "false", "no",
+                                                                                               "off"):
+        raise ValueError("QK fusion requires eval inference with FP32 norm enabled")
+    decoder = copy.copy(raw)
+    decoder._modules = raw._modules.copy()
+    blocks = []
+    for block in raw.transformer_blocks:
+        new = copy.copy(block)
+        new._modules = block._modules.copy()
+        new.attn = FusedQKAttention(block.attn, rows).eval()
+        blocks.append(new)
+    decoder.transformer_blocks = torch.nn.ModuleList(blocks)
+    return decoder

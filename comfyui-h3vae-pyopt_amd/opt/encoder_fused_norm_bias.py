@@ -1,0 +1,141 @@
+"""Encoder residual block whose norm/SiLU/pad producers carry the conv bias.
+
+Mirror of opt/encoder_fused_norm_bias.py (``BiasFusedResidualBlock``,
+:121-140) and of the norm-pack holder ``FusedNormPadConv``
+(opt/encoder_fused_temporal_norm.py:101-118; opaque op
+opt/encoder_fused_norm_opaque.py:10-21) in fishelegs/ComfyUI-H3VAE-PyOpt.
+
+With INT8 wrappers installed and norm fusion on (the gfx950 default), a block
+is two ``h3vae_encoder::int8_norm_conv3d`` calls.  The first conv's bias is
+not applied in its epilogue; it is folded into the second producer as
+``pre_bias`` (v = fp16(v + bias) before the statistics).  The block input
+(or its ``nin_shortcut`` projection) is added last.
+
+Without INT8 wrappers (the FP16 encoder mode, outside the INT8 hot path) the
+same producers run as PyTorch GPU ops; nothing in this file ever falls back
+from the INT8 path to them.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def _check_channel_vectors(x, *vectors):
+    c = x.shape[1]
+    for parameter in vectors:
+        if (parameter.shape != (c,) or parameter.dtype != x.dtype or parameter.device != x.device
+                or not parameter.is_contiguous()):
+            raise ValueError("Expected contiguous FP16 channel vectors on input device")
+
+
+def fused_temporal_norm_pad(x, weight, bias, eps, pre_bias=None):
+    """FP16 encoder mode: per-frame GroupNorm(32), SiLU, 2 causal zero frames + reflect pad 1.
+
+    -> fp16 [1, C, D+2, H+2, W+2] channels-last-3d.  PyTorch ops on the GPU.
+    """
+    b, c, d, h, w = x.shape
+    if b != 1 or x.dtype != torch.float16 or c % 32 or min(h, w) < 2:
+        raise ValueError("Validated scope: batch-one FP16, C divisible by 32, spatial >=2")
+    _check_channel_vectors(x, weight, bias, *(() if pre_bias is None else (pre_bias,)))
+    v = x.float()
+    if pre_bias is not None:
+        v = (v + pre_bias.float().view(1, c, 1, 1, 1)).half().float()
+    g = v.view(1, 32, c // 32, d, h, w)
+    mean = g.mean(dim=(2, 4, 5), keepdim=True)
+    var = g.var(dim=(2, 4, 5), unbiased=False, keepdim=True)
+    z = ((g - mean) * torch.rsqrt(var + eps)).view(1, c, d, h, w)
+    z = (z * weight.float().view(1, c, 1, 1, 1) + bias.float().view(1, c, 1, 1, 1)).half().float()
+    z = (z / (1.0 + torch.exp(-z))).half()
+    z = F.pad(z, (1, 1, 1, 1, 0, 0), mode="reflect")
+    y = torch.zeros((b, c, d + 2, h + 2, w + 2), device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
+    y[:, :, 2:] = z
+    return y
+
+
+@torch.library.custom_op("h3vae_encoder::temporal_norm_pack", mutates_args=(), device_types="cuda")
+def temporal_norm_pack(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float) -> torch.Tensor:
+    return fused_temporal_norm_pad(x, weight, bias, eps)
+
+
+@temporal_norm_pack.register_fake
+def _fake_norm_pack(x, weight, bias, eps):
+    b, c, d, h, w = x.shape
+    return torch.empty((b, c, d + 2, h + 2, w + 2), device=x.device, dtype=x.dtype,
+                       memory_format=torch.channels_last_3d)
+
+
+@torch.library.custom_op("h3vae_encoder::bias_temporal_norm_pack", mutates_args=(), device_types="cuda")
+def bias_temporal_norm_pack(x: torch.Tensor, pre_bias: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor,
+                            eps: float) -> torch.Tensor:
+    return fused_temporal_norm_pad(x, weight, bias, eps, pre_bias=pre_bias)
+
+
+@bias_temporal_norm_pack.register_fake
+def _fake_bias_norm_pack(x, pre_bias, weight, bias, eps):
+    b, c, d, h, w = x.shape
+    return torch.empty((b, c, d + 2, h + 2, w + 2), device=x.device, dtype=x.dtype,
+                       memory_format=torch.channels_last_3d)
+
+
+class FusedNormPadConv(torch.nn.Module):
+    """GroupNorm(32) + SiLU + causal/reflect pad feeding a 3x3x3 conv (reference :101-118)."""
+
+    def __init__(self, norm, conv, config=(128, 32, 4), with_conv=True):
+        super().__init__()
+        if type(norm).__name__ != "TemporalIsolatedSpatialParallelGroupNorm" or norm.num_groups != 32:
+            raise ValueError("Expected temporal-isolated GroupNorm with 32 groups")
+        if (conv.padding != (1, 1, 1) or conv.kernel_size != (3, 3, 3) or not conv.causal
+                or conv.pad_mode != "reflect" or conv.pad_mode_t != "constant" or conv.spatial_parallel):
+            raise ValueError("Expected single-GPU causal 3x3x3 reflect-padded conv")
+        self.norm_weight = norm.weight
+        self.norm_bias = norm.bias
+        self.eps = norm.eps
+        self.weight = conv.weight
+        self.bias = conv.bias
+        self.stride = conv.stride
+        self.config = config
+        self.with_conv = with_conv
+
+    def forward(self, x):
+        y = temporal_norm_pack(x, self.norm_weight, self.norm_bias, self.eps)
+        return F.conv3d(y, self.weight, self.bias, stride=self.stride) if self.with_conv else y
+
+
+# The reference's opaque-op subclass has the same behaviour here (every producer is an opaque op).
+OpaqueFusedNormPadConv = FusedNormPadConv
+
+
+class BiasFusedResidualBlock(torch.nn.Module):
+    """Residual block: norm1/conv1 -> norm2(+conv1 bias)/conv2 -> + shortcut (reference :121-140)."""
+
+    def __init__(self, block):
+        super().__init__()
+        if block.use_fused_norm or block.conv1.bias is None:
+            raise ValueError("Expected original residual block with conv1 bias")
+        self.first = OpaqueFusedNormPadConv(block.norm1, block.conv1, with_conv=False)
+        self.second = OpaqueFusedNormPadConv(block.norm2, block.conv2, with_conv=False)
+        self.shortcut = getattr(block, "nin_shortcut", None)
+        # INT8 wrappers are installed by encoder_int8_integration.install_int8_encoder_prefix;
+        # None keeps the FP16 encoder mode.
+        self.int8_first = None
+        self.int8_second = None
+
+    def _residual_body(self, x, second_bias):
+        if self.int8_first is not None and self.int8_first.fuse_norm:
+            h = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
+            return self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias,
+                                                 self.second.eps, pre_bias=self.first.bias)
+        first_input = self.first(x)
+        h = (self.int8_first(first_input) if self.int8_first is not None
+             else F.conv3d(first_input, self.first.weight, None, stride=self.first.stride))
+        second_input = bias_temporal_norm_pack(h, self.first.bias, self.second.norm_weight,
+                                               self.second.norm_bias, self.second.eps)
+        return (self.int8_second(second_input) if self.int8_second is not None
+                else F.conv3d(second_input, self.second.weight, second_bias, stride=self.second.stride))
+
+    def forward(self, x, zq=None):
+        if zq is not None:
+            raise ValueError("Unconditional inference only")
+        h = self._residual_body(x, self.second.bias)
+        return (self.shortcut(x) if self.shortcut is not None else x) + h

@@ -153,6 +153,15 @@ int h3v_residual_layernorm(const uint16_t* h, const uint16_t* o, const uint16_t*
 int h3v_qk_rope(const uint16_t* qkv, const uint16_t* cosv, const uint16_t* sinv, int64_t tokens, int heads,
                 int head_dim, int rot_dim, float eps, uint16_t* q, uint16_t* k, hipStream_t stream);
 
+/* Residual + bias pack ahead of the stride-2 downsample conv of the last encoder prefix block.
+ * x, residual: fp16 NDHWC [d, h, w, c] (batch one); bias: fp16 [c];
+ * out: fp16 NDHWC [d+2, h+1, w+1, c] = two leading zero frames, then
+ * fp16(residual + (x + bias)) (fp32 adds, one rounding) with one reflected row/column at the
+ * bottom/right (index h -> h-2, w -> w-2).  c % 8 == 0, h, w >= 2, 16-byte aligned buffers.
+ * Replaces residual_downsample_pack / _residual_pack (opt/encoder_fused_residual_pack.py:12-55). */
+int h3v_residual_downsample_pack(const uint16_t* x, const uint16_t* residual, const uint16_t* bias, uint16_t* out,
+                                 int c, int d, int h, int w, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -53,6 +53,7 @@ _SIGNATURES = {
     "ora_rms_fp16": (None, [_P, _P, _F, _I64, _I, _P]),
     "ora_residual_layernorm": (None, [_P, _P, _P, _P, _P, _F, _I64, _I, _P]),
     "ora_qk_rope": (None, [_P, _P, _P, _I64, _I, _I, _I, _F, _P, _P]),
+    "ora_residual_downsample_pack": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
     "ora_tree_sumsq_w16": (_F, [_P, _I]),
     "ora_tree_sum_plain": (_F, [_P, _I]),
     "ora_num_threads": (_I, []),
@@ -319,6 +320,15 @@ def qk_rope(x, cos, sin, heads, eps):
     lib().ora_qk_rope(_ptr(x), _ptr(_f16(cos)), _ptr(_f16(sin)), tokens, heads, dh, rot,
                       float(eps), _ptr(q), _ptr(k))
     return q, k
+
+
+def residual_downsample_pack(x_ndhwc, residual_ndhwc, bias):
+    """E9 pack: fp16 NDHWC [D,H,W,C] x2 + bias [C] -> fp16 [D+2, H+1, W+1, C]."""
+    x = _f16(x_ndhwc)
+    d, h, w, c = x.shape
+    out = np.empty((d + 2, h + 1, w + 1, c), np.float16)
+    lib().ora_residual_downsample_pack(_ptr(x), _ptr(_f16(residual_ndhwc)), _ptr(_f16(bias)), _ptr(out), c, d, h, w)
+    return out
 
 
 __all__ = [name for name in dir() if not name.startswith("_")]

@@ -653,6 +653,35 @@ API void ora_qk_rope(const uint16_t* x, const uint16_t* cosv, const uint16_t* si
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* E9 residual + bias pack before the stage-1 downsample conv                */
+/* (opt/encoder_fused_residual_pack.py:12-55, _residual_pack :12-33)         */
+/* ------------------------------------------------------------------------ */
+
+/* x, r: fp16 NDHWC [d, h, w, c]; bias fp16 [c]; out fp16 [d+2, h+1, w+1, c].
+ * Two leading zero frames; the extra bottom row / right column reflect
+ * (index h -> h-2, w -> w-2, :25-26); y = fp32 r + (fp32 x + fp32 b), one
+ * fp16 rounding at the store (:31-32). */
+API void ora_residual_downsample_pack(const uint16_t* x, const uint16_t* r, const uint16_t* bias, uint16_t* out,
+                                      int c, int d, int h, int w) {
+    const int64_t ho = h + 1, wo = w + 1;
+    for (int64_t t2 = 0; t2 < d + 2; ++t2)
+        for (int64_t y = 0; y < ho; ++y)
+            for (int64_t xw = 0; xw < wo; ++xw) {
+                uint16_t* dst = out + ((t2 * ho + y) * wo + xw) * c;
+                if (t2 < 2) {
+                    memset(dst, 0, sizeof(uint16_t) * (size_t)c);
+                    continue;
+                }
+                const int64_t t = t2 - 2;
+                const int64_t hs = y == h ? h - 2 : y;
+                const int64_t ws = xw == w ? w - 2 : xw;
+                const int64_t src = ((t * h + hs) * w + ws) * c;
+                for (int ch = 0; ch < c; ++ch)
+                    dst[ch] = ora_f2h(hf(r[src + ch]) + (hf(x[src + ch]) + hf(bias[ch])));
+            }
+}
+
 API int ora_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

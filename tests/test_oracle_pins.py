@@ -356,3 +356,33 @@ def test_qk_rope_closed_forms(oracle):
     want[..., :24] = -q0[..., 24:48]
     want[..., 24:48] = q0[..., :24]
     assert np.array_equal(q_rot[0].astype(np.float32), want)
+
+
+# ---------------------------------------------------------------------------
+# E9 residual + bias downsample pack (opt/encoder_fused_residual_pack.py:12-33)
+# ---------------------------------------------------------------------------
+
+def test_residual_pack_layout_and_exact_sums(oracle):
+    d, h, w, c = 3, 5, 4, 16
+    # small integers: every sum is exact in fp16, so the values pin the index mapping alone
+    x = RNG.integers(-8, 8, size=(d, h, w, c)).astype(np.float16)
+    r = RNG.integers(-8, 8, size=(d, h, w, c)).astype(np.float16)
+    b = RNG.integers(-4, 4, size=(c,)).astype(np.float16)
+    y = oracle.residual_downsample_pack(x, r, b)
+    assert y.shape == (d + 2, h + 1, w + 1, c)
+    assert not y[:2].any()                                        # two causal zero frames
+    body = (x.astype(np.float64) + r + b).astype(np.float16)
+    assert np.array_equal(y[2:, :h, :w], body)
+    assert np.array_equal(y[2:, h, :w], body[:, h - 2])           # bottom row reflects row h-2
+    assert np.array_equal(y[2:, :h, w], body[:, :, w - 2])        # right column reflects column w-2
+    assert np.array_equal(y[2:, h, w], body[:, h - 2, w - 2])
+
+
+def test_residual_pack_single_fp16_rounding(oracle):
+    # x + b + r = 1 + 2^-11 + 2^-11 = 1 + 2^-10 exactly in fp32.  One rounding at the store keeps it;
+    # rounding x + b to fp16 first (a tie, to even = 1.0) would give 1.0.
+    x = np.full((1, 2, 2, 8), 1.0, np.float16)
+    r = np.full((1, 2, 2, 8), 2.0 ** -11, np.float16)
+    b = np.full((8,), 2.0 ** -11, np.float16)
+    y = oracle.residual_downsample_pack(x, r, b)
+    assert (y[2:] == np.float16(1.0 + 2.0 ** -10)).all()
