@@ -14,3 +14,7 @@ __version__ = "0.1.0"
 # Same process-wide defaults as the reference plugin entry (__init__.py:23-24).
 os.environ.setdefault("MINIMAX_H3_TORCH_SDPA_BACKEND", "auto")
 os.environ.setdefault("MINIMAX_H3_VAE_DECODER_VIT_FP32_NORM", "1")
+
+from .h3vae_nodes import NODE_CLASS_MAPPINGS, NODE_DISPLAY_NAME_MAPPINGS  # noqa: E402
+
+__all__ = ["NODE_CLASS_MAPPINGS", "NODE_DISPLAY_NAME_MAPPINGS"]
