@@ -12,10 +12,13 @@
 // per-row and a per-k term.  With C a multiple of the K tile every K tile is one
 // tap and a contiguous channel slice.
 //
-// Tiling: BM x BN x 64 workgroup tile of 8 waves (2 per SIMD), each owning a
+// Tiling: BM x BN x BK workgroup tile of 8 waves (2 per SIMD), each owning a
 // 128 x 64 block built from v_mfma_i32_32x32x32_i8.  Operands stream
-// global -> LDS with LDS-DMA (global_load_lds_dwordx4) into a 4-stage ring,
-// three K steps ahead of the MFMAs; one barrier per K step.  LDS rows are
+// global -> LDS with LDS-DMA (global_load_lds_dwordx4) into an NS-stage ring
+// issued NS-1 K steps ahead of the MFMAs; one barrier per K step.  BK = 128 is
+// the default: every row segment a K step fetches is then one whole 128-byte
+// cache line (64-byte segments use half of each line fetched into L1 and
+// halve the L2 -> LDS rate, measured 28 vs 63 B/clk/CU).  LDS rows are
 // XOR-swizzled in 16-byte chunks so fragment reads are bank-conflict free.
 // Workgroup ids are remapped so that each XCD (own L2) walks a contiguous,
 // M-grouped range of tiles.
@@ -44,6 +47,8 @@ struct GemmParams {
     void* out;
     int64_t ldo;
     int tiles_m, tiles_n;
+    int vec_epi;       // sw (and bias) aligned for 4-column vector loads (and N % 4 == 0 for SwiGLU)
+    int vec_out;       // fp16 output 16-byte aligned with ldo % 8 == 0: 16-byte row stores
 };
 
 constexpr int kXcds = 8;
@@ -112,18 +117,50 @@ __device__ __forceinline__ float g1_value(int32_t acc, float sx, float sw, const
     return bias ? __builtin_fmaf(v, sw, h2f(bias[col])) : v * sw;
 }
 
+// The same epilogue with the weight scale and bias already in registers.
+__device__ __forceinline__ float g1_reg(int32_t acc, float sx, float sw, bool has_bias, uint16_t b) {
+    float v = (float)acc * sx;
+    return has_bias ? __builtin_fmaf(v, sw, h2f(b)) : v * sw;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Weight scales and fp16 bias of 4 consecutive weight rows c..c+3: one 16-byte
+// and one 8-byte load when aligned and in range, else clamped scalar loads.
+__device__ __forceinline__ void load_col4(const GemmParams& p, int c, int limit, f32x4& sw, u16x4& b) {
+    if (p.vec_epi && c + 4 <= limit) {
+        sw = *reinterpret_cast<const f32x4*>(p.sw + c);
+        if (p.bias) b = *reinterpret_cast<const u16x4*>(p.bias + c);
+        else b = u16x4{0, 0, 0, 0};
+        return;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int ce = c + e < limit ? c + e : limit - 1;
+        sw[e] = p.sw[ce];
+        b[e] = p.bias ? p.bias[ce] : 0;
+    }
+}
+
 // LDS-DMA helpers.  global_load_lds_dwordx4 writes lane i's 16 bytes to
-// M0 + 16*i, so one wave instruction fills 1 KB of LDS contiguously: 16 tile
-// rows of 64 bytes.  Lane i loads row i/4 and puts its 16-byte chunk in slot
-// i%4; the chunk it fetches is slot ^ swz(row) so that slot s of row r holds
-// k-chunk s ^ swz(r).  swz(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1) (bits 1-3 of the
-// row, so it is the same for a row's DMA lane and its reader) makes the 16-byte
-// fragment reads conflict free both for 8-lane groups on 32 banks and for
-// 16-lane groups on 64 banks (rows r, r+4, r+8, r+12 get distinct slots).
+// M0 + 16*i, so one wave instruction fills 1 KB of LDS contiguously: 1024/BK
+// tile rows of BK bytes.  Lane i loads row i/(BK/16) and puts its 16-byte chunk
+// in slot i%(BK/16); the chunk it fetches is slot ^ swz(row), so slot s of row
+// r holds k-chunk s ^ swz(r), with r the row's index in the tile (the same for
+// the DMA lane and the fragment reader).  The swizzles make the 16-byte
+// fragment reads (lane l: row l%32 of a 32-row block, chunk l/32 + 2*ks)
+// conflict free both for 8-lane groups on 32 banks and for 16-lane groups on
+// 64 banks:
+//   BK = 64:  swz(r) = ((r >> 1) & 3) ^ ((r >> 3) & 1)
+//   BK = 128: swz(r) = ((r >> 1) & 7) ^ ((r & 1) << 2)
 typedef __attribute__((address_space(3))) void* lds_void_t;
 typedef const __attribute__((address_space(1))) void* gbl_void_t;
 
-__device__ __forceinline__ int swz(int row) { return ((row >> 1) & 3) ^ ((row >> 3) & 1); }
+template <int BK>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (BK == 64) return ((row >> 1) & 3) ^ ((row >> 3) & 1);
+    else return ((row >> 1) & 7) ^ ((row & 1) << 2);
+}
 
 __device__ __forceinline__ void lds_dma16(const void* g, void* lds) {
     __builtin_amdgcn_global_load_lds((gbl_void_t)g, (lds_void_t)lds, 16, 0, 0);
@@ -154,20 +191,23 @@ __device__ __forceinline__ void wait_stage(int ahead) {
     else wait_vmcnt<0>();
 }
 
-// BM x BN x 64 workgroup tile, WGM x WGN waves of (BM/WGM) x (BN/WGN), NS-stage
-// LDS ring filled by LDS-DMA loads issued up to NS K steps ahead of the MFMAs.
-template <int BM, int BN, int WGM, int WGN, int NS, AMode AM, Epi EP>
+// BM x BN x BK workgroup tile, WGM x WGN waves of (BM/WGM) x (BN/WGN), NS-stage
+// LDS ring filled by LDS-DMA loads issued up to NS-1 K steps ahead of the MFMAs.
+template <int BM, int BN, int BK, int WGM, int WGN, int NS, AMode AM, Epi EP>
 __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
-    constexpr int BK = 64;
+    static_assert(BK == 64 || BK == 128, "K step");
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int KS = BK / 32;                               // MFMA K sub-steps per K step
+    constexpr int RPI = 1024 / BK;                            // tile rows per DMA instruction
+    constexpr int LPR = BK / 16;                              // DMA lanes per tile row
     constexpr int A_BYTES = BM * BK, STAGE = (BM + BN) * BK;
-    constexpr int A_PW = BM / 16 / NW, B_PW = BN / 16 / NW;   // 16-row groups per wave
+    constexpr int A_PW = BM / RPI / NW, B_PW = BN / RPI / NW; // row groups per wave
     constexpr int LPS = A_PW + B_PW;                          // DMA instructions per stage per wave
-    static_assert(A_PW * 16 * NW == BM && B_PW * 16 * NW == BN, "tile rows must split into 16-row groups per wave");
+    static_assert(A_PW * RPI * NW == BM && B_PW * RPI * NW == BN, "tile rows must split into row groups per wave");
     static_assert(EP != Epi::SwiGLU || (WN % 64) == 0, "SwiGLU pairs need 64-column wave tiles");
-    static_assert(NS >= 2 && NS <= 4, "LDS ring depth");
+    static_assert(NS >= 2 && NS <= 4 && (NS - 1) * LPS < 64, "LDS ring depth");
 
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
@@ -180,20 +220,21 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     grouped_tile(xcd_remap(blockIdx.x, gridDim.x), p.tiles_m, p.tiles_n, 8, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
 
-    const int lrow = lane >> 2;
-    const int gchunk = ((lane & 3) ^ swz(lrow)) * 16;
+    const int lrow = lane / LPR;
+    const int lslot = lane % LPR;
 
     int64_t aoff[A_PW];
 #pragma unroll
     for (int j = 0; j < A_PW; ++j) {
-        int m = m0 + (wave * A_PW + j) * 16 + lrow;
+        const int r = (wave * A_PW + j) * RPI + lrow;
+        int m = m0 + r;
         m = m < p.M ? m : p.M - 1;
-        aoff[j] = (AM == AMode::Gemm ? (int64_t)m * p.lda : conv_row_offset(p, m)) + gchunk;
+        aoff[j] = (AM == AMode::Gemm ? (int64_t)m * p.lda : conv_row_offset(p, m)) + ((lslot ^ swz<BK>(r)) << 4);
     }
     const int8_t* bptr[B_PW];
 #pragma unroll
     for (int j = 0; j < B_PW; ++j) {
-        int r = (wave * B_PW + j) * 16 + lrow;
+        int r = (wave * B_PW + j) * RPI + lrow;
         int wrow;
         if constexpr (EP == Epi::SwiGLU) {
             // tile row r -> pair r/64, half (r/32)&1 (0 gate, 1 up), column r&31
@@ -204,7 +245,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
             int n = n0 + r;
             wrow = n < p.N ? n : p.N - 1;
         }
-        bptr[j] = p.b + (int64_t)wrow * p.K + gchunk;
+        bptr[j] = p.b + (int64_t)wrow * p.K + ((lslot ^ swz<BK>(r)) << 4);
     }
 
     const int kb0 = (AM == AMode::Conv) ? conv_first_kblock(p, m0, BM, BK) : 0;
@@ -228,7 +269,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
 
     // fragment addressing: lane reads row (lane & 31) of a 32-row block, 16-byte
-    // k-chunk (lane >> 5) + 2*ks of the 64-byte K step
+    // k-chunk (lane >> 5) + 2*ks of the K step
     const int frow = lane & 31;
     const int fhi = lane >> 5;
     auto load_frags = [&](int it, int ks, v4i (&af)[FM], v4i (&bf)[FN]) {
@@ -238,12 +279,12 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int r = wm * WM + i * 32 + frow;
-            af[i] = *reinterpret_cast<const v4i*>(sa + r * BK + ((kc ^ swz(r)) << 4));
+            af[i] = *reinterpret_cast<const v4i*>(sa + r * BK + ((kc ^ swz<BK>(r)) << 4));
         }
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
             const int r = wn * WN + j * 32 + frow;
-            bf[j] = *reinterpret_cast<const v4i*>(sb + r * BK + ((kc ^ swz(r)) << 4));
+            bf[j] = *reinterpret_cast<const v4i*>(sb + r * BK + ((kc ^ swz<BK>(r)) << 4));
         }
     };
     auto mfma_all = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
@@ -258,125 +299,164 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
 #pragma unroll
     for (int s = 0; s < NS; ++s)
         if (s < nk) issue(s);
-    v4i a0[FM], b0[FN], a1[FM], b1[FN];
+    v4i fa[2][FM], fb[2][FN];
     if (nk > 0) {
         wait_stage<LPS>(nk - 1 < NS - 1 ? nk - 1 : NS - 1);
         lds_barrier();
-        load_frags(0, 0, a0, b0);
+        load_frags(0, 0, fa[0], fb[0]);
     }
-    // Per K step: MFMA the first half while reading the second half's fragments,
-    // then (behind the barrier that publishes the next stage) refill the freed
-    // ring slot and MFMA the second half while reading the next step's first
-    // half.  sched_group_barrier interleaves 2 MFMAs with 1 LDS read so the
-    // reads hide under the matrix pipeline.
+    // Per K step, KS sub-steps of 32: MFMA sub-step ks while reading the
+    // fragments of ks+1 into the other register buffer.  Before the last
+    // sub-step the barrier publishes the next stage and the freed ring slot is
+    // refilled; the last sub-step's MFMAs then hide the reads of the next K
+    // step's first fragments.  sched_group_barrier interleaves the MFMAs with
+    // the LDS reads so the reads hide under the matrix pipeline.
     constexpr int NFRAG = FM + FN;
     constexpr int NMFMA = FM * FN;
+    static_assert(KS % 2 == 0, "fragment double buffer parity");
     for (int it = 0; it < nk; ++it) {
-        mfma_all(a0, b0);
-        load_frags(it, 1, a1, b1);
 #pragma unroll
-        for (int g = 0; g < NFRAG; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NFRAG, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const bool more = it + 1 < nk;
-        if (more) {
-            wait_stage<LPS>(nk - 2 - it < NS - 2 ? nk - 2 - it : NS - 2);
-            lds_barrier();
-            if (it + NS < nk) issue(it + NS);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_all(a1, b1);
-        // on the last step this re-reads a stale slot; the values are never used
-        load_frags(more ? it + 1 : it, 0, a0, b0);
+        for (int ks = 0; ks < KS; ++ks) {
+            const int cur = ks & 1;
+            if (ks == KS - 1) {
+                const bool more = it + 1 < nk;
+                if (more) {
+                    wait_stage<LPS>(nk - 2 - it < NS - 2 ? nk - 2 - it : NS - 2);
+                    lds_barrier();
+                    if (it + NS < nk) issue(it + NS);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_all(fa[cur], fb[cur]);
+                // on the last step this re-reads a stale slot; the values are never used
+                load_frags(more ? it + 1 : it, 0, fa[cur ^ 1], fb[cur ^ 1]);
+            } else {
+                mfma_all(fa[cur], fb[cur]);
+                load_frags(it, ks + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            }
 #pragma unroll
-        for (int g = 0; g < NFRAG; ++g) {
-            __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NFRAG, 0);
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            for (int g = 0; g < NFRAG; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NFRAG, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __builtin_amdgcn_sched_barrier(0);
     }
 
     // Epilogue.  The MFMAs compute W * A^T blocks, so in the v_mfma 32x32 result
     // layout lane l holds output row m = lane&31 of the block and, in register
     // r, output column n = (r/4)*8 + (l/32)*4 + r%4: four consecutive columns per
-    // register quad, stored as one 8-byte (fp16) or 16-byte (int32) vector.
+    // register quad.
     const int mrow = lane & 31;
     const int ncol = (lane >> 5) * 4;
-    if constexpr (EP == Epi::SwiGLU) {
-        uint16_t* out = static_cast<uint16_t*>(p.out);
+    if constexpr (EP == Epi::Int32) {
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int row = m0 + wm * WM + i * 32 + mrow;
-            if (row >= p.M) continue;
-            const float sx = p.sx[(int64_t)row * p.sx_stride];
+        for (int j = 0; j < FN; ++j) {
 #pragma unroll
-            for (int j = 0; j < FN / 2; ++j) {
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int c0 = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
+                if (c0 >= p.N) continue;
+                const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const int c0 = tn * (BN / 2) + (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
-                    if (c0 >= p.N) continue;
-                    u16x4 v;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int c = c0 + e < p.N ? c0 + e : p.N - 1;
-                        float g = rt16(g1_value(acc[i][2 * j][q4 * 4 + e], sx, p.sw[c], p.bias, c));
-                        float u = rt16(g1_value(acc[i][2 * j + 1][q4 * 4 + e], sx, p.sw[p.N + c], p.bias, p.N + c));
-                        v[e] = f2h(silu(g) * u);
-                    }
-                    uint16_t* dst = out + (int64_t)row * p.ldo + c0;
-                    if (c0 + 4 <= p.N && (p.ldo & 3) == 0) {
-                        *reinterpret_cast<u16x4*>(dst) = v;
+                for (int i = 0; i < FM; ++i) {
+                    const int row = m0 + wm * WM + i * 32 + mrow;
+                    if (row >= p.M) continue;
+                    int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
+                    if (full) {
+                        v4i v = {acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
+                        *reinterpret_cast<v4i*>(dst) = v;
                     } else {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            if (c0 + e < p.N) dst[e] = v[e];
+                            if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
                     }
                 }
             }
         }
     } else {
+        // fp16 outputs go through LDS: each wave converts its block into the
+        // (now idle) LDS ring, laid out as the workgroup's output tile
+        // [BM][OUTW] with 16-byte chunks XOR-swizzled by row, and then every
+        // thread stores 16-byte pieces of whole tile rows, so each store
+        // instruction writes complete 128-byte lines (direct 8-byte stores from
+        // the MFMA layout touch 32 partial lines per instruction and cost about
+        // a third of the kernel).
+        constexpr int OUTW = (EP == Epi::SwiGLU) ? BN / 2 : BN;
+        constexpr int RCH = OUTW / 8;
+        constexpr int SWM = (RCH < 32 ? RCH : 32) - 1;
+        static_assert(RCH >= 8 && BM * OUTW * 2 <= NS * STAGE, "output tile must fit the LDS ring");
+        int8_t* ep = smem;
+        auto put = [&](int r, int c, const u16x4& v) {   // c: tile column, a multiple of 4
+            const int ch = c >> 3;
+            *reinterpret_cast<u16x4*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4) + ((c & 4) << 1)) = v;
+        };
+        const bool has_bias = p.bias != nullptr;
+        float sxr[FM];
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int row = m0 + wm * WM + i * 32 + mrow;
-            if (row >= p.M) continue;
-            float sx = 0.0f;
-            if constexpr (EP == Epi::Dequant) sx = p.sx[(int64_t)row * p.sx_stride];
+            sxr[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
+        }
+        lds_barrier();   // every wave has finished reading operand fragments
+        if constexpr (EP == Epi::SwiGLU) {
+#pragma unroll
+            for (int j = 0; j < FN / 2; ++j) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int tc = (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
+                    const int c0 = tn * (BN / 2) + tc;
+                    f32x4 swg, swu;
+                    u16x4 bg, bu;
+                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swg, bg);
+                    load_col4(p, p.N + (c0 < p.N ? c0 : p.N - 1), 2 * p.N, swu, bu);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        u16x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float g = rt16(g1_reg(acc[i][2 * j][q4 * 4 + e], sxr[i], swg[e], has_bias, bg[e]));
+                            float u = rt16(g1_reg(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], swu[e], has_bias, bu[e]));
+                            v[e] = f2h(silu(g) * u);
+                        }
+                        put(wm * WM + i * 32 + mrow, tc, v);
+                    }
+                }
+            }
+        } else {
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
-                    const int c0 = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
-                    if (c0 >= p.N) continue;
-                    const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
-                    if constexpr (EP == Epi::Int32) {
-                        int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
-                        if (full) {
-                            v4i v = {acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
-                            *reinterpret_cast<v4i*>(dst) = v;
-                        } else {
+                    const int tc = wn * WN + j * 32 + q4 * 8 + ncol;
+                    const int c0 = n0 + tc;
+                    f32x4 swv;
+                    u16x4 bv;
+                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swv, bv);
 #pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
-                        }
-                    } else {
+                    for (int i = 0; i < FM; ++i) {
                         u16x4 v;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const int c = c0 + e < p.N ? c0 + e : p.N - 1;
-                            v[e] = f2h(g1_value(acc[i][j][q4 * 4 + e], sx, p.sw[c], p.bias, c));
-                        }
-                        uint16_t* dst = static_cast<uint16_t*>(p.out) + (int64_t)row * p.ldo + c0;
-                        if (full) {
-                            *reinterpret_cast<u16x4*>(dst) = v;
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                if (c0 + e < p.N) dst[e] = v[e];
-                        }
+                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg(acc[i][j][q4 * 4 + e], sxr[i], swv[e], has_bias, bv[e]));
+                        put(wm * WM + i * 32 + mrow, tc, v);
                     }
                 }
+            }
+        }
+        lds_barrier();   // the output tile is complete in LDS
+        const int gcol0 = (EP == Epi::SwiGLU) ? tn * (BN / 2) : n0;
+        uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll 4
+        for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
+            const int r = idx / RCH, ch = idx - r * RCH;
+            const int grow = m0 + r, gcol = gcol0 + ch * 8;
+            if (grow >= p.M || gcol >= p.N) continue;
+            const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
+            uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+            if (p.vec_out && gcol + 8 <= p.N) {
+                *reinterpret_cast<u16x8*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gcol + e < p.N) dst[e] = v[e];
             }
         }
     }
@@ -421,18 +501,19 @@ __global__ __launch_bounds__(256) void gemm_i8_generic(GemmParams p) {
     }
 }
 
-constexpr int kBK = 64;
-
-template <int BM, int BN, int WGM, int WGN, int NS, AMode AM, Epi EP>
+template <int BM, int BN, int BK, int WGM, int WGN, int NS, AMode AM, Epi EP>
 int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     int ncols = (EP == Epi::SwiGLU) ? 2 * p.N : p.N;
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (ncols + BN - 1) / BN;
+    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) &&
+                (EP != Epi::SwiGLU || p.N % 4 == 0);
+    p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
     int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
     if (grid > 0x7fffffff) return fail(H3V_EINVAL, "%s: too many tiles", what);
-    const size_t lds = (size_t)NS * (BM + BN) * kBK;   // LDS ring (at most 160 KB on gfx950)
-    static_assert((size_t)NS * (BM + BN) * kBK <= 163840, "LDS ring exceeds 160 KB");
-    auto kernel = &gemm_i8_mfma<BM, BN, WGM, WGN, NS, AM, EP>;
+    const size_t lds = (size_t)NS * (BM + BN) * BK;   // LDS ring (at most 160 KB on gfx950)
+    static_assert((size_t)NS * (BM + BN) * BK <= 163840, "LDS ring exceeds 160 KB");
+    auto kernel = &gemm_i8_mfma<BM, BN, BK, WGM, WGN, NS, AM, EP>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, lds,
@@ -452,20 +533,25 @@ int launch_generic(GemmParams p, hipStream_t stream, const char* what) {
 
 template <Epi EP>
 int run_gemm(GemmParams p, hipStream_t stream, const char* what) {
-    bool tiled = p.K % kBK == 0 && p.lda % 16 == 0 && aligned(p.a, 16) && aligned(p.b, 16);
-    if (!tiled) return launch_generic<AMode::Gemm, EP>(p, stream, what);
-    return launch_tiled<256, 256, 2, 4, 4, AMode::Gemm, EP>(p, stream, what);
+    const bool al = p.lda % 16 == 0 && aligned(p.a, 16) && aligned(p.b, 16);
+    if (al && p.K % 128 == 0) return launch_tiled<256, 256, 128, 2, 4, 2, AMode::Gemm, EP>(p, stream, what);
+    if (al && p.K % 64 == 0) return launch_tiled<256, 256, 64, 2, 4, 4, AMode::Gemm, EP>(p, stream, what);
+    return launch_generic<AMode::Gemm, EP>(p, stream, what);
 }
 
 template <Epi EP>
 int run_conv(GemmParams p, hipStream_t stream, const char* what) {
-    bool tiled = p.C % kBK == 0 && aligned(p.a, 16) && aligned(p.b, 16);
-    if (!tiled) {
-        p.causal_skip = 0;  // the generic path always runs the full reduction
-        return launch_generic<AMode::Conv, EP>(p, stream, what);
+    const bool al = aligned(p.a, 16) && aligned(p.b, 16);
+    if (al && p.C % 128 == 0) {
+        if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, AMode::Conv, EP>(p, stream, what);
+        return launch_tiled<256, 256, 128, 2, 4, 2, AMode::Conv, EP>(p, stream, what);
     }
-    if (p.N <= 128) return launch_tiled<512, 128, 4, 2, 4, AMode::Conv, EP>(p, stream, what);
-    return launch_tiled<256, 256, 2, 4, 4, AMode::Conv, EP>(p, stream, what);
+    if (al && p.C % 64 == 0) {
+        if (p.N <= 128) return launch_tiled<512, 128, 64, 4, 2, 4, AMode::Conv, EP>(p, stream, what);
+        return launch_tiled<256, 256, 64, 2, 4, 4, AMode::Conv, EP>(p, stream, what);
+    }
+    p.causal_skip = 0;  // the generic path always runs the full reduction
+    return launch_generic<AMode::Conv, EP>(p, stream, what);
 }
 
 int check_gemm_dims(const char* what, int64_t m, int64_t n, int64_t k) {
