@@ -14,8 +14,10 @@
 //
 // Tiling: BM x BN x BK workgroup tile of 8 waves (2 per SIMD), each owning a
 // 128 x 64 block built from v_mfma_i32_32x32x32_i8.  Operands stream
-// global -> LDS with LDS-DMA (global_load_lds_dwordx4) into an NS-stage ring
-// issued NS-1 K steps ahead of the MFMAs; one barrier per K step.  BK = 128 is
+// global -> LDS with LDS-DMA (global_load_lds_dwordx4) into an NSA-slot A ring
+// and an NSB-slot B ring, issued NSA-1 / NSB-1 K steps ahead of the MFMAs; one
+// barrier per K step.  The activation operand A misses L2 more often than the
+// weights, so it gets the deeper ring when the LDS allows.  BK = 128 is
 // the default: every row segment a K step fetches is then one whole 128-byte
 // cache line (64-byte segments use half of each line fetched into L1 and
 // halve the L2 -> LDS rate, measured 28 vs 63 B/clk/CU).  LDS rows are
@@ -191,9 +193,12 @@ __device__ __forceinline__ void wait_stage(int ahead) {
     else wait_vmcnt<0>();
 }
 
-// BM x BN x BK workgroup tile, WGM x WGN waves of (BM/WGM) x (BN/WGN), NS-stage
-// LDS ring filled by LDS-DMA loads issued up to NS-1 K steps ahead of the MFMAs.
-template <int BM, int BN, int BK, int WGM, int WGN, int NS, AMode AM, Epi EP>
+// BM x BN x BK workgroup tile, WGM x WGN waves of (BM/WGM) x (BN/WGN).  A and B
+// stream through separate LDS rings of NSA and NSB slots.  Loads are issued B
+// before A for each stage, so with NSB = 2 < NSA the barrier that publishes
+// stage it+1 can leave the newest A batch (stage it+NSA-1) in flight: vmcnt
+// counts loads in issue order.
+template <int BM, int BN, int BK, int WGM, int WGN, int NSA, int NSB, AMode AM, Epi EP>
 __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     static_assert(BK == 64 || BK == 128, "K step");
     constexpr int NW = WGM * WGN;
@@ -202,12 +207,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     constexpr int KS = BK / 32;                               // MFMA K sub-steps per K step
     constexpr int RPI = 1024 / BK;                            // tile rows per DMA instruction
     constexpr int LPR = BK / 16;                              // DMA lanes per tile row
-    constexpr int A_BYTES = BM * BK, STAGE = (BM + BN) * BK;
+    constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+    constexpr int B_RING = NSA * A_BYTES, RING = NSA * A_BYTES + NSB * B_BYTES;
     constexpr int A_PW = BM / RPI / NW, B_PW = BN / RPI / NW; // row groups per wave
     constexpr int LPS = A_PW + B_PW;                          // DMA instructions per stage per wave
     static_assert(A_PW * RPI * NW == BM && B_PW * RPI * NW == BN, "tile rows must split into row groups per wave");
     static_assert(EP != Epi::SwiGLU || (WN % 64) == 0, "SwiGLU pairs need 64-column wave tiles");
-    static_assert(NS >= 2 && NS <= 4 && (NS - 1) * LPS < 64, "LDS ring depth");
+    static_assert(NSA >= 2 && NSA <= 4 && NSB >= 2 && NSB <= NSA && (NSA == NSB || NSB == 2), "LDS ring depths");
+    static_assert((NSA - 1) * A_PW + (NSB - 1) * B_PW < 64, "outstanding DMA must fit vmcnt");
 
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
@@ -251,13 +258,44 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     const int kb0 = (AM == AMode::Conv) ? conv_first_kblock(p, m0, BM, BK) : 0;
     const int nk = p.K / BK - kb0;
 
-    auto issue = [&](int it) {
-        const int kb = kb0 + it;
-        int8_t* sa = smem + (it % NS) * STAGE;
-        int8_t* sb = sa + A_BYTES;
-        const int64_t koff = (AM == AMode::Gemm) ? (int64_t)kb * BK : conv_k_offset(p, kb * BK);
+    // A stages are issued strictly in order, so the conv's k offset is kept as a
+    // running (kd, kh, kw, c0) position advanced by BK per issue: no integer
+    // division in the loop.
+    int ck_kd = 0, ck_kh = 0, ck_kw = 0, ck_c0 = 0;
+    if constexpr (AM == AMode::Conv) {
+        const int k0 = kb0 * BK;
+        const int tap = k0 / p.C;
+        ck_c0 = k0 - tap * p.C;
+        ck_kd = tap / (p.KH * p.KW);
+        const int rem = tap - ck_kd * p.KH * p.KW;
+        ck_kh = rem / p.KW;
+        ck_kw = rem - ck_kh * p.KW;
+    }
+    auto issue_a = [&](int it) {
+        int8_t* sa = smem + (it % NSA) * A_BYTES;
+        int64_t koff;
+        if constexpr (AM == AMode::Gemm) {
+            koff = (int64_t)(kb0 + it) * BK;
+        } else {
+            koff = (((int64_t)ck_kd * p.Hp + ck_kh) * p.Wp + ck_kw) * p.C + ck_c0;
+            ck_c0 += BK;
+            if (ck_c0 == p.C) {
+                ck_c0 = 0;
+                if (++ck_kw == p.KW) {
+                    ck_kw = 0;
+                    if (++ck_kh == p.KH) {
+                        ck_kh = 0;
+                        ++ck_kd;
+                    }
+                }
+            }
+        }
 #pragma unroll
         for (int j = 0; j < A_PW; ++j) lds_dma16(p.a + aoff[j] + koff, sa + (wave * A_PW + j) * 1024);
+    };
+    auto issue_b = [&](int it) {
+        const int kb = kb0 + it;
+        int8_t* sb = smem + B_RING + (it % NSB) * B_BYTES;
 #pragma unroll
         for (int j = 0; j < B_PW; ++j) lds_dma16(bptr[j] + (int64_t)kb * BK, sb + (wave * B_PW + j) * 1024);
     };
@@ -273,8 +311,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     const int frow = lane & 31;
     const int fhi = lane >> 5;
     auto load_frags = [&](int it, int ks, v4i (&af)[FM], v4i (&bf)[FN]) {
-        const int8_t* sa = smem + (it % NS) * STAGE;
-        const int8_t* sb = sa + A_BYTES;
+        const int8_t* sa = smem + (it % NSA) * A_BYTES;
+        const int8_t* sb = smem + B_RING + (it % NSB) * B_BYTES;
         const int kc = fhi + 2 * ks;
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
@@ -295,13 +333,16 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
                 acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
     };
 
-    // Prologue: fill the whole ring, then wait for stage 0.
+    // Prologue: fill both rings (B before A per stage), then wait for stage 0.
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
-        if (s < nk) issue(s);
+    for (int s = 0; s < NSA; ++s) {
+        if (s < NSB && s < nk) issue_b(s);
+        if (s < nk) issue_a(s);
+    }
     v4i fa[2][FM], fb[2][FN];
     if (nk > 0) {
-        wait_stage<LPS>(nk - 1 < NS - 1 ? nk - 1 : NS - 1);
+        if (nk >= NSA) wait_vmcnt<(NSA - 1) * A_PW + (NSB - 1) * B_PW>();
+        else wait_vmcnt<0>();
         lds_barrier();
         load_frags(0, 0, fa[0], fb[0]);
     }
@@ -321,9 +362,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
             if (ks == KS - 1) {
                 const bool more = it + 1 < nk;
                 if (more) {
-                    wait_stage<LPS>(nk - 2 - it < NS - 2 ? nk - 2 - it : NS - 2);
+                    // stage it+1 must have landed; later loads may stay in flight
+                    if constexpr (NSA == NSB) {
+                        wait_stage<LPS>(nk - 2 - it < NSA - 2 ? nk - 2 - it : NSA - 2);
+                    } else {
+                        // the only load issued after B(it+1) is A(it+NSA-1)
+                        if (it + NSA - 1 < nk) wait_vmcnt<A_PW>();
+                        else wait_vmcnt<0>();
+                    }
                     lds_barrier();
-                    if (it + NS < nk) issue(it + NS);
+                    if (it + NSB < nk) issue_b(it + NSB);
+                    if (it + NSA < nk) issue_a(it + NSA);
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 mfma_all(fa[cur], fb[cur]);
@@ -383,7 +432,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         constexpr int OUTW = (EP == Epi::SwiGLU) ? BN / 2 : BN;
         constexpr int RCH = OUTW / 8;
         constexpr int SWM = (RCH < 32 ? RCH : 32) - 1;
-        static_assert(RCH >= 8 && BM * OUTW * 2 <= NS * STAGE, "output tile must fit the LDS ring");
+        static_assert(RCH >= 8 && BM * OUTW * 2 <= RING, "output tile must fit the LDS ring");
         int8_t* ep = smem;
         auto put = [&](int r, int c, const u16x4& v) {   // c: tile column, a multiple of 4
             const int ch = c >> 3;
@@ -501,7 +550,7 @@ __global__ __launch_bounds__(256) void gemm_i8_generic(GemmParams p) {
     }
 }
 
-template <int BM, int BN, int BK, int WGM, int WGN, int NS, AMode AM, Epi EP>
+template <int BM, int BN, int BK, int WGM, int WGN, int NSA, int NSB, AMode AM, Epi EP>
 int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     int ncols = (EP == Epi::SwiGLU) ? 2 * p.N : p.N;
     p.tiles_m = (p.M + BM - 1) / BM;
@@ -511,9 +560,10 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
     int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
     if (grid > 0x7fffffff) return fail(H3V_EINVAL, "%s: too many tiles", what);
-    const size_t lds = (size_t)NS * (BM + BN) * BK;   // LDS ring (at most 160 KB on gfx950)
-    static_assert((size_t)NS * (BM + BN) * BK <= 163840, "LDS ring exceeds 160 KB");
-    auto kernel = &gemm_i8_mfma<BM, BN, BK, WGM, WGN, NS, AM, EP>;
+    constexpr size_t kLds = (size_t)(NSA * BM + NSB * BN) * BK;   // LDS rings (at most 160 KB on gfx950)
+    static_assert(kLds <= 163840, "LDS rings exceed 160 KB");
+    const size_t lds = kLds;
+    auto kernel = &gemm_i8_mfma<BM, BN, BK, WGM, WGN, NSA, NSB, AM, EP>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, lds,
@@ -534,8 +584,8 @@ int launch_generic(GemmParams p, hipStream_t stream, const char* what) {
 template <Epi EP>
 int run_gemm(GemmParams p, hipStream_t stream, const char* what) {
     const bool al = p.lda % 16 == 0 && aligned(p.a, 16) && aligned(p.b, 16);
-    if (al && p.K % 128 == 0) return launch_tiled<256, 256, 128, 2, 4, 2, AMode::Gemm, EP>(p, stream, what);
-    if (al && p.K % 64 == 0) return launch_tiled<256, 256, 64, 2, 4, 4, AMode::Gemm, EP>(p, stream, what);
+    if (al && p.K % 128 == 0) return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Gemm, EP>(p, stream, what);
+    if (al && p.K % 64 == 0) return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Gemm, EP>(p, stream, what);
     return launch_generic<AMode::Gemm, EP>(p, stream, what);
 }
 
@@ -543,12 +593,12 @@ template <Epi EP>
 int run_conv(GemmParams p, hipStream_t stream, const char* what) {
     const bool al = aligned(p.a, 16) && aligned(p.b, 16);
     if (al && p.C % 128 == 0) {
-        if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, AMode::Conv, EP>(p, stream, what);
-        return launch_tiled<256, 256, 128, 2, 4, 2, AMode::Conv, EP>(p, stream, what);
+        if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, EP>(p, stream, what);
+        return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, EP>(p, stream, what);
     }
     if (al && p.C % 64 == 0) {
-        if (p.N <= 128) return launch_tiled<512, 128, 64, 4, 2, 4, AMode::Conv, EP>(p, stream, what);
-        return launch_tiled<256, 256, 64, 2, 4, 4, AMode::Conv, EP>(p, stream, what);
+        if (p.N <= 128) return launch_tiled<512, 128, 64, 4, 2, 4, 4, AMode::Conv, EP>(p, stream, what);
+        return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Conv, EP>(p, stream, what);
     }
     p.causal_skip = 0;  // the generic path always runs the full reduction
     return launch_generic<AMode::Conv, EP>(p, stream, what);

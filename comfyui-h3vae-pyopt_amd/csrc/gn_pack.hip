@@ -12,8 +12,17 @@
 //                 per (frame, channel) max and min of the (pre-biased) input
 //   gn_merge      grid D: Chan merge of the chunks -> (mean, rstd); absmax
 //                 candidate from the per-channel extremes (below)
-//   norm_pack<0>  full absmax pass, only when the candidate cannot be proven exact
-//   norm_pack<1>  every padded value -> int8 with the per-tensor scale; writes the scale
+//   norm_absmax   full absmax pass, only when the candidate cannot be proven exact
+//   build_lut     the int8 code of every fp16 pre-activation z under the final scale
+//   norm_pack_lut every padded value -> int8 through that table; writes the scale
+//
+// Quantize table.  After the normalisation rounds z to fp16, the rest of the
+// chain (SiLU, fp16 rounding, division by the tensor scale, half-away
+// rounding, clamp) is a fixed function of z's 16-bit code for one call, so it
+// is evaluated once per code (65536 entries, 64 KB) and each block looks the
+// codes up from LDS: no exp and no division per element.  Every entry is the
+// same scalar code path as the direct evaluation, so the output is bitwise
+// identical (NaN codes included).
 //
 // Absmax shortcut.  z = fp16(((v - mean) * rstd) * gamma + beta) is monotone in
 // v for each channel (every rounding step is monotone; the direction is the
@@ -90,8 +99,17 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     float pb[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) pb[e] = PRE_BIAS ? h2f(pre_bias[cv * 8 + e]) : 0.0f;
-    auto load = [&](int p, float* v) {
-        load8(base + (int64_t)p * C, v);
+    // The thread's whole slice of the chunk stays in registers for both passes:
+    // every load is issued up front and the data is read from memory once.
+    u16x8 xr[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const int p = pl + s * PL;
+        if (p < npix) xr[s] = *reinterpret_cast<const u16x8*>(base + (int64_t)p * C);
+    }
+    auto load = [&](int s, float* v) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = h2f(xr[s][e]);
         if constexpr (PRE_BIAS) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
@@ -103,11 +121,12 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     for (int gi = 0; gi < GPT; ++gi) ls[gi] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) { vmx[e] = -__builtin_inff(); vmn[e] = __builtin_inff(); }
+#pragma unroll
     for (int s = 0; s < STEPS; ++s) {
         int p = pl + s * PL;
         if (p >= npix) break;
         float v[8];
-        load(p, v);
+        load(s, v);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             vmx[e] = __builtin_fmaxf(vmx[e], v[e]);
@@ -148,11 +167,12 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     float a[GPT], lm[GPT];
 #pragma unroll
     for (int gi = 0; gi < GPT; ++gi) { a[gi] = avg_s[cv * GPT + gi]; lm[gi] = 0.0f; }
+#pragma unroll
     for (int s = 0; s < STEPS; ++s) {
         int p = pl + s * PL;
         if (p >= npix) break;
         float v[8];
-        load(p, v);
+        load(s, v);
 #pragma unroll
         for (int gi = 0; gi < GPT; ++gi) {
             float dv = v[gi * CG] - a[gi];
@@ -205,6 +225,8 @@ __global__ __launch_bounds__(kNT) void gn_merge(const float* __restrict__ part_a
         for (int i = tid; i < nb * kGroups; i += kNT) sa[i] = pa[(int64_t)j0 * kGroups + i];
         __syncthreads();
         if (tid < kGroups) {
+            // the sum is sequential in j; unrolling lets the LDS reads run ahead of it
+#pragma unroll 16
             for (int j = 0; j < nb; ++j) {
                 int jj = j0 + j;
                 int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
@@ -224,6 +246,7 @@ __global__ __launch_bounds__(kNT) void gn_merge(const float* __restrict__ part_a
         }
         __syncthreads();
         if (tid < kGroups) {
+#pragma unroll 16
             for (int j = 0; j < nb; ++j) {
                 int jj = j0 + j;
                 int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
@@ -265,25 +288,17 @@ __global__ __launch_bounds__(kNT) void gn_merge(const float* __restrict__ part_a
 
 __device__ __forceinline__ int reflect(int i, int n) { return i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i); }
 
-// PASS 0: absmax of all padded values (skipped when the candidate is exact).
-// PASS 1: int8 with the per-tensor scale.
-template <int C, bool PRE_BIAS, int PASS>
-__global__ __launch_bounds__(kNT) void norm_pack(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
-                                                 const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
-                                                 const float* __restrict__ stats, int d, int h, int w,
-                                                 uint32_t* __restrict__ amax_bits, int8_t* __restrict__ q,
-                                                 float* __restrict__ scale) {
+// Full absmax of all padded values; exits at once when the candidate is exact.
+template <int C, bool PRE_BIAS>
+__global__ __launch_bounds__(kNT) void norm_absmax(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
+                                                   const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+                                                   const float* __restrict__ stats, int d, int h, int w,
+                                                   uint32_t* __restrict__ amax_bits) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
+    if (__builtin_bit_cast(float, *amax_bits) >= kShortcutFloor) return;
     const int hp = h + 2, wp = w + 2;
     const int64_t nvec = (int64_t)(d + 2) * hp * wp * TPP;
-    float s = 0.0f;
-    if constexpr (PASS == 0) {
-        if (__builtin_bit_cast(float, *amax_bits) >= kShortcutFloor) return;
-    } else {
-        s = e3_scale(__builtin_bit_cast(float, *amax_bits));
-        if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
-    }
     float amax = 0.0f;
     const int64_t stride = (int64_t)gridDim.x * kNT;
     for (int64_t vi = (int64_t)blockIdx.x * kNT + threadIdx.x; vi < nvec; vi += stride) {
@@ -292,59 +307,134 @@ __global__ __launch_bounds__(kNT) void norm_pack(const uint16_t* __restrict__ x,
         const int jj = (int)(pix % wp);
         const int64_t r = pix / wp;
         const int ii = (int)(r % hp);
-        const int tp = (int)(r / hp);
-        const int t = tp - 2;
-        float z[8];
-        if (t >= 0) {
-            const int si = reflect(ii - 1, h), sj = reflect(jj - 1, w);
-            float v[8];
-            load8(x + (((int64_t)t * h + si) * w + sj) * C + cv * 8, v);
-            float gm[8], bt[8];
-            load8(gamma + cv * 8, gm);
-            load8(beta + cv * 8, bt);
-            if constexpr (PRE_BIAS) {
-                float pb[8];
-                load8(pre_bias + cv * 8, pb);
+        const int t = (int)(r / hp) - 2;
+        if (t < 0) continue;   // causal zero frames
+        const int si = reflect(ii - 1, h), sj = reflect(jj - 1, w);
+        float v[8], gm[8], bt[8];
+        load8(x + (((int64_t)t * h + si) * w + sj) * C + cv * 8, v);
+        load8(gamma + cv * 8, gm);
+        load8(beta + cv * 8, bt);
+        if constexpr (PRE_BIAS) {
+            float pb[8];
+            load8(pre_bias + cv * 8, pb);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int g = (cv * 8 + e) / CG;
-                const float mean = stats[(t * kGroups + g) * 2];
-                const float rstd = stats[(t * kGroups + g) * 2 + 1];
-                float zz = rt16(((v[e] - mean) * rstd) * gm[e] + bt[e]);
-                z[e] = rt16(silu(zz));
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) z[e] = 0.0f;
+            for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
         }
-        if constexpr (PASS == 0) {
 #pragma unroll
-            for (int e = 0; e < 8; ++e) amax = __builtin_fmaxf(amax, __builtin_fabsf(z[e]));
-        } else {
-            uint32_t lo = pack4(e3_quant(z[0], s), e3_quant(z[1], s), e3_quant(z[2], s), e3_quant(z[3], s));
-            uint32_t hi = pack4(e3_quant(z[4], s), e3_quant(z[5], s), e3_quant(z[6], s), e3_quant(z[7], s));
-            *reinterpret_cast<uint2*>(q + vi * 8) = make_uint2(lo, hi);
+        for (int e = 0; e < 8; ++e) {
+            const int g = (cv * 8 + e) / CG;
+            const float mean = stats[(t * kGroups + g) * 2];
+            const float rstd = stats[(t * kGroups + g) * 2 + 1];
+            const float zz = rt16(((v[e] - mean) * rstd) * gm[e] + bt[e]);
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(rt16(silu(zz))));
         }
     }
-    if constexpr (PASS == 0) {
-        __shared__ float red[kNT / 64];
-        amax = wave_max(amax);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float m = red[0];
-            for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
-            atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
-        }
+    __shared__ float red[kNT / 64];
+    amax = wave_max(amax);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float m = red[0];
+        for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
+        atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
     }
 }
 
+constexpr int kLutFloats = 65536 / 4;    // the int8 quantize table
+
 int64_t workspace_floats(int d, int h, int w) {
     int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
-    return 2 * (int64_t)d * nchunk * kGroups + 2 * (int64_t)d * kMaxC;
+    return 2 * (int64_t)d * nchunk * kGroups + 2 * (int64_t)d * kMaxC + kLutFloats;
+}
+
+// q code of every fp16 value z under the scale derived from the final absmax.
+__global__ __launch_bounds__(kNT) void build_lut(const uint32_t* __restrict__ amax_bits, int8_t* __restrict__ lut) {
+    const int code = blockIdx.x * kNT + threadIdx.x;
+    const float s = e3_scale(__builtin_bit_cast(float, *amax_bits));
+    lut[code] = (int8_t)e3_quant(rt16(silu(h2f((uint16_t)code))), s);
+}
+
+// PASS 1 through the table.  The grid stride is a multiple of C/8, so each
+// thread keeps one 8-channel slice (gamma, beta, pre-bias, groups) for the
+// whole loop; the (mean, rstd) pairs are reloaded when the frame changes.
+template <int C, bool PRE_BIAS>
+__global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ pre_bias,
+                                                     const uint16_t* __restrict__ gamma,
+                                                     const uint16_t* __restrict__ beta, const float* __restrict__ stats,
+                                                     int d, int h, int w, const uint32_t* __restrict__ amax_bits,
+                                                     const int8_t* __restrict__ lut_g, int8_t* __restrict__ q,
+                                                     float* __restrict__ scale) {
+    constexpr int CG = C / kGroups;
+    constexpr int TPP = C / 8;
+    constexpr int NG = 8 / CG > 1 ? 8 / CG : 1;    // groups touched by one 8-channel slice
+    __shared__ __attribute__((aligned(16))) int8_t lut[65536];
+    for (int i = threadIdx.x; i < 65536 / 16; i += kNT)
+        reinterpret_cast<u16x8*>(lut)[i] = reinterpret_cast<const u16x8*>(lut_g)[i];
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale = e3_scale(__builtin_bit_cast(float, *amax_bits));
+    __syncthreads();
+
+    const int hp = h + 2, wp = w + 2;
+    const int64_t nvec = (int64_t)(d + 2) * hp * wp * TPP;
+    const int64_t stride = (int64_t)gridDim.x * kNT;
+    const int64_t v0 = (int64_t)blockIdx.x * kNT + threadIdx.x;
+    const int cv = (int)(v0 % TPP);
+    float gm[8], bt[8], pb[8] = {};
+    load8(gamma + cv * 8, gm);
+    load8(beta + cv * 8, bt);
+    if constexpr (PRE_BIAS) load8(pre_bias + cv * 8, pb);
+    const int g0 = cv * 8 / CG;
+    int tcur = -1;
+    float mean[NG], rstd[NG];
+    // U independent vectors per iteration: their loads are all issued before
+    // any is used, so each lane keeps U 16-byte reads in flight (only 8 waves
+    // fit on a CU next to the 64 KB table).
+    constexpr int U = 4;
+    for (int64_t base = v0; base < nvec; base += U * stride) {
+        u16x8 xv[U];
+        int tt[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t vi = base + u * stride;
+            const int64_t pix = vi / TPP;
+            const int jj = (int)(pix % wp);
+            const int64_t r = pix / wp;
+            const int ii = (int)(r % hp);
+            tt[u] = (vi < nvec) ? (int)(r / hp) - 2 : -1;
+            if (tt[u] >= 0) {
+                const int si = reflect(ii - 1, h), sj = reflect(jj - 1, w);
+                xv[u] = *reinterpret_cast<const u16x8*>(x + (((int64_t)tt[u] * h + si) * w + sj) * C + cv * 8);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t vi = base + u * stride;
+            if (vi >= nvec) break;
+            const int t = tt[u];
+            uint32_t lo = 0, hi = 0;
+            if (t >= 0) {
+                if (t != tcur) {
+                    tcur = t;
+#pragma unroll
+                    for (int k = 0; k < NG; ++k) {
+                        mean[k] = stats[(t * kGroups + g0 + k) * 2];
+                        rstd[k] = stats[(t * kGroups + g0 + k) * 2 + 1];
+                    }
+                }
+                int code[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    float ve = h2f(xv[u][e]);
+                    if constexpr (PRE_BIAS) ve = rt16(ve + pb[e]);
+                    const int k = (NG > 1) ? e / CG : 0;
+                    code[e] = f2h(((ve - mean[k]) * rstd[k]) * gm[e] + bt[e]);
+                }
+                lo = pack4(lut[code[0]], lut[code[1]], lut[code[2]], lut[code[3]]);
+                hi = pack4(lut[code[4]], lut[code[5]], lut[code[6]], lut[code[7]]);
+            }
+            *reinterpret_cast<uint2*>(q + vi * 8) = make_uint2(lo, hi);
+        }
+    }
 }
 
 template <int C, bool PB>
@@ -357,6 +447,7 @@ void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
     float* part_m2 = ws + (int64_t)d * nchunk * kGroups;
     uint32_t* vmax = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups);
     uint32_t* vmin = vmax + (int64_t)d * kMaxC;
+    int8_t* lut = reinterpret_cast<int8_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + 2 * (int64_t)d * kMaxC);
     hipLaunchKernelGGL(gn_init, dim3((d * C + kNT - 1) / kNT), dim3(kNT), 0, stream, vmax, vmin, d * C, amax_bits);
     hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
                        part_m2, vmax, vmin);
@@ -365,10 +456,13 @@ void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
     const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
     int64_t want = (nvec + kNT - 1) / kNT;
     unsigned blocks = (unsigned)(want > 16384 ? 16384 : want);
-    hipLaunchKernelGGL((norm_pack<C, PB, 0>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
-                       w, amax_bits, q, scale);
-    hipLaunchKernelGGL((norm_pack<C, PB, 1>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
-                       w, amax_bits, q, scale);
+    hipLaunchKernelGGL((norm_absmax<C, PB>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
+                       w, amax_bits);
+    hipLaunchKernelGGL(build_lut, dim3(65536 / kNT), dim3(kNT), 0, stream, amax_bits, lut);
+    // 64 KB of LDS per block: two blocks per CU; each block walks many vectors
+    unsigned lut_blocks = (unsigned)(want > 512 ? 512 : want);
+    hipLaunchKernelGGL((norm_pack_lut<C, PB>), dim3(lut_blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats,
+                       d, h, w, amax_bits, lut, q, scale);
 }
 
 }  // namespace
@@ -395,8 +489,8 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
                 what);
     H3V_REQUIRE(eps > 0.0f, "%s: eps must be positive", what);
     H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(beta, 16) && (!pre_bias || aligned(pre_bias, 16)) &&
-                    aligned(q, 8) && aligned(workspace, 4),
-                "%s: x, gamma, beta, pre_bias need 16-byte and q 8-byte alignment", what);
+                    aligned(q, 8) && aligned(workspace, 16),
+                "%s: x, gamma, beta, pre_bias, workspace need 16-byte and q 8-byte alignment", what);
     if (c == 128) {
         if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
         else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);

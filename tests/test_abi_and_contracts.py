@@ -35,7 +35,8 @@ def test_library_loads_and_exports_every_declared_symbol(ops):
     table = set(ops.hip.SIGNATURES) | set(ops.hip.SPECIAL)
     assert set(names) == table
     assert lib.h3v_abi_version() == ops.hip.ABI_VERSION
-    assert lib.h3v_gn_norm_pack_workspace_floats(17, 256, 256) == 2 * 17 * 256 * 32 + 2 * 17 * 256
+    # per-chunk (avg, M2) partials, per-(frame, channel) extreme keys, the 64 KB quantize table
+    assert lib.h3v_gn_norm_pack_workspace_floats(17, 256, 256) == 2 * 17 * 256 * 32 + 2 * 17 * 256 + 65536 // 4
     assert lib.h3v_gn_norm_pack_workspace_floats(0, 1, 1) == -1
 
 
