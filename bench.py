@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--traffic-sample", action="store_true",
+                   help="run only a 1 GiB elementwise copy and three stage-0 fused layers (for rocprofv3 --pmc)")
     p.add_argument("--enc-calls", type=int, default=ENC_CALLS, help=argparse.SUPPRESS)
     p.add_argument("--dec-calls", type=int, default=DEC_CALLS, help=argparse.SUPPRESS)
     return p.parse_args()
@@ -278,6 +280,24 @@ def cpu_baseline(budget_s: float):
     }
 
 
+TRAFFIC_PROFILE = ROOT / "profiles" / "stage0_conv_traffic_pmc.md"
+
+
+def stage0_conv_traffic():
+    """HBM (L2-miss) bytes per stage-0 conv launch from the committed FETCH_SIZE/WRITE_SIZE summary.
+
+    The summary holds one line `traffic_bytes_per_launch: N`, derived from two rocprofv3 --pmc runs of
+    `bench.py --traffic-sample`, each scaled by the counter's reading for a copy of known size.
+    """
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -294,6 +314,21 @@ def main():
     wl = Workload(torch, hip)
     stream = hip.stream(wl.dev)
     enc_calls, dec_calls = args.enc_calls, args.dec_calls
+
+    if args.traffic_sample:
+        # Counter calibration + the dominant kernel in pipeline context.  FETCH_SIZE/WRITE_SIZE of the
+        # copy (1 GiB read + 1 GiB written) give the counter's scale; the stage-0 conv launches follow
+        # their producer exactly as in a step.
+        with torch.inference_mode():
+            src = torch.ones(1 << 29, device=wl.dev, dtype=torch.float16)   # 1 GiB
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                torch.neg(src, out=dst)
+            for _ in range(3):
+                wl.norm_conv(wl.x0, 0, wl.a0, 256, 256, stream)
+            torch.cuda.synchronize()
+        print("[bench] traffic sample done: 3 x neg(1 GiB fp16), 3 x stage-0 producer + conv", file=sys.stderr)
+        return
 
     def step(timings=None):
         t0 = time.perf_counter()
@@ -365,13 +400,13 @@ def main():
         "int8_tops_step": round((enc_ops + dec_ops) / sec_per_step / 1e12, 1),
         "int8_mfma_frac_step": round((enc_ops + dec_ops) / sec_per_step / 1e12 / INT8_PEAK_TOPS, 4),
         "roofline": {
-            "kernel": "gemm_i8_mfma<512,128,128,4,2,2,Conv,Dequant> (stage-0 conv C128->128, [1,128,19,258,258] int8)",
+            "kernel": "gemm_i8_mfma<512,128,128,4,2,2,2,Conv,Dequant> (stage-0 conv C128->128, [1,128,19,258,258] int8)",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": INT8_PEAK_TOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / INT8_PEAK_TOPS, 4),
-            "traffic": None,
+            "traffic": stage0_conv_traffic(),
             "launches_timed": len(conv_ms),
             "avg_us": round(conv_avg_s * 1e6, 1),
             "algorithmic_ops_per_launch": conv_useful,
