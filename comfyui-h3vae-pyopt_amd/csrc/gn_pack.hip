@@ -10,7 +10,7 @@
 //   gn_init       clears the per-(frame, channel) max/min keys and the absmax word
 //   gn_partial    grid (chunks, D): per 256-pixel chunk and group, avg and M2;
 //                 per (frame, channel) max and min of the (pre-biased) input
-//   gn_merge      grid D: Chan merge of the chunks -> (mean, rstd); absmax
+//   gn_merge      grid (32, D): Chan merge of the chunks -> (mean, rstd); absmax
 //                 candidate from the per-channel extremes (below)
 //   norm_absmax   full absmax pass, only when the candidate cannot be proven exact
 //   build_lut     the int8 code of every fp16 pre-activation z under the final scale
@@ -192,98 +192,92 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     if (tid < kGroups) {
         for (int off = PL / 2; off >= 1; off >>= 1)
             for (int i = 0; i < off; ++i) red[i][tid] = red[i][tid] + red[i + off][tid];
-        int64_t dst = ((int64_t)t * nchunk + j) * kGroups + tid;
+        // group-major [frame][group][chunk]: each merge reads one contiguous run
+        int64_t dst = ((int64_t)t * kGroups + tid) * nchunk + j;
         part_avg[dst] = avg_s[tid];
         part_m2[dst] = red[0][tid];
     }
 }
 
-// One workgroup per frame.  Chunk partials are staged through LDS in batches;
-// the 32 group threads then merge them sequentially as in _merge.
-constexpr int kMergeBatch = 256;
+// One wave per (group, frame).  The group's chunk partials are staged through
+// LDS in batches and lane 0 merges them sequentially as in _merge; the lanes of
+// the group's channels then form the absmax candidates.
+constexpr int kMergeBatch = 1024;
 
-__global__ __launch_bounds__(kNT) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
-                                                const uint32_t* __restrict__ vmax, const uint32_t* __restrict__ vmin,
-                                                const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
-                                                int hw, int nchunk, int c, float eps, float* __restrict__ stats,
-                                                uint32_t* __restrict__ amax_bits) {
-    __shared__ float sa[kMergeBatch * kGroups];
-    __shared__ float sm[kMergeBatch * kGroups];
-    __shared__ float mean_s[kGroups], rstd_s[kGroups];
-    __shared__ float red[kNT / 64];
-    const int t = blockIdx.x, tid = threadIdx.x;
+__global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
+                                               const uint32_t* __restrict__ vmax, const uint32_t* __restrict__ vmin,
+                                               const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+                                               int hw, int nchunk, int c, float eps, float* __restrict__ stats,
+                                               uint32_t* __restrict__ amax_bits) {
+    __shared__ float sa[kMergeBatch];
+    __shared__ float sm[kMergeBatch];
+    __shared__ float ms[2];
+    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
     const int cg = c / kGroups;
     const float total = (float)(hw * cg);
-    const float* pa = part_avg + (int64_t)t * nchunk * kGroups;
-    const float* pm = part_m2 + (int64_t)t * nchunk * kGroups;
+    const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
+    const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
 
+    // The terms of both sums are formed by all lanes; lane 0 adds them in chunk
+    // order, so the result is the sequential merge of _merge.
     // pass 1: mean = (sum_j avg_j * n_j) / N
     float san = 0.0f;
     for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
         const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
         __syncthreads();
-        for (int i = tid; i < nb * kGroups; i += kNT) sa[i] = pa[(int64_t)j0 * kGroups + i];
+        for (int i = tid; i < nb; i += 64) {
+            const int jj = j0 + i;
+            const int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
+            sa[i] = pa[jj] * (float)(cnt * cg);
+        }
         __syncthreads();
-        if (tid < kGroups) {
-            // the sum is sequential in j; unrolling lets the LDS reads run ahead of it
+        if (tid == 0) {
 #pragma unroll 16
-            for (int j = 0; j < nb; ++j) {
-                int jj = j0 + j;
-                int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
-                san = san + sa[j * kGroups + tid] * (float)(cnt * cg);
-            }
+            for (int j = 0; j < nb; ++j) san = san + sa[j];
         }
     }
-    const float mean = san / total;
+    if (tid == 0) ms[0] = san / total;
+    __syncthreads();
+    const float mean = ms[0];
     // pass 2: var = (sum_j (m2_j + (n_j * d_j) * d_j)) / N
     float sv = 0.0f;
     for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
         const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
         __syncthreads();
-        for (int i = tid; i < nb * kGroups; i += kNT) {
-            sa[i] = pa[(int64_t)j0 * kGroups + i];
-            sm[i] = pm[(int64_t)j0 * kGroups + i];
+        for (int i = tid; i < nb; i += 64) {
+            const int jj = j0 + i;
+            const int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
+            const float dl = pa[jj] - mean;
+            const float nj = (float)(cnt * cg);
+            sm[i] = pm[jj] + (nj * dl) * dl;
         }
         __syncthreads();
-        if (tid < kGroups) {
+        if (tid == 0) {
 #pragma unroll 16
-            for (int j = 0; j < nb; ++j) {
-                int jj = j0 + j;
-                int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
-                float dl = sa[j * kGroups + tid] - mean;
-                float nj = (float)(cnt * cg);
-                sv = sv + (sm[j * kGroups + tid] + (nj * dl) * dl);
-            }
+            for (int j = 0; j < nb; ++j) sv = sv + sm[j];
         }
     }
-    if (tid < kGroups) {
+    if (tid == 0) {
         float var = sv / total;
         if (var < 0.0f) var = 0.0f;
         const float rstd = rsqrt_rn(var + eps);
-        stats[(t * kGroups + tid) * 2] = mean;
-        stats[(t * kGroups + tid) * 2 + 1] = rstd;
-        mean_s[tid] = mean;
-        rstd_s[tid] = rstd;
+        stats[(t * kGroups + g) * 2] = mean;
+        stats[(t * kGroups + g) * 2 + 1] = rstd;
+        ms[1] = rstd;
     }
     __syncthreads();
     // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map
     float cand = 0.0f;
-    if (tid < c) {
-        const int g = tid / cg;
-        const float gm = h2f(gamma[tid]), bt = h2f(beta[tid]);
-        const float v = gm >= 0.0f ? fval(vmax[t * c + tid]) : fval(vmin[t * c + tid]);
-        const float z = rt16(((v - mean_s[g]) * rstd_s[g]) * gm + bt);
+    if (tid < cg) {
+        const int ch = g * cg + tid;
+        const float gm = h2f(gamma[ch]), bt = h2f(beta[ch]);
+        const float v = gm >= 0.0f ? fval(vmax[t * c + ch]) : fval(vmin[t * c + ch]);
+        const float z = rt16(((v - mean) * ms[1]) * gm + bt);
         cand = __builtin_fabsf(rt16(silu(z)));
     }
     cand = wave_max(cand);
-    if ((tid & 63) == 0) red[tid >> 6] = cand;
-    __syncthreads();
-    if (tid == 0) {
-        float m = red[0];
-        for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
-        // every candidate is the |value| of a real element, so it never exceeds the true absmax
-        atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
-    }
+    // every candidate is the |value| of a real element, so it never exceeds the true absmax
+    if (tid == 0) atomicMax(amax_bits, __builtin_bit_cast(uint32_t, cand));
 }
 
 __device__ __forceinline__ int reflect(int i, int n) { return i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i); }
@@ -451,8 +445,8 @@ void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
     hipLaunchKernelGGL(gn_init, dim3((d * C + kNT - 1) / kNT), dim3(kNT), 0, stream, vmax, vmin, d * C, amax_bits);
     hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
                        part_m2, vmax, vmin);
-    hipLaunchKernelGGL(gn_merge, dim3(d), dim3(kNT), 0, stream, part_avg, part_m2, vmax, vmin, gamma, beta, hw, nchunk,
-                       C, eps, stats, amax_bits);
+    hipLaunchKernelGGL(gn_merge, dim3(kGroups, d), dim3(64), 0, stream, part_avg, part_m2, vmax, vmin, gamma, beta, hw,
+                       nchunk, C, eps, stats, amax_bits);
     const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
     int64_t want = (nvec + kNT - 1) / kNT;
     unsigned blocks = (unsigned)(want > 16384 ? 16384 : want);
