@@ -96,16 +96,16 @@ API float ora_expf(float x) {
     const float LN2_HI = 0x1.62e4p-1f;     /* 15 significant bits of ln 2 */
     const float LN2_LO = 0x1.7f7d1cp-20f;  /* ln 2 - LN2_HI */
     float n = rintf(x * LOG2E);
-    float r = x - n * LN2_HI;
-    r = r - n * LN2_LO;
+    float r = fmaf(-n, LN2_HI, x);          /* n * LN2_HI is exact: one rounding either way */
+    r = fmaf(-n, LN2_LO, r);
     float p = 0x1.a01a02p-13f;             /* 1/5040 */
-    p = p * r + 0x1.6c16c2p-10f;           /* 1/720  */
-    p = p * r + 0x1.111112p-7f;            /* 1/120  */
-    p = p * r + 0x1.555556p-5f;            /* 1/24   */
-    p = p * r + 0x1.555556p-3f;            /* 1/6    */
-    p = p * r + 0.5f;
-    p = p * r + 1.0f;
-    p = p * r + 1.0f;
+    p = fmaf(p, r, 0x1.6c16c2p-10f);       /* 1/720  */
+    p = fmaf(p, r, 0x1.111112p-7f);        /* 1/120  */
+    p = fmaf(p, r, 0x1.555556p-5f);        /* 1/24   */
+    p = fmaf(p, r, 0x1.555556p-3f);        /* 1/6    */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
     return ldexpf(p, (int)n);
 }
 
