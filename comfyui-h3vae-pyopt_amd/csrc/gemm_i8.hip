@@ -15,8 +15,8 @@
 // Tiling: BM x BN x BK workgroup tile of 8 waves (2 per SIMD), each owning a
 // 128 x 64 block built from v_mfma_i32_32x32x32_i8.  Operands stream
 // global -> LDS with LDS-DMA (global_load_lds_dwordx4) into an NSA-slot A ring
-// and an NSB-slot B ring, issued NSA-1 / NSB-1 K steps ahead of the MFMAs; one
-// barrier per K step.  The activation operand A misses L2 more often than the
+// and an NSB-slot B ring, issued NSA-1 / NSB-1 K steps ahead of the MFMAs by
+// one wave per SIMD (the other keeps the matrix pipe busy); one barrier per K step.  The activation operand A misses L2 more often than the
 // weights, so it gets the deeper ring when the LDS allows.  BK = 128 is
 // the default: every row segment a K step fetches is then one whole 128-byte
 // cache line (64-byte segments use half of each line fetched into L1 and
@@ -210,9 +210,15 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     constexpr int LPR = BK / 16;                              // DMA lanes per tile row
     constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
     constexpr int B_RING = NSA * A_BYTES, RING = NSA * A_BYTES + NSB * B_BYTES;
-    constexpr int A_PW = BM / RPI / NW, B_PW = BN / RPI / NW; // row groups per wave
-    constexpr int LPS = A_PW + B_PW;                          // DMA instructions per stage per wave
-    static_assert(A_PW * RPI * NW == BM && B_PW * RPI * NW == BN, "tile rows must split into row groups per wave");
+    // Only the first half of the waves (one per SIMD: wave w runs on SIMD w % 4) issue the DMA.
+    // A global_load_lds instruction holds up its wave's MFMA issue for about as long as the
+    // transfer takes; with every wave issuing, both waves of a SIMD stall together and its matrix
+    // pipe idles (measured: 62% of peak for MFMA + DMA on all waves, 72% with one issuing wave per
+    // SIMD, in a barrier-free probe).  The other wave keeps the pipe busy meanwhile.
+    constexpr int NWD = NW / 2;                               // DMA-issuing waves
+    constexpr int A_PW = BM / RPI / NWD, B_PW = BN / RPI / NWD; // row groups per issuing wave
+    constexpr int LPS = A_PW + B_PW;                          // DMA instructions per stage per issuing wave
+    static_assert(A_PW * RPI * NWD == BM && B_PW * RPI * NWD == BN, "tile rows must split into row groups per wave");
     static_assert(EP != Epi::SwiGLU || (WN % 64) == 0, "SwiGLU pairs need 64-column wave tiles");
     static_assert(NSA >= 2 && NSA <= 4 && NSB >= 2 && NSB <= NSA && (NSA == NSB || NSB == 2), "LDS ring depths");
     static_assert((NSA - 1) * A_PW + (NSB - 1) * B_PW < 64, "outstanding DMA must fit vmcnt");
@@ -240,11 +246,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
 
     const int lrow = lane / LPR;
     const int lslot = lane % LPR;
+    const bool dma_wave = wave < NWD;
+    const int dw = dma_wave ? wave : 0;                       // index among the issuing waves
 
     int64_t aoff[A_PW];
 #pragma unroll
     for (int j = 0; j < A_PW; ++j) {
-        const int r = (wave * A_PW + j) * RPI + lrow;
+        const int r = (dw * A_PW + j) * RPI + lrow;
         int m = m0 + r;
         m = m < p.M ? m : p.M - 1;
         aoff[j] = (AM == AMode::Gemm ? (int64_t)m * p.lda : conv_row_offset(p, m)) + ((lslot ^ swz<BK>(r)) << 4);
@@ -252,7 +260,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     const int8_t* bptr[B_PW];
 #pragma unroll
     for (int j = 0; j < B_PW; ++j) {
-        int r = (wave * B_PW + j) * RPI + lrow;
+        int r = (dw * B_PW + j) * RPI + lrow;
         int wrow;
         if constexpr (EP == Epi::SwiGLU) {
             // tile row r -> pair r/64, half (r/32)&1 (0 gate, 1 up), column r&31
@@ -301,14 +309,16 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
                 }
             }
         }
+        if (!dma_wave) return;
 #pragma unroll
-        for (int j = 0; j < A_PW; ++j) lds_dma16(p.a + aoff[j] + koff, sa + (wave * A_PW + j) * 1024);
+        for (int j = 0; j < A_PW; ++j) lds_dma16(p.a + aoff[j] + koff, sa + (dw * A_PW + j) * 1024);
     };
     auto issue_b = [&](int it) {
         const int kb = kb0 + it;
         int8_t* sb = smem + B_RING + (it % NSB) * B_BYTES;
+        if (!dma_wave) return;
 #pragma unroll
-        for (int j = 0; j < B_PW; ++j) lds_dma16(bptr[j] + (int64_t)kb * BK, sb + (wave * B_PW + j) * 1024);
+        for (int j = 0; j < B_PW; ++j) lds_dma16(bptr[j] + (int64_t)kb * BK, sb + (dw * B_PW + j) * 1024);
     };
 
     v16i acc[FM][FN];
