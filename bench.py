@@ -51,6 +51,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-configs", action="store_true", help="skip the per-config (BASELINE configs 1-4) kernel timings")
     p.add_argument("--traffic-sample", action="store_true",
                    help="run only a 1 GiB elementwise copy and three stage-0 fused layers (for rocprofv3 --pmc)")
     p.add_argument("--enc-calls", type=int, default=ENC_CALLS, help=argparse.SUPPRESS)
@@ -61,7 +62,7 @@ def parse():
 class Workload:
     """Preallocated synthetic inputs, weights and scratch for the hot path."""
 
-    def __init__(self, torch, hip, seed=20261002):
+    def __init__(self, torch, hip, kitchen, enc, seed=20261002):
         self.torch, self.hip = torch, hip
         dev = self.dev = torch.device("cuda:0")
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -70,8 +71,16 @@ class Workload:
         def randn(*shape, scale=1.0):
             return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * scale).to(f16)
 
-        def randi8(*shape, lo=-127, hi=128):
-            return torch.randint(lo, hi, shape, generator=g, device=dev, dtype=i8)
+        def linear(n, k):
+            """Random-init nn.Linear weight N(0, 0.02) quantized per row by the INT8 weight quantizer."""
+            q, s = kitchen.quantize_int8_rowwise(randn(n, k, scale=0.02))
+            return q, s.reshape(-1).contiguous(), randn(n, scale=0.02)
+
+        def conv(cout, cin):
+            """Kaiming-normal 3x3x3 conv weight packed + quantized per output channel (E1)."""
+            w = randn(cout, cin, 3, 3, 3, scale=(2.0 / (27 * cin)) ** 0.5)
+            qw, ws, _ = enc.prepare_int8_weight(w)
+            return qw, ws
 
         # ---------------- encoder (stage 0 @256^2 C128, stage 1 @128^2) ----------------
         t = 17
@@ -80,11 +89,10 @@ class Workload:
         self.enc_layers += [(128, 256, 128, 128)] + [(256, 256, 128, 128)] * 3
         self.enc_w = []
         for cin, cout, h, w in self.enc_layers:
-            qw = randi8(cout, 27 * cin)
-            ws = (torch.rand(cout, generator=g, device=dev) * 2e-4 + 1e-5).to(f32)
-            bias = randn(cout, scale=0.1)
-            gamma = (1 + 0.1 * torch.randn(cin, generator=g, device=dev)).to(f16)
-            beta = randn(cin, scale=0.1)
+            qw, ws = conv(cout, cin)
+            bias = randn(cout, scale=0.02)
+            gamma = torch.ones(cin, device=dev, dtype=f16)        # unit GroupNorm affine at init
+            beta = torch.zeros(cin, device=dev, dtype=f16)
             self.enc_w.append((qw, ws, bias, gamma, beta))
         self.x0 = randn(t, 256, 256, 128)                         # NDHWC stage-0 input
         self.x1 = randn(t, 128, 128, 128)                         # stage-1 input (after the FP16 downsample)
@@ -105,21 +113,16 @@ class Workload:
         self.blocks = []
         for _ in range(DEC_BLOCKS):
             blk = {
-                "g1": (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16),
-                "g2": (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16),
+                "g1": torch.ones(d, device=dev, dtype=f16), "g2": torch.ones(d, device=dev, dtype=f16),
                 "scale1": randn(d, scale=0.1), "scale2": randn(d, scale=0.1),
-                "qkv": randi8(6144, d), "qkv_s": (torch.rand(6144, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
-                "qkv_b": randn(6144, scale=0.02),
-                "out": randi8(d, d), "out_s": (torch.rand(d, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
-                "out_b": randn(d, scale=0.02),
-                "up": randi8(16384, d), "up_s": (torch.rand(16384, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
-                "up_b": randn(16384, scale=0.02),
-                "down": randi8(d, 8192), "down_s": (torch.rand(d, generator=g, device=dev) * 1e-3 + 1e-4).to(f32),
-                "down_b": randn(d, scale=0.02),
             }
+            blk["qkv"], blk["qkv_s"], blk["qkv_b"] = linear(6144, d)
+            blk["out"], blk["out_s"], blk["out_b"] = linear(d, d)
+            blk["up"], blk["up_s"], blk["up_b"] = linear(16384, d)
+            blk["down"], blk["down_s"], blk["down_b"] = linear(d, 8192)
             self.blocks.append(blk)
-        self.ln_g = (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16)
-        self.ln_b = randn(d, scale=0.02)
+        self.ln_g = torch.ones(d, device=dev, dtype=f16)
+        self.ln_b = torch.zeros(d, device=dev, dtype=f16)
         self.tokens0 = randn(m, d)
         self.attn_y = randn(m, d)                     # stand-in for the SDPA output
         cos_sin = torch.rand(m, 48, generator=g, device=dev) * 6.283
@@ -137,6 +140,7 @@ class Workload:
         self.gate_up = torch.empty((m, 16384), device=dev, dtype=f16)
         self.final = torch.empty((m, d), device=dev, dtype=f16)
         self.conv_events = None
+        torch.cuda.synchronize()
 
     # -- raw C-ABI helpers ---------------------------------------------------------------
     def _p(self, t):
@@ -205,6 +209,124 @@ class Workload:
             h, h2 = h2, h
         call("h3v_residual_layernorm", p(h), p(self.o), p(self.blocks[-1]["scale2"]), p(self.ln_g), p(self.ln_b),
              9.999999747378752e-06, m, d, p(self.final), stream)
+
+
+def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
+    """BASELINE.json configs 1-4 on their own shapes: mean kernel time and roofline fraction each.
+
+    Every entry is timed with HIP events on the launch stream over `reps` launches after 3 warm-up
+    launches; `frac` is achieved INT8 ops / the INT8 dense peak (MFMA-bound kernels) or algorithmic
+    bytes / 8 TB/s (memory-bound kernels).
+    """
+    import torch.nn.functional as F
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(20261002)
+    f16, i8, f32 = torch.float16, torch.int8, torch.float32
+    call, p = hip.call, hip.ptr
+
+    def randn(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=f32) * scale).to(f16)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps          # microseconds
+
+    def mfma(us, ops):
+        return {"us": round(us, 2), "tops": round(ops / us / 1e6, 1), "frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
+                "bound": "mfma", "ops": ops}
+
+    def hbm(us, nbytes):
+        return {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+                "bound": "hbm", "bytes": nbytes}
+
+    out = {}
+    with torch.inference_mode():
+        # cfg1: causal conv3d C128 -> 128 on [1,128,9,64,64]: per-tensor quant of the padded input + INT8 conv
+        x = randn(1, 128, 9, 64, 64)
+        xp = F.pad(x.float(), (1, 1, 1, 1, 0, 0), mode="reflect").to(f16)
+        xp = F.pad(xp, (0, 0, 0, 0, 2, 0))                                   # two zero causal frames
+        xn = xp[0].permute(1, 2, 3, 0).contiguous()                           # [11, 66, 66, 128]
+        qw, ws, _ = enc.prepare_int8_weight(randn(128, 128, 3, 3, 3, scale=3456 ** -0.5))
+        bias = randn(128, scale=0.1)
+        qx = torch.empty(xn.numel(), device=dev, dtype=i8)
+        xs = torch.empty(1, device=dev, dtype=f32)
+        amax = torch.empty(1, device=dev, dtype=torch.int32)
+        y = torch.empty((9, 64, 64, 128), device=dev, dtype=f16)
+        t_q = timed(lambda: call("h3v_tensor_quant_i8", p(xn), xn.numel(), p(qx), p(xs), p(amax), stream))
+        t_c = timed(lambda: call("h3v_conv3d_i8", p(qx), p(xs), p(qw), p(ws), p(bias), p(y), 1, 128, 11, 66, 66, 128,
+                                 3, 3, 3, 1, 1, 1, 1, stream))
+        useful = 2 * 36864 * 128 * 3456 * 8 // 9
+        out["cfg1_causal_conv3d_c128_9x64x64"] = {"tensor_quant": hbm(t_q, xn.numel() * 3),
+                                                   "conv": mfma(t_c, useful)}
+        del x, xp, xn, qx, y
+
+        # cfg2: residual + norm1 (RMS, W16 tree) + row quant, then QKV GEMM 1024 -> 3072, M = 16384
+        m, d = 16384, 1024
+        h, o = randn(m, d), randn(m, d)
+        gate, gam, beta = randn(d, scale=0.1), (1 + 0.1 * torch.randn(d, generator=g, device=dev)).to(f16), randn(d, scale=0.02)
+        h_out = torch.empty_like(h)
+        q = torch.empty((m, 8192), device=dev, dtype=i8)
+        sx = torch.empty(m, device=dev, dtype=f32)
+        wq, wqs = kitchen.quantize_int8_rowwise(randn(3072, d, scale=0.02))
+        wqs = wqs.reshape(-1).contiguous()
+        bq = randn(3072, scale=0.02)
+        qkv = torch.empty((m, 3072), device=dev, dtype=f16)
+        t_n = timed(lambda: call("h3v_residual_norm1_quant", p(h), p(o), p(gate), p(gam), 1e-5, m, d, p(h_out), p(q),
+                                 p(sx), stream))
+        t_ln = timed(lambda: call("h3v_residual_layernorm", p(h), p(o), p(gate), p(gam), p(beta), 1e-5, m, d, p(h_out),
+                                  stream))
+        t_g = timed(lambda: call("h3v_gemm_i8_dequant", p(q), p(sx), p(wq), p(wqs), p(bq), p(qkv), m, 3072, d, stream))
+        out["cfg2_norm1_qkv_m16384_d1024"] = {"residual_rms_quant": hbm(t_n, m * d * 7 + m * 4),
+                                              "residual_layernorm": hbm(t_ln, m * d * 6),
+                                              "qkv_gemm": mfma(t_g, 2 * m * 3072 * d)}
+
+        # cfg3: FFN-up GEMM over [gate | up] (1024 -> 2 x 4096) + SwiGLU row quant + down GEMM 4096 -> 1024
+        xq = randn(m, d)
+        t_rq = timed(lambda: call("h3v_row_quant", p(xq), m, d, p(q), p(sx), stream))
+        wu, wus = kitchen.quantize_int8_rowwise(randn(8192, d, scale=0.02))
+        wd, wds = kitchen.quantize_int8_rowwise(randn(d, 4096, scale=0.02))
+        wus, wds = wus.reshape(-1).contiguous(), wds.reshape(-1).contiguous()
+        bu, bd = randn(8192, scale=0.02), randn(d, scale=0.02)
+        gu = torch.empty((m, 8192), device=dev, dtype=f16)
+        q2 = torch.empty((m, 4096), device=dev, dtype=i8)
+        s2 = torch.empty(m, device=dev, dtype=f32)
+        yo = torch.empty((m, d), device=dev, dtype=f16)
+        t_up = timed(lambda: call("h3v_gemm_i8_dequant", p(q), p(sx), p(wu), p(wus), p(bu), p(gu), m, 8192, d, stream))
+        t_sw = timed(lambda: call("h3v_swiglu_row_quant", p(gu), m, 4096, p(q2), p(s2), stream))
+        t_dn = timed(lambda: call("h3v_gemm_i8_dequant", p(q2), p(s2), p(wd), p(wds), p(bd), p(yo), m, d, 4096, stream))
+        out["cfg3_ffn_m16384_d1024_h4096"] = {"row_quant": hbm(t_rq, m * d * 3 + m * 4),
+                                              "up_gemm": mfma(t_up, 2 * m * 8192 * d),
+                                              "swiglu_row_quant": hbm(t_sw, m * 8192 * 2 + m * 4096 + m * 4),
+                                              "down_gemm": mfma(t_dn, 2 * m * d * 4096)}
+        del gu
+
+        # cfg4: QK-RMSNorm-RoPE on [16384, 16 heads x (q|k|v)], attention-out row quant + GEMM 1024 -> 1024
+        heads = 16
+        qkv4 = randn(m, heads * 192)
+        ang = torch.rand(m, 48, generator=g, device=dev) * 6.283
+        cos, sin = ang.cos().to(f16), ang.sin().to(f16)
+        rq = torch.empty((m, heads, 64), device=dev, dtype=f16)
+        rk = torch.empty((m, heads, 64), device=dev, dtype=f16)
+        t_r = timed(lambda: call("h3v_qk_rope", p(qkv4), p(cos), p(sin), m, heads, 64, 48, 1e-6, p(rq), p(rk), stream))
+        ya = randn(m, d)
+        wo, wos = kitchen.quantize_int8_rowwise(randn(d, d, scale=0.02))
+        wos = wos.reshape(-1).contiguous()
+        bo = randn(d, scale=0.02)
+        t_oq = timed(lambda: call("h3v_row_quant", p(ya), m, d, p(q), p(sx), stream))
+        t_og = timed(lambda: call("h3v_gemm_i8_dequant", p(q), p(sx), p(wo), p(wos), p(bo), p(yo), m, d, d, stream))
+        rope_bytes = m * heads * 128 * 2 * 2 + 2 * m * 48 * 2
+        out["cfg4_qk_rope_out_proj_16384tok_16x64"] = {"qk_rope": hbm(t_r, rope_bytes),
+                                                       "out_row_quant": hbm(t_oq, m * d * 3 + m * 4),
+                                                       "out_gemm": mfma(t_og, 2 * m * d * d)}
+    torch.cuda.synchronize()
+    return out
 
 
 def enc_ops_per_call():
@@ -313,7 +435,9 @@ def main():
     import importlib
     hip = importlib.import_module(f"{pkg.__name__}._hip")
     hip.require_gfx950("cuda:0", "bench")
-    wl = Workload(torch, hip)
+    kitchen = importlib.import_module(f"{pkg.__name__}.opt.kitchen_int8")
+    enc = importlib.import_module(f"{pkg.__name__}.opt.encoder_int8")
+    wl = Workload(torch, hip, kitchen, enc)
     stream = hip.stream(wl.dev)
     enc_calls, dec_calls = args.enc_calls, args.dec_calls
 
@@ -387,7 +511,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (seeded random int8 weights of H3 shape, random fp16 activations, resident in HBM)",
+        "data": ("synthetic, seeded: random-init H3-shaped weights (linears N(0,0.02), kaiming-normal convs, unit norm "
+                 "affines) quantized by the build's INT8 weight quantizers; N(0,1) fp16 activations; all resident in HBM"),
         "config": {
             "workload": "h3vae_int8_hot_path_encode_decode_1x3x124x768x1344_tile256",
             "encode_prefix_calls": enc_calls,
@@ -414,6 +539,9 @@ def main():
             "algorithmic_ops_per_launch": conv_useful,
         },
     }
+    if not args.no_configs:
+        log("timing BASELINE configs 1-4 on their own shapes")
+        result["configs"] = config_measurements(torch, hip, kitchen, enc, stream)
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline sample")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

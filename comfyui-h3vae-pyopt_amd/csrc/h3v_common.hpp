@@ -51,6 +51,30 @@ __device__ __forceinline__ float exp_f32(float x) {
 // SiLU written as the reference writes it: z / (1 + exp(-z)).
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + exp_f32(-z)); }
 
+// Quotient a / b (b > 0) through the hardware reciprocal and one fused Newton
+// correction of the quotient: q0 = a * r, e = a - q0 * b (exact), q = q0 + e * r,
+// with the sign of q0 (which is the quotient's sign; it keeps -0 / b = -0).  The
+// error is within a tiny fraction of an ulp beyond 1/2, so q is the IEEE quotient
+// unless a / b lies almost exactly on a rounding boundary.  Used only where that
+// never happens for the operands that occur; h3v_selftest_fast_div checks every
+// case on the device (all fp16 numerators against all finite positive fp16
+// divisors, and every fp16 SiLU argument).
+__device__ __forceinline__ float div_newton(float a, float b, float r) {
+    const float q0 = a * r;
+    const float e = __builtin_fmaf(-q0, b, a);
+    return __builtin_copysignf(__builtin_fmaf(e, r, q0), q0);
+}
+
+// SiLU of an fp16-valued z with the fast quotient where the denominator is a
+// finite normal number; the IEEE path keeps the special cases (|z| large, inf, NaN).
+__device__ __forceinline__ float silu_fast(float z) {
+    if (__builtin_fabsf(z) <= 80.0f) {
+        const float den = 1.0f + exp_f32(-z);
+        return div_newton(z, den, __builtin_amdgcn_rcpf(den));
+    }
+    return silu(z);
+}
+
 // 1/sqrt as two correctly rounded operations.
 __device__ __forceinline__ float rsqrt_rn(float x) { return 1.0f / __builtin_sqrtf(x); }
 
@@ -64,6 +88,31 @@ __device__ __forceinline__ float q1_scale(float amax) {
 // v = fp16(a / d); v = rint(v); NaN -> -128; clamp [-128, 127].
 __device__ __forceinline__ int q1_quant(float a, float d) {
     float v = rt16(a / d);
+    v = __builtin_rintf(v);
+    if (v != v) return -128;
+    v = __builtin_fminf(127.0f, __builtin_fmaxf(-128.0f, v));
+    return (int)v;
+}
+
+// The row quantizer's divisor d = fp32(fp16(scale)) with its reciprocal.  When d is
+// finite and positive, every finite fp16 numerator goes through the fast quotient
+// (both operands have 11-bit significands, so their quotient never sits near an
+// fp32 rounding boundary without being on it); otherwise the IEEE division runs.
+struct Q1Div {
+    float d, r;
+    bool fast;
+};
+__device__ __forceinline__ Q1Div q1_div(float d) {
+    Q1Div q;
+    q.d = d;
+    q.r = __builtin_amdgcn_rcpf(d);
+    q.fast = d > 0.0f && d <= 65504.0f;
+    return q;
+}
+// q1_quant with the divisor prepared once per row; identical results.  A row whose
+// divisor is finite and positive holds no infinite value (its amax would be infinite).
+__device__ __forceinline__ int q1_quant(float a, const Q1Div& q) {
+    float v = rt16(q.fast ? div_newton(a, q.d, q.r) : a / q.d);
     v = __builtin_rintf(v);
     if (v != v) return -128;
     v = __builtin_fminf(127.0f, __builtin_fmaxf(-128.0f, v));

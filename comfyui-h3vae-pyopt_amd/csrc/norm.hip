@@ -1,13 +1,22 @@
 // Decoder row producers: residual + RMSNorm + row quantization (norm1 / norm2),
 // the block-0 RMSNorm and the final residual + LayerNorm.
 //
-// One 256-thread workgroup per row of width K (K/4 a power of two, K <= 4096).
-// Reductions follow a fixed tree that does not depend on the wave size: the
-// row is split into K/4 "virtual threads" of four consecutive values; each
-// forms a partial, partials are combined by a butterfly over groups of 32
-// (offsets 16, 8, 4, 2, 1) and the group results by a butterfly over the
-// groups.  Virtual thread v lives in real thread v % 256, so the 32-groups map
-// onto 32-lane halves of a wave64 and the in-group butterfly is a lane shuffle.
+// One wave per row of width K = NCH * 512 (K in {1024, 2048, 4096}); four rows
+// per 256-thread workgroup, no LDS and no workgroup barrier (measured against
+// one 256-thread workgroup per row: 20.7 vs 27.5 us at 16384 x 1024, equal at
+// 7188 x 2048).  Lane L holds the
+// eight consecutive values [c*512 + 8L, c*512 + 8L + 8) of each chunk c, read
+// and written with 16-byte accesses.
+//
+// Reductions follow a fixed tree that does not depend on how lanes hold the
+// row: the row is split into K/4 "virtual threads" of four consecutive values;
+// each forms a partial, partials are combined by a butterfly over groups of 32
+// (offsets 16, 8, 4, 2, 1) and the K/128 group results by the halving tree
+// g[i] += g[i + off], off = K/256 .. 1.  Lane L holds virtual threads
+// c*128 + 2L and c*128 + 2L + 1, so the butterfly offsets 16..2 are lane XORs
+// 8..1 inside 16-lane segments and offset 1 is a lane-local add; group
+// c*4 + L/16 sits in chunk c of segment L/16, so the halving tree is local
+// across chunks for off >= 4 and lane XORs 32 and 16 for off = 2 and 1.
 //
 // Partial of four values:
 //   W16 recipe (norm1, docs/decoder_norm1_contract_2026-10-03.md:57-70):
@@ -20,35 +29,9 @@ namespace h3v {
 namespace {
 
 constexpr int kNT = 256;
+constexpr int kRowsPerBlock = kNT / 64;
 
 enum class Recipe { W16, Plain };
-
-template <int VPT>
-struct RowTree {
-    // partial of one virtual thread -> in-group butterfly -> group butterfly
-    __device__ static float reduce(float (&p)[VPT], float* lds) {
-        const int t = threadIdx.x;
-#pragma unroll
-        for (int j = 0; j < VPT; ++j)
-#pragma unroll
-            for (int off = 16; off >= 1; off >>= 1) p[j] = p[j] + __shfl_xor(p[j], off, 64);
-        // group index of virtual thread t + j*256 is t/32 + j*8
-        if ((t & 31) == 0) {
-#pragma unroll
-            for (int j = 0; j < VPT; ++j) lds[t / 32 + j * (kNT / 32)] = p[j];
-        }
-        __syncthreads();
-        constexpr int NG = VPT * (kNT / 32);
-        if (t == 0) {
-            for (int off = NG / 2; off >= 1; off >>= 1)
-                for (int i = 0; i < off; ++i) lds[i] = lds[i] + lds[i + off];
-        }
-        __syncthreads();
-        float r = lds[0];
-        __syncthreads();  // lds may be reused by the caller
-        return r;
-    }
-};
 
 __device__ __forceinline__ float partial_w16(const float* x) {
     float s1 = x[1] * x[1];
@@ -60,155 +43,176 @@ __device__ __forceinline__ float partial_w16(const float* x) {
 
 __device__ __forceinline__ float partial_plain(const float* t) { return ((t[0] + t[1]) + t[2]) + t[3]; }
 
-__device__ __forceinline__ void load4(const uint16_t* p, float* v) {
-    u16x4 a = *reinterpret_cast<const u16x4*>(p);
-    v[0] = h2f(a[0]); v[1] = h2f(a[1]); v[2] = h2f(a[2]); v[3] = h2f(a[3]);
-}
-
-__device__ __forceinline__ void store4(uint16_t* p, const float* v) {
-    u16x4 a = {f2h(v[0]), f2h(v[1]), f2h(v[2]), f2h(v[3])};
-    *reinterpret_cast<u16x4*>(p) = a;
-}
-
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = wave_max(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = red[0];
+// Tree sum of the row from the two partials p[c][0..1] every lane holds per chunk.
+template <int NCH>
+__device__ __forceinline__ float row_tree(float (&p)[NCH][2]) {
 #pragma unroll
-    for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
-    return m;
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int off = 8; off >= 1; off >>= 1) p[c][h] = p[c][h] + __shfl_xor(p[c][h], off, 64);
+    float g[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) g[c] = p[c][0] + p[c][1];
+#pragma unroll
+    for (int off = NCH * 2; off >= 4; off >>= 1)
+#pragma unroll
+        for (int c = 0; c < off / 4; ++c) g[c] = g[c] + g[c + off / 4];
+    g[0] = g[0] + __shfl_xor(g[0], 32, 64);
+    g[0] = g[0] + __shfl_xor(g[0], 16, 64);
+    return __shfl(g[0], 0, 64);
+}
+
+__device__ __forceinline__ void load8f(const uint16_t* p, float* v) {
+    u16x8 a = *reinterpret_cast<const u16x8*>(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = h2f(a[e]);
+}
+
+__device__ __forceinline__ void store8h(uint16_t* p, const float* v) {
+    u16x8 a;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = f2h(v[e]);
+    *reinterpret_cast<u16x8*>(p) = a;
 }
 
 // N1 / F1: raw = fma(o, g, h); h_out = fp16(raw); ss = tree(raw^2);
 // inv = 1/sqrt(ss/K + eps); n = fp16((fp32(h_out) * inv) * w); row-quantize n.
-template <int VPT, Recipe R>
+template <int NCH, Recipe R>
 __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t* h, const uint16_t* __restrict__ o,
                                                                  const uint16_t* __restrict__ g, const uint16_t* __restrict__ w,
                                                                  float eps, uint16_t* h_out, int8_t* __restrict__ q,
-                                                                 float* __restrict__ s) {
-    constexpr int K = VPT * kNT * 4;
-    __shared__ float lds[VPT * (kNT / 32)];
-    __shared__ float red[kNT / 64];
-    const int64_t row = blockIdx.x;
-    const int t = threadIdx.x;
-    float raw[VPT][4];
-    float part[VPT];
+                                                                 float* __restrict__ s, int64_t m) {
+    constexpr int K = NCH * 512;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= m) return;
+    float raw[NCH][8];
+    float part[NCH][2];
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int col = (t + j * kNT) * 4;
-        float hv[4], ov[4], gv[4];
-        load4(h + row * K + col, hv);
-        load4(o + row * K + col, ov);
-        load4(g + col, gv);
+    for (int c = 0; c < NCH; ++c) {
+        const int col = c * 512 + lane * 8;
+        float hv[8], ov[8], gv[8];
+        load8f(h + row * K + col, hv);
+        load8f(o + row * K + col, ov);
+        load8f(g + col, gv);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) raw[j][e] = __builtin_fmaf(ov[e], gv[e], hv[e]);
-        if constexpr (R == Recipe::W16) {
-            part[j] = partial_w16(raw[j]);
-        } else {
-            float sq[4] = {raw[j][0] * raw[j][0], raw[j][1] * raw[j][1], raw[j][2] * raw[j][2], raw[j][3] * raw[j][3]};
-            part[j] = partial_plain(sq);
+        for (int e = 0; e < 8; ++e) raw[c][e] = __builtin_fmaf(ov[e], gv[e], hv[e]);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const float* x = &raw[c][hh * 4];
+            if constexpr (R == Recipe::W16) {
+                part[c][hh] = partial_w16(x);
+            } else {
+                float sq[4] = {x[0] * x[0], x[1] * x[1], x[2] * x[2], x[3] * x[3]};
+                part[c][hh] = partial_plain(sq);
+            }
         }
     }
-    const float ss = RowTree<VPT>::reduce(part, lds);
+    const float ss = row_tree<NCH>(part);
     const float inv = rsqrt_rn(ss / (float)K + eps);
-    float nrm[VPT][4];
     float amax = 0.0f;
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int col = (t + j * kNT) * 4;
-        float wv[4], hr[4];
-        load4(w + col, wv);
+    for (int c = 0; c < NCH; ++c) {
+        const int col = c * 512 + lane * 8;
+        float wv[8], hr[8];
+        load8f(w + col, wv);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            hr[e] = rt16(raw[j][e]);
-            nrm[j][e] = rt16((hr[e] * inv) * wv[e]);
-            amax = __builtin_fmaxf(amax, __builtin_fabsf(nrm[j][e]));
+        for (int e = 0; e < 8; ++e) {
+            hr[e] = rt16(raw[c][e]);
+            raw[c][e] = rt16((hr[e] * inv) * wv[e]);
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(raw[c][e]));
         }
-        store4(h_out + row * K + col, hr);
+        store8h(h_out + row * K + col, hr);
     }
-    amax = block_max(amax, red);
+    amax = wave_max(amax);
     const float sc = q1_scale(amax);
-    const float d = rt16(sc);
+    const Q1Div qd = q1_div(rt16(sc));
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int col = (t + j * kNT) * 4;
-        *reinterpret_cast<uint32_t*>(q + row * K + col) =
-            pack4(q1_quant(nrm[j][0], d), q1_quant(nrm[j][1], d), q1_quant(nrm[j][2], d), q1_quant(nrm[j][3], d));
+    for (int c = 0; c < NCH; ++c) {
+        const int col = c * 512 + lane * 8;
+        const float* v = raw[c];
+        uint32_t lo = pack4(q1_quant(v[0], qd), q1_quant(v[1], qd), q1_quant(v[2], qd), q1_quant(v[3], qd));
+        uint32_t hi = pack4(q1_quant(v[4], qd), q1_quant(v[5], qd), q1_quant(v[6], qd), q1_quant(v[7], qd));
+        *reinterpret_cast<uint2*>(q + row * K + col) = make_uint2(lo, hi);
     }
-    if (t == 0) s[row] = sc;
+    if (lane == 0) s[row] = sc;
 }
 
 // N3: out = fp16((x * inv) * gamma), inv = 1/sqrt(W16(x^2)/K + eps).
-template <int VPT>
+template <int NCH>
 __global__ __launch_bounds__(kNT) void rms_fp16_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma,
-                                                       float eps, uint16_t* __restrict__ out) {
-    constexpr int K = VPT * kNT * 4;
-    __shared__ float lds[VPT * (kNT / 32)];
-    const int64_t row = blockIdx.x;
-    const int t = threadIdx.x;
-    float xv[VPT][4], part[VPT];
+                                                       float eps, uint16_t* __restrict__ out, int64_t m) {
+    constexpr int K = NCH * 512;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= m) return;
+    float xv[NCH][8], part[NCH][2];
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        load4(x + row * K + (t + j * kNT) * 4, xv[j]);
-        part[j] = partial_w16(xv[j]);
+    for (int c = 0; c < NCH; ++c) {
+        load8f(x + row * K + c * 512 + lane * 8, xv[c]);
+        part[c][0] = partial_w16(&xv[c][0]);
+        part[c][1] = partial_w16(&xv[c][4]);
     }
-    const float inv = rsqrt_rn(RowTree<VPT>::reduce(part, lds) / (float)K + eps);
+    const float inv = rsqrt_rn(row_tree<NCH>(part) / (float)K + eps);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int col = (t + j * kNT) * 4;
-        float gv[4], r[4];
-        load4(gamma + col, gv);
+    for (int c = 0; c < NCH; ++c) {
+        const int col = c * 512 + lane * 8;
+        float gv[8], r[8];
+        load8f(gamma + col, gv);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (xv[j][e] * inv) * gv[e];
-        store4(out + row * K + col, r);
+        for (int e = 0; e < 8; ++e) r[e] = (xv[c][e] * inv) * gv[e];
+        store8h(out + row * K + col, r);
     }
 }
 
 // N4: raw = fma(o, gate, h); mean = plain(raw)/K; var = plain((raw-mean)^2)/K;
 // y = fp16(fma((raw - mean) * inv, gamma, beta)).
-template <int VPT>
+template <int NCH>
 __global__ __launch_bounds__(kNT) void residual_layernorm_kernel(const uint16_t* __restrict__ h, const uint16_t* __restrict__ o,
                                                                  const uint16_t* __restrict__ gate, const uint16_t* __restrict__ gamma,
                                                                  const uint16_t* __restrict__ beta, float eps,
-                                                                 uint16_t* __restrict__ out) {
-    constexpr int K = VPT * kNT * 4;
-    __shared__ float lds[VPT * (kNT / 32)];
-    const int64_t row = blockIdx.x;
-    const int t = threadIdx.x;
-    float raw[VPT][4], part[VPT];
+                                                                 uint16_t* __restrict__ out, int64_t m) {
+    constexpr int K = NCH * 512;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= m) return;
+    float raw[NCH][8], part[NCH][2];
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int col = (t + j * kNT) * 4;
-        float hv[4], ov[4], gv[4];
-        load4(h + row * K + col, hv);
-        load4(o + row * K + col, ov);
-        load4(gate + col, gv);
+    for (int c = 0; c < NCH; ++c) {
+        const int col = c * 512 + lane * 8;
+        float hv[8], ov[8], gv[8];
+        load8f(h + row * K + col, hv);
+        load8f(o + row * K + col, ov);
+        load8f(gate + col, gv);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) raw[j][e] = __builtin_fmaf(ov[e], gv[e], hv[e]);
-        part[j] = partial_plain(raw[j]);
+        for (int e = 0; e < 8; ++e) raw[c][e] = __builtin_fmaf(ov[e], gv[e], hv[e]);
+        part[c][0] = partial_plain(&raw[c][0]);
+        part[c][1] = partial_plain(&raw[c][4]);
     }
-    const float mean = RowTree<VPT>::reduce(part, lds) / (float)K;
+    const float mean = row_tree<NCH>(part) / (float)K;
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        float sq[4];
+    for (int c = 0; c < NCH; ++c) {
+        float sq[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            float dv = raw[j][e] - mean;
+        for (int e = 0; e < 8; ++e) {
+            float dv = raw[c][e] - mean;
             sq[e] = dv * dv;
         }
-        part[j] = partial_plain(sq);
+        part[c][0] = partial_plain(&sq[0]);
+        part[c][1] = partial_plain(&sq[4]);
     }
-    const float inv = rsqrt_rn(RowTree<VPT>::reduce(part, lds) / (float)K + eps);
+    const float inv = rsqrt_rn(row_tree<NCH>(part) / (float)K + eps);
 #pragma unroll
-    for (int j = 0; j < VPT; ++j) {
-        const int col = (t + j * kNT) * 4;
-        float gv[4], bv[4], r[4];
-        load4(gamma + col, gv);
-        load4(beta + col, bv);
+    for (int c = 0; c < NCH; ++c) {
+        const int col = c * 512 + lane * 8;
+        float gv[8], bv[8], r[8];
+        load8f(gamma + col, gv);
+        load8f(beta + col, bv);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = __builtin_fmaf((raw[j][e] - mean) * inv, gv[e], bv[e]);
-        store4(out + row * K + col, r);
+        for (int e = 0; e < 8; ++e) r[e] = __builtin_fmaf((raw[c][e] - mean) * inv, gv[e], bv[e]);
+        store8h(out + row * K + col, r);
     }
 }
 
@@ -232,19 +236,19 @@ static int residual_quant_common(const uint16_t* h, const uint16_t* o, const uin
     H3V_REQUIRE(h && o && g && w && h_out && q && scale, "%s: null pointer argument", what);
     int rc = check_row_width(what, m, k);
     if (rc) return rc;
-    H3V_REQUIRE(aligned(h, 8) && aligned(o, 8) && aligned(g, 8) && aligned(w, 8) && aligned(h_out, 8) && aligned(q, 4),
-                "%s: pointers must be 8-byte aligned", what);
+    H3V_REQUIRE(aligned(h, 16) && aligned(o, 16) && aligned(g, 16) && aligned(w, 16) && aligned(h_out, 16) && aligned(q, 8),
+                "%s: fp16 pointers must be 16-byte and q 8-byte aligned", what);
     H3V_REQUIRE(h_out == h || (h_out + m * k <= o || o + m * k <= h_out),
                 "%s: h_out must not overlap o", what);
-    dim3 grid((unsigned)m), block(kNT);
+    dim3 grid((unsigned)((m + kRowsPerBlock - 1) / kRowsPerBlock)), block(kNT);
     if (w16) {
-        if (k == 1024) hipLaunchKernelGGL((residual_rms_quant_kernel<1, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale);
-        else if (k == 2048) hipLaunchKernelGGL((residual_rms_quant_kernel<2, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale);
-        else hipLaunchKernelGGL((residual_rms_quant_kernel<4, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale);
+        if (k == 1024) hipLaunchKernelGGL((residual_rms_quant_kernel<2, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
+        else if (k == 2048) hipLaunchKernelGGL((residual_rms_quant_kernel<4, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
+        else hipLaunchKernelGGL((residual_rms_quant_kernel<8, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
     } else {
-        if (k == 1024) hipLaunchKernelGGL((residual_rms_quant_kernel<1, Recipe::Plain>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale);
-        else if (k == 2048) hipLaunchKernelGGL((residual_rms_quant_kernel<2, Recipe::Plain>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale);
-        else hipLaunchKernelGGL((residual_rms_quant_kernel<4, Recipe::Plain>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale);
+        if (k == 1024) hipLaunchKernelGGL((residual_rms_quant_kernel<2, Recipe::Plain>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
+        else if (k == 2048) hipLaunchKernelGGL((residual_rms_quant_kernel<4, Recipe::Plain>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
+        else hipLaunchKernelGGL((residual_rms_quant_kernel<8, Recipe::Plain>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
     }
     return launch_status(what);
 }
@@ -265,12 +269,12 @@ int h3v_rms_fp16(const uint16_t* x, const uint16_t* gamma, float eps, int64_t m,
     H3V_REQUIRE(x && gamma && out, "%s: null pointer argument", what);
     int rc = check_row_width(what, m, k);
     if (rc) return rc;
-    H3V_REQUIRE(aligned(x, 8) && aligned(gamma, 8) && aligned(out, 8), "%s: pointers must be 8-byte aligned", what);
+    H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(out, 16), "%s: pointers must be 16-byte aligned", what);
     H3V_REQUIRE(out + m * k <= x || x + m * k <= out, "%s: output must own separate storage", what);
-    dim3 grid((unsigned)m), block(kNT);
-    if (k == 1024) hipLaunchKernelGGL((rms_fp16_kernel<1>), grid, block, 0, stream, x, gamma, eps, out);
-    else if (k == 2048) hipLaunchKernelGGL((rms_fp16_kernel<2>), grid, block, 0, stream, x, gamma, eps, out);
-    else hipLaunchKernelGGL((rms_fp16_kernel<4>), grid, block, 0, stream, x, gamma, eps, out);
+    dim3 grid((unsigned)((m + kRowsPerBlock - 1) / kRowsPerBlock)), block(kNT);
+    if (k == 1024) hipLaunchKernelGGL((rms_fp16_kernel<2>), grid, block, 0, stream, x, gamma, eps, out, m);
+    else if (k == 2048) hipLaunchKernelGGL((rms_fp16_kernel<4>), grid, block, 0, stream, x, gamma, eps, out, m);
+    else hipLaunchKernelGGL((rms_fp16_kernel<8>), grid, block, 0, stream, x, gamma, eps, out, m);
     return launch_status(what);
 }
 
@@ -281,15 +285,15 @@ int h3v_residual_layernorm(const uint16_t* h, const uint16_t* o, const uint16_t*
     H3V_REQUIRE(h && o && gate && gamma && beta && out, "%s: null pointer argument", what);
     int rc = check_row_width(what, m, k);
     if (rc) return rc;
-    H3V_REQUIRE(aligned(h, 8) && aligned(o, 8) && aligned(gate, 8) && aligned(gamma, 8) && aligned(beta, 8) &&
-                    aligned(out, 8),
-                "%s: pointers must be 8-byte aligned", what);
+    H3V_REQUIRE(aligned(h, 16) && aligned(o, 16) && aligned(gate, 16) && aligned(gamma, 16) && aligned(beta, 16) &&
+                    aligned(out, 16),
+                "%s: pointers must be 16-byte aligned", what);
     H3V_REQUIRE((out + m * k <= h || h + m * k <= out) && (out + m * k <= o || o + m * k <= out),
                 "%s: output must own separate storage", what);
-    dim3 grid((unsigned)m), block(kNT);
-    if (k == 1024) hipLaunchKernelGGL((residual_layernorm_kernel<1>), grid, block, 0, stream, h, o, gate, gamma, beta, eps, out);
-    else if (k == 2048) hipLaunchKernelGGL((residual_layernorm_kernel<2>), grid, block, 0, stream, h, o, gate, gamma, beta, eps, out);
-    else hipLaunchKernelGGL((residual_layernorm_kernel<4>), grid, block, 0, stream, h, o, gate, gamma, beta, eps, out);
+    dim3 grid((unsigned)((m + kRowsPerBlock - 1) / kRowsPerBlock)), block(kNT);
+    if (k == 1024) hipLaunchKernelGGL((residual_layernorm_kernel<2>), grid, block, 0, stream, h, o, gate, gamma, beta, eps, out, m);
+    else if (k == 2048) hipLaunchKernelGGL((residual_layernorm_kernel<4>), grid, block, 0, stream, h, o, gate, gamma, beta, eps, out, m);
+    else hipLaunchKernelGGL((residual_layernorm_kernel<8>), grid, block, 0, stream, h, o, gate, gamma, beta, eps, out, m);
     return launch_status(what);
 }
 

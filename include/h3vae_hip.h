@@ -30,9 +30,8 @@ extern "C" {
 #define H3V_EINVAL 1   /* shape / dtype / alignment / contract violation */
 #define H3V_ELAUNCH 2  /* the HIP runtime rejected a launch */
 
-#ifndef __HIP_PLATFORM_AMD__
+/* The same typedef as the HIP runtime's own; repeating it is valid C11 and C++. */
 typedef struct ihipStream_t* hipStream_t;
-#endif
 
 /* ABI version of the loaded library (H3V_ABI_VERSION). */
 int h3v_abi_version(void);
@@ -54,6 +53,14 @@ int h3v_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* q, floa
  * Replaces opt/int8_swiglu_fused.py:22-38 (`quant`) / :52-65 (`quantize_swiglu`). */
 int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* q, float* scale,
                          hipStream_t stream);
+
+/* Device self-test of the fast quotients the quantizers use instead of IEEE
+ * division (no counterpart in the reference; it backs the bit-exactness claim).
+ * counts: 3 uint32 of device memory, overwritten with the number of mismatches
+ * against IEEE division: [0] fp32 quotients and [1] int8 codes over every fp16
+ * numerator (infinities excluded) and every finite positive fp16 divisor, [2]
+ * SiLU over every fp16 argument.  All three are zero on a correct build. */
+int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream);
 
 /* ---- INT8 GEMMs (int32 accumulation on MFMA) ---------------------------
  * acc[m, n] = sum_k a[m, k] * w[n, k]; a: int8 [m, k], w: int8 [n, k], both

@@ -31,7 +31,7 @@ def _row_quant_gpu(ops, x):
 
 
 @pytest.mark.parametrize("m,k", [(1, 2048), (17, 2048), (129, 1024), (7188, 2048), (33, 8192), (5, 5), (3, 40),
-                                 (2, 16384)])
+                                 (2, 16384), (6, 4096), (9, 512)])
 def test_row_quant_matches_oracle(ops, oracle, m, k):
     gen = _gen(m * 31 + k)
     x = torch.randn(m, k, generator=gen).half()
@@ -49,10 +49,12 @@ def test_row_quant_matches_oracle(ops, oracle, m, k):
         assert (q[1] == -128).all() and s[1] == np.float32(1e-30)
 
 
-@pytest.mark.parametrize("m,k", [(1, 8192), (17, 4096), (129, 8192), (4, 5)])
-def test_swiglu_row_quant_matches_oracle(ops, oracle, m, k):
+@pytest.mark.parametrize("m,k,scale", [(1, 8192, 3.0), (17, 4096, 3.0), (129, 8192, 3.0), (4, 5, 3.0), (6, 1024, 3.0),
+                                       (7, 2048, 400.0)])
+def test_swiglu_row_quant_matches_oracle(ops, oracle, m, k, scale):
+    # scale 400: |gate| > 80 takes the IEEE SiLU path and products overflow to inf (amax inf rows)
     gen = _gen(k + m)
-    x = (torch.randn(m, 2 * k, generator=gen) * 3).half()
+    x = (torch.randn(m, 2 * k, generator=gen) * scale).half()
     q = torch.empty((m, k), dtype=torch.int8, device=DEV)
     s = torch.empty(m, dtype=torch.float32, device=DEV)
     xd = x.to(DEV)
@@ -201,3 +203,11 @@ def test_tensor_quant_reference_kats(ops):
     q, s = _tensor_quant_gpu(ops, x)
     assert s == 1.0
     assert q.tolist() == [-127, -1, -2, 0, 1, 2, 127]
+
+
+def test_fast_quotients_match_ieee_division_exhaustively(ops):
+    """The quantizers' reciprocal + Newton quotient equals IEEE division on every operand they see."""
+    counts = torch.full((3,), 7, dtype=torch.int32, device=DEV)
+    ops.hip.call("h3v_selftest_fast_div", ops.hip.ptr(counts), ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    assert counts.tolist() == [0, 0, 0], f"fast quotient mismatches (div, q, silu): {counts.tolist()}"
