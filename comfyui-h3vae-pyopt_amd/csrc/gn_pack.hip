@@ -348,9 +348,12 @@ __global__ __launch_bounds__(kNT) void build_lut(const uint32_t* __restrict__ am
     lut[code] = (int8_t)e3_quant(rt16(silu(h2f((uint16_t)code))), s);
 }
 
-// PASS 1 through the table.  The grid stride is a multiple of C/8, so each
-// thread keeps one 8-channel slice (gamma, beta, pre-bias, groups) for the
-// whole loop; the (mean, rstd) pairs are reloaded when the frame changes.
+// PASS 1 through the table.  Each block walks whole padded output rows
+// (frame, padded row): the source row follows from the row index alone, so the
+// only per-vector index arithmetic is a shift by C/8 and a reflect of the
+// column.  256 threads stride a row in steps that are a multiple of C/8, so each
+// thread keeps one 8-channel slice (gamma, beta, pre-bias, groups) for the whole
+// kernel; the (mean, rstd) pairs are reloaded when the frame changes.
 template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict__ x,
                                                      const uint16_t* __restrict__ pre_bias,
@@ -361,6 +364,8 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
                                                      float* __restrict__ scale) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
+    constexpr int LOG_TPP = TPP == 16 ? 4 : 5;
+    static_assert((1 << LOG_TPP) == TPP, "C/8 is a power of two");
     constexpr int NG = 8 / CG > 1 ? 8 / CG : 1;    // groups touched by one 8-channel slice
     __shared__ __attribute__((aligned(16))) int8_t lut[65536];
     for (int i = threadIdx.x; i < 65536 / 16; i += kNT)
@@ -369,10 +374,9 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
     __syncthreads();
 
     const int hp = h + 2, wp = w + 2;
-    const int64_t nvec = (int64_t)(d + 2) * hp * wp * TPP;
-    const int64_t stride = (int64_t)gridDim.x * kNT;
-    const int64_t v0 = (int64_t)blockIdx.x * kNT + threadIdx.x;
-    const int cv = (int)(v0 % TPP);
+    const int nrow = (d + 2) * hp;
+    const int rowvec = wp * TPP;                    // 8-channel vectors per padded row
+    const int cv = threadIdx.x & (TPP - 1);
     float gm[8], bt[8], pb[8] = {};
     load8(gamma + cv * 8, gm);
     load8(beta + cv * 8, bt);
@@ -380,41 +384,35 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
     const int g0 = cv * 8 / CG;
     int tcur = -1;
     float mean[NG], rstd[NG];
-    // U independent vectors per iteration: their loads are all issued before
-    // any is used, so each lane keeps U 16-byte reads in flight (only 8 waves
-    // fit on a CU next to the 64 KB table).
-    constexpr int U = 4;
-    for (int64_t base = v0; base < nvec; base += U * stride) {
-        u16x8 xv[U];
-        int tt[U];
+    constexpr int U = 4;   // independent 16-byte loads in flight per lane
+    for (int row = blockIdx.x; row < nrow; row += gridDim.x) {
+        const int t = row / hp - 2;
+        const int ii = row - (t + 2) * hp;
+        int8_t* dst = q + (int64_t)row * rowvec * 8;
+        if (t < 0) {   // causal zero frames
+            for (int j = threadIdx.x; j < rowvec; j += kNT) *reinterpret_cast<uint2*>(dst + (int64_t)j * 8) = make_uint2(0u, 0u);
+            continue;
+        }
+        if (t != tcur) {
+            tcur = t;
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t vi = base + u * stride;
-            const int64_t pix = vi / TPP;
-            const int jj = (int)(pix % wp);
-            const int64_t r = pix / wp;
-            const int ii = (int)(r % hp);
-            tt[u] = (vi < nvec) ? (int)(r / hp) - 2 : -1;
-            if (tt[u] >= 0) {
-                const int si = reflect(ii - 1, h), sj = reflect(jj - 1, w);
-                xv[u] = *reinterpret_cast<const u16x8*>(x + (((int64_t)tt[u] * h + si) * w + sj) * C + cv * 8);
+            for (int k = 0; k < NG; ++k) {
+                mean[k] = stats[(t * kGroups + g0 + k) * 2];
+                rstd[k] = stats[(t * kGroups + g0 + k) * 2 + 1];
             }
         }
+        const uint16_t* src = x + ((int64_t)t * h + reflect(ii - 1, h)) * w * C + cv * 8;
+        for (int j0 = threadIdx.x; j0 < rowvec; j0 += U * kNT) {
+            u16x8 xv[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int64_t vi = base + u * stride;
-            if (vi >= nvec) break;
-            const int t = tt[u];
-            uint32_t lo = 0, hi = 0;
-            if (t >= 0) {
-                if (t != tcur) {
-                    tcur = t;
+            for (int u = 0; u < U; ++u) {
+                const int j = j0 + u * kNT;
+                if (j < rowvec) xv[u] = *reinterpret_cast<const u16x8*>(src + (int64_t)reflect((j >> LOG_TPP) - 1, w) * C);
+            }
 #pragma unroll
-                    for (int k = 0; k < NG; ++k) {
-                        mean[k] = stats[(t * kGroups + g0 + k) * 2];
-                        rstd[k] = stats[(t * kGroups + g0 + k) * 2 + 1];
-                    }
-                }
+            for (int u = 0; u < U; ++u) {
+                const int j = j0 + u * kNT;
+                if (j >= rowvec) break;
                 int code[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -423,10 +421,10 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
                     const int k = (NG > 1) ? e / CG : 0;
                     code[e] = f2h(((ve - mean[k]) * rstd[k]) * gm[e] + bt[e]);
                 }
-                lo = pack4(lut[code[0]], lut[code[1]], lut[code[2]], lut[code[3]]);
-                hi = pack4(lut[code[4]], lut[code[5]], lut[code[6]], lut[code[7]]);
+                const uint32_t lo = pack4(lut[code[0]], lut[code[1]], lut[code[2]], lut[code[3]]);
+                const uint32_t hi = pack4(lut[code[4]], lut[code[5]], lut[code[6]], lut[code[7]]);
+                *reinterpret_cast<uint2*>(dst + (int64_t)j * 8) = make_uint2(lo, hi);
             }
-            *reinterpret_cast<uint2*>(q + vi * 8) = make_uint2(lo, hi);
         }
     }
 }
