@@ -24,6 +24,8 @@
 // XOR-swizzled in 16-byte chunks so fragment reads are bank-conflict free.
 // Workgroup ids are remapped so that each XCD (own L2) walks a contiguous,
 // M-grouped range of tiles.
+#include <type_traits>
+
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
@@ -125,10 +127,13 @@ __device__ __forceinline__ float g1_value(int32_t acc, float sx, float sw, const
     return bias ? __builtin_fmaf(v, sw, h2f(bias[col])) : v * sw;
 }
 
-// The same epilogue with the weight scale and bias already in registers.
-__device__ __forceinline__ float g1_reg(int32_t acc, float sx, float sw, bool has_bias, uint16_t b) {
+// The same epilogue with the weight scale and bias already in registers; the
+// bias presence is a compile-time choice so no per-element select is emitted.
+template <bool HAS_BIAS>
+__device__ __forceinline__ float g1_reg(int32_t acc, float sx, float sw, uint16_t b) {
     float v = (float)acc * sx;
-    return has_bias ? __builtin_fmaf(v, sw, h2f(b)) : v * sw;
+    if constexpr (HAS_BIAS) return __builtin_fmaf(v, sw, h2f(b));
+    else return v * sw;
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -477,6 +482,9 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
             sxr[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
         }
         lds_barrier();   // every wave has finished reading operand fragments
+        // one instantiation per bias presence (uniform per launch)
+        auto convert = [&](auto hb) {
+        constexpr bool HB = decltype(hb)::value;
         if constexpr (EP == Epi::SwiGLU) {
 #pragma unroll
             for (int j = 0; j < FN / 2; ++j) {
@@ -493,8 +501,8 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
                         u16x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            float g = rt16(g1_reg(acc[i][2 * j][q4 * 4 + e], sxr[i], swg[e], has_bias, bg[e]));
-                            float u = rt16(g1_reg(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], swu[e], has_bias, bu[e]));
+                            float g = rt16(g1_reg<HB>(acc[i][2 * j][q4 * 4 + e], sxr[i], swg[e], bg[e]));
+                            float u = rt16(g1_reg<HB>(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], swu[e], bu[e]));
                             v[e] = f2h(silu(g) * u);
                         }
                         put(wm * WM + i * 32 + mrow, tc, v);
@@ -515,12 +523,15 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
                     for (int i = 0; i < FM; ++i) {
                         u16x4 v;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg(acc[i][j][q4 * 4 + e], sxr[i], swv[e], has_bias, bv[e]));
+                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], swv[e], bv[e]));
                         put(wm * WM + i * 32 + mrow, tc, v);
                     }
                 }
             }
         }
+        };
+        if (has_bias) convert(std::true_type{});
+        else convert(std::false_type{});
         lds_barrier();   // the output tile is complete in LDS
         const int gcol0 = (EP == Epi::SwiGLU) ? tn * (BN / 2) : n0;
         uint16_t* out = static_cast<uint16_t*>(p.out);

@@ -27,10 +27,7 @@ __device__ __forceinline__ float rt16(float f) { return (float)(f16)f; }
 // LN2_HI has 15 significant bits so n*LN2_HI is exact; |r| <= 0.35 keeps the
 // truncation error below 6e-9 relative; error <= 2 ulp against float64.
 // The same operation sequence is the CPU oracle's ora_expf.
-__device__ __forceinline__ float exp_f32(float x) {
-    if (x != x) return x;
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (x < -103.972084045410156f) return 0.0f;
+__device__ __forceinline__ float exp_f32_core(float x) {   // finite x in [-103.97, 88.72]
     const float LOG2E = 0x1.715476p+0f;
     const float LN2_HI = 0x1.62e4p-1f;
     const float LN2_LO = 0x1.7f7d1cp-20f;
@@ -46,6 +43,12 @@ __device__ __forceinline__ float exp_f32(float x) {
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
     return __builtin_amdgcn_ldexpf(p, (int)n);
+}
+__device__ __forceinline__ float exp_f32(float x) {
+    if (x != x) return x;
+    if (x > 88.72283935546875f) return __builtin_inff();
+    if (x < -103.972084045410156f) return 0.0f;
+    return exp_f32_core(x);
 }
 
 // SiLU written as the reference writes it: z / (1 + exp(-z)).
@@ -69,7 +72,7 @@ __device__ __forceinline__ float div_newton(float a, float b, float r) {
 // finite normal number; the IEEE path keeps the special cases (|z| large, inf, NaN).
 __device__ __forceinline__ float silu_fast(float z) {
     if (__builtin_fabsf(z) <= 80.0f) {
-        const float den = 1.0f + exp_f32(-z);
+        const float den = 1.0f + exp_f32_core(-z);
         return div_newton(z, den, __builtin_amdgcn_rcpf(den));
     }
     return silu(z);
