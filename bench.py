@@ -527,7 +527,7 @@ def main():
         "int8_tops_step": round((enc_ops + dec_ops) / sec_per_step / 1e12, 1),
         "int8_mfma_frac_step": round((enc_ops + dec_ops) / sec_per_step / 1e12 / INT8_PEAK_TOPS, 4),
         "roofline": {
-            "kernel": "gemm_i8_mfma<512,128,128,4,2,2,2,Conv,Dequant> (stage-0 conv C128->128, [1,128,19,258,258] int8)",
+            "kernel": "conv3_halo_i8<256,Dequant> (stage-0 conv C128->128, [1,128,19,258,258] int8)",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": INT8_PEAK_TOPS,

@@ -207,6 +207,147 @@ __device__ __forceinline__ void wait_stage(int ahead) {
     else wait_vmcnt<0>();
 }
 
+// Epilogue of the tiled kernels: the wave's (BM/WGM) x (BN/WGN) block of
+// int32 accumulators of the workgroup's BM x BN tile at (m0, n0), weight tile
+// tn, is dequantized (or stored raw) to the output.  LDS_BYTES of LDS (the
+// operand rings, idle by now) stage the fp16 tile.
+template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP>
+__device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
+                                           int8_t* smem, int m0, int n0, int tn) {
+    constexpr int NW = WGM * WGN;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int RING = LDS_BYTES;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
+    const int wm = wave / WGN, wn = wave % WGN;
+    // Epilogue.  The MFMAs compute W * A^T blocks, so in the v_mfma 32x32 result
+    // layout lane l holds output row m = lane&31 of the block and, in register
+    // r, output column n = (r/4)*8 + (l/32)*4 + r%4: four consecutive columns per
+    // register quad.
+    const int mrow = lane & 31;
+    const int ncol = (lane >> 5) * 4;
+    if constexpr (EP == Epi::Int32) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int c0 = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
+                if (c0 >= p.N) continue;
+                const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    const int row = m0 + wm * WM + i * 32 + mrow;
+                    if (row >= p.M) continue;
+                    int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
+                    if (full) {
+                        v4i v = {acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
+                        *reinterpret_cast<v4i*>(dst) = v;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
+                    }
+                }
+            }
+        }
+    } else {
+        // fp16 outputs go through LDS: each wave converts its block into the
+        // (now idle) LDS ring, laid out as the workgroup's output tile
+        // [BM][OUTW] with 16-byte chunks XOR-swizzled by row, and then every
+        // thread stores 16-byte pieces of whole tile rows, so each store
+        // instruction writes complete 128-byte lines (direct 8-byte stores from
+        // the MFMA layout touch 32 partial lines per instruction and cost about
+        // a third of the kernel).
+        constexpr int OUTW = (EP == Epi::SwiGLU) ? BN / 2 : BN;
+        constexpr int RCH = OUTW / 8;
+        constexpr int SWM = (RCH < 32 ? RCH : 32) - 1;
+        static_assert(RCH >= 8 && BM * OUTW * 2 <= RING, "output tile must fit the LDS ring");
+        int8_t* ep = smem;
+        auto put = [&](int r, int c, const u16x4& v) {   // c: tile column, a multiple of 4
+            const int ch = c >> 3;
+            *reinterpret_cast<u16x4*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4) + ((c & 4) << 1)) = v;
+        };
+        const bool has_bias = p.bias != nullptr;
+        float sxr[FM];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+            const int row = m0 + wm * WM + i * 32 + mrow;
+            sxr[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
+        }
+        lds_barrier();   // every wave has finished reading operand fragments
+        // one instantiation per bias presence (uniform per launch)
+        auto convert = [&](auto hb) {
+        constexpr bool HB = decltype(hb)::value;
+        if constexpr (EP == Epi::SwiGLU) {
+#pragma unroll
+            for (int j = 0; j < FN / 2; ++j) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int tc = (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
+                    const int c0 = tn * (BN / 2) + tc;
+                    f32x4 swg, swu;
+                    u16x4 bg, bu;
+                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swg, bg);
+                    load_col4(p, p.N + (c0 < p.N ? c0 : p.N - 1), 2 * p.N, swu, bu);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        u16x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float g = rt16(g1_reg<HB>(acc[i][2 * j][q4 * 4 + e], sxr[i], swg[e], bg[e]));
+                            float u = rt16(g1_reg<HB>(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], swu[e], bu[e]));
+                            v[e] = f2h(silu(g) * u);
+                        }
+                        put(wm * WM + i * 32 + mrow, tc, v);
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j) {
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int tc = wn * WN + j * 32 + q4 * 8 + ncol;
+                    const int c0 = n0 + tc;
+                    f32x4 swv;
+                    u16x4 bv;
+                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swv, bv);
+#pragma unroll
+                    for (int i = 0; i < FM; ++i) {
+                        u16x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], swv[e], bv[e]));
+                        put(wm * WM + i * 32 + mrow, tc, v);
+                    }
+                }
+            }
+        }
+        };
+        if (has_bias) convert(std::true_type{});
+        else convert(std::false_type{});
+        lds_barrier();   // the output tile is complete in LDS
+        const int gcol0 = (EP == Epi::SwiGLU) ? tn * (BN / 2) : n0;
+        uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll 4
+        for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
+            const int r = idx / RCH, ch = idx - r * RCH;
+            const int grow = m0 + r, gcol = gcol0 + ch * 8;
+            if (grow >= p.M || gcol >= p.N) continue;
+            const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
+            uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+            if (p.vec_out && gcol + 8 <= p.N) {
+                *reinterpret_cast<u16x8*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gcol + e < p.N) dst[e] = v[e];
+            }
+        }
+    }
+}
+
 // BM x BN x BK workgroup tile, WGM x WGN waves of (BM/WGM) x (BN/WGN).  A and B
 // stream through separate LDS rings of NSA and NSB slots.  Loads are issued B
 // before A for each stage, so with NSB = 2 < NSA the barrier that publishes
@@ -240,7 +381,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int wm = wave / WGN, wn = wave % WGN;
 
     int tm, tn;
@@ -427,130 +568,220 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         }
     }
 
-    // Epilogue.  The MFMAs compute W * A^T blocks, so in the v_mfma 32x32 result
-    // layout lane l holds output row m = lane&31 of the block and, in register
-    // r, output column n = (r/4)*8 + (l/32)*4 + r%4: four consecutive columns per
-    // register quad.
-    const int mrow = lane & 31;
-    const int ncol = (lane >> 5) * 4;
-    if constexpr (EP == Epi::Int32) {
+    write_tile<BM, BN, WGM, WGN, RING, EP>(p, acc, smem, m0, n0, tn);
+}
+
+// LDS of conv3_halo_i8<WO>: two stages of window + weights, or the fp16 output tile if larger.
+constexpr int halo_lds_bytes(int wo) {
+    const int hb = ((512 / wo + 2) * ((wo + 2 + 15) / 16 * 16) * 32 + 4095) / 4096 * 4096;
+    const int ring = 2 * (hb + 9 * 128 * 32);
+    return ring > 512 * 128 * 2 ? ring : 512 * 128 * 2;
+}
+
+// Stride-1 3x3x3 convolution with the input window of a tile held in LDS.
+//
+// A tile is BM = 512 consecutive output voxels = RO = 512 / WO whole output
+// rows of one frame, times BN = 128 output channels.  For one depth tap kd and
+// one 32-channel slice the nine (kh, kw) taps of every voxel in the tile read
+// the same RO + 2 input rows, so a stage stages that window once ([RO + 2]
+// rows of WO + 2 pixels, 32 bytes each) together with the nine taps' weights
+// ([9][128][32]) and runs 9 MFMA K steps on it; the implicit-GEMM kernel above
+// fetches every input row up to nine times per depth tap instead.  LDS-DMA
+// instructions, whose issue is what holds the matrix pipe back, drop 2.6x.
+// Stages run kd-major (kd0..2) then channel slice, double-buffered: one
+// barrier per 9 taps.  Causal-zero depth taps (output frames 0 and 1 of the
+// fused producer's input) are skipped per tile; the tile is one frame.
+//
+// Window layout: pixel (row hr, column px) at LDS pixel hr * HPL + px with
+// HPL = WO + 2 rounded up to 16, so a (kh, kw) shift of the window is a
+// uniform offset for kh and a per-lane one for kw; each pixel's two 16-byte
+// halves are swapped when (px >> 3) & 1, which keeps the 16-lane fragment
+// reads (16 consecutive pixels, one half) on 16 distinct 16-byte bank groups.
+// Weight rows (tap, n) are swizzled the same way by (n >> 3) & 1.
+template <int WO, Epi EP>
+__global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
+    constexpr int BM = 512, BN = 128, WGM = 4, WGN = 2, NWD = 4;
+    constexpr int WM = BM / WGM, WN = BN / WGN;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int RO = BM / WO;                               // output rows per tile
+    constexpr int HR = RO + 2;                                // window rows
+    constexpr int HPL = (WO + 2 + 15) / 16 * 16;              // LDS pixels per window row
+    constexpr int ROWB = HPL * 32;                            // LDS bytes per window row
+    constexpr int HB = (HR * ROWB + 4095) / 4096 * 4096;      // window bytes (whole instructions per issuing wave)
+    constexpr int WB = 9 * BN * 32;                           // weight bytes of a stage
+    constexpr int STAGE = HB + WB;
+    constexpr int NH = HB / 1024 / NWD, NWT = WB / 1024 / NWD; // DMA instructions per issuing wave and stage
+    constexpr int LDS = 2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2;
+    static_assert(WO == 64 || WO == 128 || WO == 256, "output width");
+    static_assert(LDS <= 163840, "LDS");
+    static_assert(LDS == halo_lds_bytes(WO), "host and kernel LDS sizes");
+    static_assert(NH + NWT < 64, "outstanding DMA must fit vmcnt");
+
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
+    const int wm = wave / WGN, wn = wave % WGN;
+
+    // tile -> (row block, frame, weight tile); the weight tiles of one window are
+    // adjacent, then the frames of one row block (they share input rows in L2)
+    int id = xcd_remap(blockIdx.x, gridDim.x);
+    const int tn = id % p.tiles_n;
+    id /= p.tiles_n;
+    const int nfr = p.M / (p.Ho * WO);                        // batch * Do
+    const int fr = id % nfr;
+    const int rb = id / nfr;
+    const int od = fr % p.Do;
+    const int bi = fr / p.Do;
+    const int oh0 = rb * RO;
+    const int m0 = (fr * p.Ho + oh0) * WO;
+    const int n0 = tn * BN;
+    const int CQ = p.C / 32;
+    const int kd0 = (p.causal_skip && od < 2) ? 2 - od : 0;
+    const int nst = (3 - kd0) * CQ;                           // even: C % 64 == 0
+    const uint32_t frame_bytes = (uint32_t)p.Hp * p.Wp * p.C;
+
+    const bool dma_wave = wave < NWD;
+    const int dw = dma_wave ? wave : 0;
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)p.a, 0, (int)p.a_bytes, kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb_ = __builtin_amdgcn_make_buffer_rsrc((void*)p.b, 0, (int)p.b_bytes, kRsrcWord3);
+    // per-lane DMA source offsets; the stage adds kd and the channel slice as the uniform offset
+    uint32_t hoff[NH], woff[NWT];
+    {
+        const uint32_t tile_base = (uint32_t)(((int64_t)(bi * p.Dp + od) * p.Hp + oh0) * p.Wp * p.C);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const int c0 = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
-                if (c0 >= p.N) continue;
-                const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
-#pragma unroll
-                for (int i = 0; i < FM; ++i) {
-                    const int row = m0 + wm * WM + i * 32 + mrow;
-                    if (row >= p.M) continue;
-                    int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
-                    if (full) {
-                        v4i v = {acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
-                        *reinterpret_cast<v4i*>(dst) = v;
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
-                    }
-                }
-            }
+        for (int j = 0; j < NH; ++j) {
+            const int s16 = (dw + NWD * j) * 64 + lane;       // 16-byte slot of the window buffer
+            const int pix = s16 >> 1;
+            int hr = pix / HPL, px = pix - hr * HPL;
+            const int half = (s16 & 1) ^ ((px >> 3) & 1);
+            // padding slots load a valid in-window pixel; they are never read
+            if (hr >= HR) hr = HR - 1;
+            if (px > WO + 1) px = WO + 1;
+            hoff[j] = tile_base + (uint32_t)((hr * p.Wp + px) * p.C + half * 16);
         }
-    } else {
-        // fp16 outputs go through LDS: each wave converts its block into the
-        // (now idle) LDS ring, laid out as the workgroup's output tile
-        // [BM][OUTW] with 16-byte chunks XOR-swizzled by row, and then every
-        // thread stores 16-byte pieces of whole tile rows, so each store
-        // instruction writes complete 128-byte lines (direct 8-byte stores from
-        // the MFMA layout touch 32 partial lines per instruction and cost about
-        // a third of the kernel).
-        constexpr int OUTW = (EP == Epi::SwiGLU) ? BN / 2 : BN;
-        constexpr int RCH = OUTW / 8;
-        constexpr int SWM = (RCH < 32 ? RCH : 32) - 1;
-        static_assert(RCH >= 8 && BM * OUTW * 2 <= RING, "output tile must fit the LDS ring");
-        int8_t* ep = smem;
-        auto put = [&](int r, int c, const u16x4& v) {   // c: tile column, a multiple of 4
-            const int ch = c >> 3;
-            *reinterpret_cast<u16x4*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4) + ((c & 4) << 1)) = v;
-        };
-        const bool has_bias = p.bias != nullptr;
-        float sxr[FM];
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-            const int row = m0 + wm * WM + i * 32 + mrow;
-            sxr[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
-        }
-        lds_barrier();   // every wave has finished reading operand fragments
-        // one instantiation per bias presence (uniform per launch)
-        auto convert = [&](auto hb) {
-        constexpr bool HB = decltype(hb)::value;
-        if constexpr (EP == Epi::SwiGLU) {
-#pragma unroll
-            for (int j = 0; j < FN / 2; ++j) {
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const int tc = (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
-                    const int c0 = tn * (BN / 2) + tc;
-                    f32x4 swg, swu;
-                    u16x4 bg, bu;
-                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swg, bg);
-                    load_col4(p, p.N + (c0 < p.N ? c0 : p.N - 1), 2 * p.N, swu, bu);
-#pragma unroll
-                    for (int i = 0; i < FM; ++i) {
-                        u16x4 v;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            float g = rt16(g1_reg<HB>(acc[i][2 * j][q4 * 4 + e], sxr[i], swg[e], bg[e]));
-                            float u = rt16(g1_reg<HB>(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], swu[e], bu[e]));
-                            v[e] = f2h(silu(g) * u);
-                        }
-                        put(wm * WM + i * 32 + mrow, tc, v);
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < FN; ++j) {
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const int tc = wn * WN + j * 32 + q4 * 8 + ncol;
-                    const int c0 = n0 + tc;
-                    f32x4 swv;
-                    u16x4 bv;
-                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swv, bv);
-#pragma unroll
-                    for (int i = 0; i < FM; ++i) {
-                        u16x4 v;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], swv[e], bv[e]));
-                        put(wm * WM + i * 32 + mrow, tc, v);
-                    }
-                }
-            }
-        }
-        };
-        if (has_bias) convert(std::true_type{});
-        else convert(std::false_type{});
-        lds_barrier();   // the output tile is complete in LDS
-        const int gcol0 = (EP == Epi::SwiGLU) ? tn * (BN / 2) : n0;
-        uint16_t* out = static_cast<uint16_t*>(p.out);
-#pragma unroll 4
-        for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
-            const int r = idx / RCH, ch = idx - r * RCH;
-            const int grow = m0 + r, gcol = gcol0 + ch * 8;
-            if (grow >= p.M || gcol >= p.N) continue;
-            const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
-            uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
-            if (p.vec_out && gcol + 8 <= p.N) {
-                *reinterpret_cast<u16x8*>(dst) = v;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (gcol + e < p.N) dst[e] = v[e];
-            }
+        for (int j = 0; j < NWT; ++j) {
+            const int s16 = (dw + NWD * j) * 64 + lane;
+            const int row = s16 >> 1;                         // tap * 128 + n
+            const int t9 = row >> 7, n = row & 127;
+            const int half = (s16 & 1) ^ ((n >> 3) & 1);
+            woff[j] = (uint32_t)(n0 + n) * (uint32_t)p.K + (uint32_t)(t9 * p.C + half * 16);
         }
     }
+    auto issue = [&](int kd, int cq, int slot) {
+        if (!dma_wave) return;
+        int8_t* base = smem + slot * STAGE;
+        const uint32_t sh = (uint32_t)kd * frame_bytes + (uint32_t)cq * 32;
+        const uint32_t sw = (uint32_t)(kd * 9 * p.C + cq * 32);
+#pragma unroll
+        for (int j = 0; j < NH; ++j) lds_dma16(ra, hoff[j], sh, base + (dw + NWD * j) * 1024);
+#pragma unroll
+        for (int j = 0; j < NWT; ++j) lds_dma16(rb_, woff[j], sw, base + HB + (dw + NWD * j) * 1024);
+    };
+
+    // fragment addresses: lane reads output row (lane & 31) of a 32-row block and
+    // the 16-byte half (lane >> 5) of its pixel / weight row
+    const int frow = lane & 31;
+    const int fhi = lane >> 5;
+    int aaddr[FM][3];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int r = wm * WM + i * 32 + frow;
+        const int orow = r / WO, ow = r % WO;
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw) {
+            const int px = ow + kw;
+            aaddr[i][kw] = (orow * HPL + px) * 32 + ((fhi ^ ((px >> 3) & 1)) << 4);
+        }
+    }
+    int baddr[FN];
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+        const int n = wn * WN + j * 32 + frow;
+        baddr[j] = HB + n * 32 + ((fhi ^ ((n >> 3) & 1)) << 4);
+    }
+
+    v16i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+
+    auto load_frags = [&](int slot, int t9, v4i (&af)[FM], v4i (&bf)[FN]) {
+        const int8_t* s = smem + slot * STAGE;
+        const int kh = t9 / 3, kw = t9 % 3;
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const v4i*>(s + aaddr[i][kw] + kh * ROWB);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const v4i*>(s + baddr[j] + t9 * (BN * 32));
+    };
+    auto mfma_all = [&](const v4i (&af)[FM], const v4i (&bf)[FN]) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    };
+
+    // stage s covers depth tap kd0 + s / CQ and channel slice s % CQ; the issue
+    // position is kept as a running (kd, cq) pair
+    int ikd = kd0, icq = 0;
+    auto issue_next = [&](int slot) {
+        issue(ikd, icq, slot);
+        if (++icq == CQ) {
+            icq = 0;
+            ++ikd;
+        }
+    };
+
+    v4i fa[2][FM], fb[2][FN];
+    issue_next(0);
+    issue_next(1);
+    wait_vmcnt<NH + NWT>();                                   // stage 0 landed, stage 1 may be in flight
+    lds_barrier();
+    load_frags(0, 0, fa[0], fb[0]);
+
+    constexpr int NFRAG = FM + FN;
+    constexpr int NMFMA = FM * FN;
+    // One stage: 9 taps, fragments double-buffered in registers across taps
+    // (and across the stage boundary: the last tap's MFMAs hide the reads of the
+    // next stage's first fragments).  With 9 taps the register buffer parity
+    // flips every stage, so stages are processed in (slot 0, slot 1) pairs.
+    auto run_stage = [&](auto slot_c, int s) {
+        constexpr int SL = decltype(slot_c)::value;
+#pragma unroll
+        for (int t9 = 0; t9 < 9; ++t9) {
+            const int cur = (SL + t9) & 1;
+            if (t9 == 8) {
+                const bool more = s + 1 < nst;
+                if (more) {
+                    wait_vmcnt<0>();                          // stage s+1 landed
+                    lds_barrier();                            // and every wave is done with slot SL
+                    if (s + 2 < nst) issue_next(SL);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_all(fa[cur], fb[cur]);
+                if (more) load_frags(SL ^ 1, 0, fa[cur ^ 1], fb[cur ^ 1]);
+            } else {
+                mfma_all(fa[cur], fb[cur]);
+                load_frags(SL, t9 + 1, fa[cur ^ 1], fb[cur ^ 1]);
+            }
+#pragma unroll
+            for (int g = 0; g < NFRAG; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NFRAG, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    for (int s = 0; s < nst; s += 2) {
+        run_stage(std::integral_constant<int, 0>{}, s);
+        run_stage(std::integral_constant<int, 1>{}, s + 1);
+    }
+
+    write_tile<BM, BN, WGM, WGN, LDS, EP>(p, acc, smem, m0, n0, tn);
 }
 
 // Shape-general path (any K, any channel count, unaligned pointers): one thread
@@ -626,6 +857,41 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     return launch_status(what);
 }
 
+// Stride-1 3x3x3 convolution through conv3_halo_i8: requires C % 64 == 0,
+// N % 128 == 0, Wo in {64, 128, 256} and Ho a multiple of 512 / Wo.
+bool halo_conv_fits(const GemmParams& p) {
+    const bool shape = p.KH == 3 && p.KW == 3 && p.K == 27 * p.C && p.SD == 1 && p.SH == 1 && p.SW == 1 &&
+                       p.C % 64 == 0 && p.N % 128 == 0 && (p.Wo == 64 || p.Wo == 128 || p.Wo == 256) &&
+                       p.Ho % (512 / p.Wo) == 0;
+    return shape && aligned(p.a, 16) && aligned(p.b, 16) && (int64_t)p.Hp * p.Wp * p.C * 3 < ((int64_t)1 << 31);
+}
+
+template <int WO, Epi EP>
+int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
+    p.tiles_m = p.M / 512;
+    p.tiles_n = p.N / 128;
+    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8));
+    p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
+    p.conv_tpf = 0;
+    const int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
+    const int64_t a_bytes = (int64_t)(p.M / ((int64_t)p.Do * p.Ho * p.Wo)) * p.Dp * p.Hp * p.Wp * p.C;
+    const int64_t b_bytes = (int64_t)p.N * p.K;
+    if (a_bytes >= ((int64_t)1 << 32) || b_bytes >= ((int64_t)1 << 31))
+        return fail(H3V_EINVAL, "%s: an operand exceeds the 32-bit offset range (%lld, %lld bytes)", what,
+                    (long long)a_bytes, (long long)b_bytes);
+    p.a_bytes = (uint32_t)a_bytes;
+    p.b_bytes = (uint32_t)b_bytes;
+    constexpr int lds = halo_lds_bytes(WO);
+    static_assert(lds <= 163840, "LDS exceeds 160 KB");
+    auto kernel = &conv3_halo_i8<WO, EP>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, lds,
+                                        hipGetErrorString(attr));
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(512), lds, stream, p);
+    return launch_status(what);
+}
+
 template <AMode AM, Epi EP>
 int launch_generic(GemmParams p, hipStream_t stream, const char* what) {
     int64_t total = (int64_t)p.M * p.N;
@@ -650,6 +916,11 @@ int run_gemm(GemmParams p, hipStream_t stream, const char* what) {
 template <Epi EP>
 int run_conv(GemmParams p, hipStream_t stream, const char* what) {
     const bool al = aligned(p.a, 16) && aligned(p.b, 16);
+    if (halo_conv_fits(p)) {
+        if (p.Wo == 256) return launch_halo<256, EP>(p, stream, what);
+        if (p.Wo == 128) return launch_halo<128, EP>(p, stream, what);
+        return launch_halo<64, EP>(p, stream, what);
+    }
     if (al && p.C % 128 == 0) {
         if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, EP>(p, stream, what);
         return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, EP>(p, stream, what);

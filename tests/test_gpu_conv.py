@@ -43,6 +43,11 @@ CASES = [
     (128, 128, (1, 128, 5, 17, 33), (3, 3, 3), (1, 2, 2)),
     (128, 128, (1, 128, 3, 10, 18), (1, 3, 3), (1, 1, 1)),
     (64, 128, (2, 64, 4, 6, 70), (3, 3, 3), (1, 1, 1)),
+    # window-in-LDS kernel (stride 1, C % 64 == 0, N % 128 == 0, Wo in {64, 128, 256})
+    (64, 128, (1, 64, 4, 4, 258), (3, 3, 3), (1, 1, 1)),
+    (128, 256, (2, 128, 4, 10, 66), (3, 3, 3), (1, 1, 1)),
+    (128, 128, (1, 128, 5, 6, 130), (3, 3, 3), (1, 1, 1)),
+    (256, 128, (1, 256, 3, 6, 130), (3, 3, 3), (1, 1, 1)),
 ]
 
 
@@ -81,17 +86,19 @@ def test_conv_h3_stage0_shape_sampled(ops, oracle):
         assert np.array_equal(acc[:, t:t + 1, :32], want), f"frame {t}"
 
 
+# (d, h, w, c): implicit-GEMM tiles, then the window-in-LDS kernel (Wo = 128)
+@pytest.mark.parametrize("d,h,w,c", [(5, 12, 20, 256), (4, 6, 130, 128)])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_conv_dequant_epilogue(ops, oracle, with_bias):
+def test_conv_dequant_epilogue(ops, oracle, with_bias, d, h, w, c):
     gen = _gen(5)
-    qx = torch.randint(-127, 128, (1, 5, 12, 20, 256), generator=gen, dtype=torch.int8)
-    qw = torch.randint(-127, 128, (256, 27 * 256), generator=gen, dtype=torch.int8)
+    qx = torch.randint(-127, 128, (1, d, h, w, c), generator=gen, dtype=torch.int8)
+    qw = torch.randint(-127, 128, (256, 27 * c), generator=gen, dtype=torch.int8)
     xs = torch.tensor([0.013], dtype=torch.float32)
     ws = (torch.rand(256, generator=gen) * 0.001 + 1e-4).float()
     bias = torch.randn(256, generator=gen).half() if with_bias else None
-    out = torch.empty((1, 3, 10, 18, 256), dtype=torch.float16, device=DEV)
+    out = torch.empty((1, d - 2, h - 2, w - 2, 256), dtype=torch.float16, device=DEV)
     dev = [t.to(DEV) if t is not None else None for t in (qx, xs, qw, ws, bias)]
-    ops.hip.call("h3v_conv3d_i8", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(out), 1, 256, 5, 12, 20, 256, 3, 3, 3, 1,
+    ops.hip.call("h3v_conv3d_i8", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(out), 1, c, d, h, w, 256, 3, 3, 3, 1,
                  1, 1, 0, ops.hip.stream(DEV))
     torch.cuda.synchronize()
     acc = oracle.conv3d_acc(qx.numpy(), qw.numpy(), (3, 3, 3), (1, 1, 1))
