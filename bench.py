@@ -211,6 +211,46 @@ class Workload:
              9.999999747378752e-06, m, d, p(self.final), stream)
 
 
+def mfma_ceiling(torch, hip, wl, stream):
+    """Measured INT8 MFMA ceiling for the stage-0 conv's own operands (h3v_probe_mfma_rate).
+
+    The published peak assumes the top shader clock; under a matrix load the part holds a clock that
+    depends on the power the MFMAs draw, i.e. on the data.  One stage-0 fused layer leaves its quantized
+    input in `wl.q`; the probe multiplies those bytes with the layer's quantized weights from registers
+    (no memory traffic), one workgroup of 8 waves per CU, and reports the rate and the mean clock.
+    """
+    props = torch.cuda.get_device_properties(wl.dev)
+    blocks = int(props.multi_processor_count)
+    wl.norm_conv(wl.x0, 0, wl.a0, 256, 256, stream)
+    a = wl.q[: (wl.t + 2) * 258 * 258 * 128]
+    b = wl.enc_w[0][0]
+    sink = torch.empty(blocks * 512, device=wl.dev, dtype=torch.int32)
+    clocks = torch.empty(2 * blocks, device=wl.dev, dtype=torch.int64)
+    iters = 4000
+    ops = blocks * int(hip.lib().h3v_probe_mfma_ops_per_block(iters))
+    args = (hip.ptr(a), a.numel(), hip.ptr(b), b.numel(), blocks, iters, hip.ptr(sink), hip.ptr(clocks), stream)
+    for _ in range(20):                     # ~0.1 s at the sustained clock before timing
+        hip.call("h3v_probe_mfma_rate", *args)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    e0.record()
+    for _ in range(reps):
+        hip.call("h3v_probe_mfma_rate", *args)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3 / reps
+    ticks = clocks.view(blocks, 2).double().sum(0).tolist()
+    tops = ops / sec / 1e12
+    return {
+        "kernel": "h3v_probe_mfma_rate: register-resident v_mfma_i32_32x32x32_i8, 8 waves per CU, no memory traffic",
+        "data": "stage-0 conv operands: the fused producer's int8 activations x the layer's int8 kaiming weights",
+        "tops": round(tops, 1),
+        "frac_of_peak": round(tops / INT8_PEAK_TOPS, 4),
+        "clock_mhz": round(ticks[0] / ticks[1] * 100.0, 0),
+        "blocks": blocks,
+    }
+
+
 def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
     """BASELINE.json configs 1-4 on their own shapes: mean kernel time and roofline fraction each.
 
@@ -539,6 +579,11 @@ def main():
             "algorithmic_ops_per_launch": conv_useful,
         },
     }
+    log("measuring the MFMA ceiling for the stage-0 conv operands")
+    with torch.inference_mode():
+        ceiling = mfma_ceiling(torch, hip, wl, stream)
+    ceiling["conv_frac_of_ceiling"] = round(achieved / ceiling["tops"], 4)
+    result["mfma_ceiling"] = ceiling
     if not args.no_configs:
         log("timing BASELINE configs 1-4 on their own shapes")
         result["configs"] = config_measurements(torch, hip, kitchen, enc, stream)

@@ -46,12 +46,14 @@ SIGNATURES: dict[str, list] = {
     "h3v_qk_rope": [_P, _P, _P, _I64, _I, _I, _I, _F, _P, _P, _P],
     "h3v_residual_downsample_pack": [_P, _P, _P, _P, _I, _I, _I, _I, _P],
     "h3v_selftest_fast_div": [_P, _P],
+    "h3v_probe_mfma_rate": [_P, _I64, _P, _I64, _I, _I, _P, _P, _P],
 }
 # entry points with a non-int result
 SPECIAL: dict[str, tuple] = {
     "h3v_abi_version": (ctypes.c_int, []),
     "h3v_last_error": (ctypes.c_char_p, []),
     "h3v_gn_norm_pack_workspace_floats": (ctypes.c_int64, [_I, _I, _I]),
+    "h3v_probe_mfma_ops_per_block": (ctypes.c_int64, [_I]),
 }
 
 

@@ -51,7 +51,7 @@ struct GemmParams {
     void* out;
     int64_t ldo;
     int tiles_m, tiles_n;
-    int vec_epi;       // sw (and bias) aligned for 4-column vector loads (and N % 4 == 0 for SwiGLU)
+    int vec_epi;       // sw (and bias) aligned for 4-column vector loads and N % 4 == 0
     int vec_out;       // fp16 output 16-byte aligned with ldo % 8 == 0: 16-byte row stores
     int conv_tpf;      // conv: M tiles per output frame when they do not straddle frames, else 0
     uint32_t a_bytes;  // extents of A and W in bytes (buffer resource ranges, < 4 GiB)
@@ -138,20 +138,32 @@ __device__ __forceinline__ float g1_reg(int32_t acc, float sx, float sw, uint16_
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Weight scales and fp16 bias of 4 consecutive weight rows c..c+3: one 16-byte
-// and one 8-byte load when aligned and in range, else clamped scalar loads.
-__device__ __forceinline__ void load_col4(const GemmParams& p, int c, int limit, f32x4& sw, u16x4& b) {
-    if (p.vec_epi && c + 4 <= limit) {
-        sw = *reinterpret_cast<const f32x4*>(p.sw + c);
-        if (p.bias) b = *reinterpret_cast<const u16x4*>(p.bias + c);
-        else b = u16x4{0, 0, 0, 0};
-        return;
-    }
+// Weight scales and fp16 bias of NQ column quads (4 consecutive weight rows
+// c[q]..c[q]+3 each, c[q] a multiple of 4, below limit[q]), all issued before
+// any is used.  With vec_epi (aligned, limits multiples of 4) a quad is one
+// 16-byte and one 8-byte load, its start clamped to the last full quad;
+// otherwise clamped scalar loads.  Quads past the end load valid neighbours
+// and are never stored.
+template <int NQ, bool HB>
+__device__ __forceinline__ void load_cols(const GemmParams& p, const int (&c)[NQ], const int (&limit)[NQ],
+                                          f32x4 (&sw)[NQ], u16x4 (&b)[NQ]) {
+    if (p.vec_epi) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int ce = c + e < limit ? c + e : limit - 1;
-        sw[e] = p.sw[ce];
-        b[e] = p.bias ? p.bias[ce] : 0;
+        for (int q = 0; q < NQ; ++q) {
+            const int cc = c[q] < limit[q] - 4 ? c[q] : limit[q] - 4;
+            sw[q] = *reinterpret_cast<const f32x4*>(p.sw + cc);
+            if constexpr (HB) b[q] = *reinterpret_cast<const u16x4*>(p.bias + cc);
+            else b[q] = u16x4{0, 0, 0, 0};
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int ce = c[q] + e < limit[q] ? c[q] + e : limit[q] - 1;
+                sw[q][e] = p.sw[ce];
+                b[q][e] = HB ? p.bias[ce] : 0;
+            }
     }
 }
 
@@ -276,28 +288,52 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM /
             const int row = m0 + wm * WM + i * 32 + mrow;
             sxr[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
         }
-        lds_barrier();   // every wave has finished reading operand fragments
         // one instantiation per bias presence (uniform per launch)
         auto convert = [&](auto hb) {
         constexpr bool HB = decltype(hb)::value;
+        // the wave's column parameters go out before the barrier, so their
+        // latency overlaps it: FN * 4 quads (SwiGLU: FN / 2 * 4 gate/up pairs)
+        constexpr int NQ = FN * 4;
+        int qc[NQ], ql[NQ];
+        f32x4 qsw[NQ];
+        u16x4 qb[NQ];
+        if constexpr (EP == Epi::SwiGLU) {
+#pragma unroll
+            for (int j = 0; j < FN / 2; ++j)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int c0 = tn * (BN / 2) + (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
+                    const int q = (j * 4 + q4) * 2;
+                    qc[q] = c0;
+                    ql[q] = p.N;
+                    qc[q + 1] = p.N + c0;
+                    ql[q + 1] = 2 * p.N;
+                }
+        } else {
+#pragma unroll
+            for (int j = 0; j < FN; ++j)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    qc[j * 4 + q4] = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
+                    ql[j * 4 + q4] = p.N;
+                }
+        }
+        load_cols<NQ, HB>(p, qc, ql, qsw, qb);
+        lds_barrier();   // every wave has finished reading operand fragments
         if constexpr (EP == Epi::SwiGLU) {
 #pragma unroll
             for (int j = 0; j < FN / 2; ++j) {
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
                     const int tc = (wn * WN) / 2 + j * 32 + q4 * 8 + ncol;
-                    const int c0 = tn * (BN / 2) + tc;
-                    f32x4 swg, swu;
-                    u16x4 bg, bu;
-                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swg, bg);
-                    load_col4(p, p.N + (c0 < p.N ? c0 : p.N - 1), 2 * p.N, swu, bu);
+                    const int q = (j * 4 + q4) * 2;
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
                         u16x4 v;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            float g = rt16(g1_reg<HB>(acc[i][2 * j][q4 * 4 + e], sxr[i], swg[e], bg[e]));
-                            float u = rt16(g1_reg<HB>(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], swu[e], bu[e]));
+                            float g = rt16(g1_reg<HB>(acc[i][2 * j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]));
+                            float u = rt16(g1_reg<HB>(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], qsw[q + 1][e], qb[q + 1][e]));
                             v[e] = f2h(silu(g) * u);
                         }
                         put(wm * WM + i * 32 + mrow, tc, v);
@@ -310,15 +346,12 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM /
 #pragma unroll
                 for (int q4 = 0; q4 < 4; ++q4) {
                     const int tc = wn * WN + j * 32 + q4 * 8 + ncol;
-                    const int c0 = n0 + tc;
-                    f32x4 swv;
-                    u16x4 bv;
-                    load_col4(p, c0 < p.N ? c0 : p.N - 1, p.N, swv, bv);
+                    const int q = j * 4 + q4;
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
                         u16x4 v;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], swv[e], bv[e]));
+                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]));
                         put(wm * WM + i * 32 + mrow, tc, v);
                     }
                 }
@@ -828,8 +861,7 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     int ncols = (EP == Epi::SwiGLU) ? 2 * p.N : p.N;
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (ncols + BN - 1) / BN;
-    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) &&
-                (EP != Epi::SwiGLU || p.N % 4 == 0);
+    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) && p.N % 4 == 0;
     p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
     p.conv_tpf = 0;
     if (AM == AMode::Conv && ((int64_t)p.Ho * p.Wo) % BM == 0) p.conv_tpf = (int)((int64_t)p.Ho * p.Wo / BM);
@@ -870,7 +902,7 @@ template <int WO, Epi EP>
 int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.tiles_m = p.M / 512;
     p.tiles_n = p.N / 128;
-    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8));
+    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) && p.N % 4 == 0;
     p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
     p.conv_tpf = 0;
     const int64_t grid = (int64_t)p.tiles_m * p.tiles_n;

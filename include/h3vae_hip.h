@@ -62,6 +62,20 @@ int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* 
  * SiLU over every fp16 argument.  All three are zero on a correct build. */
 int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream);
 
+/* MFMA ceiling microbenchmark (no counterpart in the reference; it measures the
+ * ceiling the INT8 kernels are judged against).  `blocks` workgroups of 8 waves
+ * (launch one per CU) each run iters x 32 back-to-back v_mfma_i32_32x32x32_i8
+ * per wave on register-resident fragments read from a[0:a_bytes) and
+ * b[0:b_bytes) (16-byte aligned int8 data, e.g. a workload's quantized
+ * activations and weights: the sustained clock depends on the data).
+ * sink: int32 [blocks * 512] (written, keeps the MFMAs live); clocks: int64
+ * [2 * blocks], per workgroup {shader-clock ticks, 100 MHz reference ticks}
+ * over the timed loop, so clock = ticks[0] / ticks[1] * 100 MHz.
+ * h3v_probe_mfma_ops_per_block(iters) = INT8 ops one workgroup performs. */
+int h3v_probe_mfma_rate(const int8_t* a, int64_t a_bytes, const int8_t* b, int64_t b_bytes, int blocks,
+                        int iters, int32_t* sink, int64_t* clocks, hipStream_t stream);
+int64_t h3v_probe_mfma_ops_per_block(int iters);
+
 /* ---- INT8 GEMMs (int32 accumulation on MFMA) ---------------------------
  * acc[m, n] = sum_k a[m, k] * w[n, k]; a: int8 [m, k], w: int8 [n, k], both
  * row-major.  Dequant epilogue:

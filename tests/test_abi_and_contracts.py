@@ -58,6 +58,10 @@ def test_entry_points_reject_bad_arguments_before_any_launch(ops):
         ops.hip.call("h3v_conv3d_i8", 16, 16, 16, 16, None, 16, 1, 8, 2, 4, 4, 8, 3, 3, 3, 1, 1, 1, 0, None)
     with pytest.raises(ValueError, match="nonempty"):
         ops.hip.call("h3v_tensor_quant_i8", 16, 0, 16, 16, 16, None)
+    with pytest.raises(ValueError, match="blocks in"):
+        ops.hip.call("h3v_probe_mfma_rate", 16, 16, 16, 16, 0, 1, 16, 16, None)
+    # 4 operand sets x 8 MFMAs x 8 waves x 32^3 MACs x 2 ops per iteration
+    assert ops.hip.lib().h3v_probe_mfma_ops_per_block(1) == 4 * 8 * 8 * 32 ** 3 * 2
 
 
 # ---------------------------------------------------------------------------

@@ -211,3 +211,22 @@ def test_fast_quotients_match_ieee_division_exhaustively(ops):
     ops.hip.call("h3v_selftest_fast_div", ops.hip.ptr(counts), ops.hip.stream(DEV))
     torch.cuda.synchronize()
     assert counts.tolist() == [0, 0, 0], f"fast quotient mismatches (div, q, silu): {counts.tolist()}"
+
+
+def test_mfma_ceiling_probe_counts_and_clock(ops):
+    """The MFMA ceiling probe multiplies what it is given: all-ones operands give 32 per MFMA
+    output, so after `iters` iterations of 4 operand sets every lane's sum of its 8 blocks x 16
+    accumulators is iters * 4 * 32 * 128; the clock it reports is a plausible shader clock."""
+    blocks, iters = 4, 3
+    a = torch.ones(4096, dtype=torch.int8, device=DEV)
+    b = torch.ones(2048, dtype=torch.int8, device=DEV)
+    sink = torch.zeros(blocks * 512, dtype=torch.int32, device=DEV)
+    clocks = torch.zeros(2 * blocks, dtype=torch.int64, device=DEV)
+    ops.hip.call("h3v_probe_mfma_rate", ops.hip.ptr(a), a.numel(), ops.hip.ptr(b), b.numel(), blocks, iters,
+                 ops.hip.ptr(sink), ops.hip.ptr(clocks), ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    assert (sink == iters * 4 * 32 * 128).all()
+    ticks = clocks.view(blocks, 2).double()
+    assert (ticks > 0).all()
+    mhz = ticks[:, 0].sum().item() / ticks[:, 1].sum().item() * 100.0
+    assert 300.0 < mhz < 3500.0, mhz
