@@ -365,6 +365,17 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
         out["cfg4_qk_rope_out_proj_16384tok_16x64"] = {"qk_rope": hbm(t_r, rope_bytes),
                                                        "out_row_quant": hbm(t_oq, m * d * 3 + m * 4),
                                                        "out_gemm": mfma(t_og, 2 * m * d * d)}
+
+        # decoder edge (opt/fp16_finalize.py): one B4 decoder call's tiles [4, 3, 28, 256, 256] fp16 -> fp32
+        import ctypes
+        px = randn(4, 3, 28, 256, 256)
+        pstd = torch.tensor([0.229, 0.224, 0.225], device=dev, dtype=f32)
+        pmean = torch.tensor([0.485, 0.456, 0.406], device=dev, dtype=f32)
+        pout = torch.empty(px.shape, device=dev, dtype=f32)
+        pstrides = (ctypes.c_int64 * 5)(*px.stride())
+        t_f = timed(lambda: call("h3v_finalize_pixels", p(px), 1, 4, 28, 256, 256,
+                                 ctypes.cast(pstrides, ctypes.c_void_p), p(pstd), p(pmean), p(pout), stream))
+        out["edge_finalize_pixels_4x3x28x256x256"] = {"finalize_pixels": hbm(t_f, px.numel() * 6)}
     torch.cuda.synchronize()
     return out
 

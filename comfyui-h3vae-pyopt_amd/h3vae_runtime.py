@@ -351,10 +351,19 @@ class H3VAEPyOptRuntime(torch.nn.Module):
                 # fewer latent frames than one temporal chunk: repeat the last one
                 zn = torch.cat([zn, zn[:, :, -1:, :, :].repeat(1, 1, 7 - t, 1, 1)], dim=2)
             dec = self.core.decode_base(zn, frame_num=self._frames_from_tokens(t))
-        pixels = dec.float() * self._img_std + self._img_mean
-        pixels = pixels.clamp_(0.0, 1.0)
+        # raw decoder output -> fp32 pixels in [0, 1] (reference :543-563)
+        if self.decode_fusions:
+            from .opt.fp16_finalize import finalize_pixels
+            direct = (output_buffer is not None and output_buffer.shape == dec.shape
+                      and output_buffer.dtype == torch.float32 and output_buffer.device == dec.device
+                      and output_buffer.is_contiguous())
+            pixels = finalize_pixels(dec, self._img_std, self._img_mean, output_buffer if direct else None)
+        else:
+            pixels = dec.float() * self._img_std + self._img_mean
+            pixels = pixels.clamp_(0.0, 1.0)
         if output_buffer is not None:
-            output_buffer.copy_(pixels)
+            if pixels is not output_buffer:
+                output_buffer.copy_(pixels)
             out = output_buffer
         else:
             out = pixels

@@ -62,6 +62,17 @@ int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* 
  * SiLU over every fp16 argument.  All three are zero on a correct build. */
 int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream);
 
+/* ---- decoder edge: pixel finalisation ------------------------------------
+ * Replaces opt/fp16_finalize.py:24-54 (`finalize_pixels`, its Triton kernel).
+ * x: decoded pixels [batch, 3, frames, height, width], fp16 (x_is_f16 = 1,
+ * uint16_t bit patterns) or fp32 (x_is_f16 = 0), element strides in
+ * strides[0..4] (host memory, any layout); std, mean: fp32 [3] device
+ * memory; out: contiguous fp32 [batch, 3, frames, height, width].
+ *   v = fp32(x) * std[c] + mean[c]   (two roundings, no FMA)
+ *   out = v < 0 ? 0 : (v > 1 ? 1 : v)   (NaN and an in-range -0 kept)       */
+int h3v_finalize_pixels(const void* x, int x_is_f16, int64_t batch, int64_t frames, int64_t height, int64_t width,
+                        const int64_t* strides, const float* std, const float* mean, float* out, hipStream_t stream);
+
 /* MFMA ceiling microbenchmark (no counterpart in the reference; it measures the
  * ceiling the INT8 kernels are judged against).  `blocks` workgroups of 8 waves
  * (launch one per CU) each run iters x 32 back-to-back v_mfma_i32_32x32x32_i8

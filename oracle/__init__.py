@@ -54,6 +54,7 @@ _SIGNATURES = {
     "ora_residual_layernorm": (None, [_P, _P, _P, _P, _P, _F, _I64, _I, _P]),
     "ora_qk_rope": (None, [_P, _P, _P, _I64, _I, _I, _I, _F, _P, _P]),
     "ora_residual_downsample_pack": (None, [_P, _P, _P, _P, _I, _I, _I, _I]),
+    "ora_finalize_pixels": (None, [_P, _I, _I64, _I64, _P, _P, _P]),
     "ora_tree_sumsq_w16": (_F, [_P, _I]),
     "ora_tree_sum_plain": (_F, [_P, _I]),
     "ora_num_threads": (_I, []),
@@ -328,6 +329,19 @@ def residual_downsample_pack(x_ndhwc, residual_ndhwc, bias):
     d, h, w, c = x.shape
     out = np.empty((d + 2, h + 1, w + 1, c), np.float16)
     lib().ora_residual_downsample_pack(_ptr(x), _ptr(_f16(residual_ndhwc)), _ptr(_f16(bias)), _ptr(out), c, d, h, w)
+    return out
+
+
+def finalize_pixels(x, std, mean):
+    """Decoder pixel finalisation: [B,3,T,H,W] fp16/fp32 -> fp32 clamp(x*std[c] + mean[c], 0, 1), NaN kept."""
+    x = np.ascontiguousarray(x)
+    if x.dtype not in (np.float16, np.float32) or x.ndim != 5 or x.shape[1] != 3:
+        raise ValueError("fp16/fp32 [B,3,T,H,W] pixels required")
+    b, _, t, h, w = x.shape
+    out = np.empty(x.shape, np.float32)
+    lib().ora_finalize_pixels(_ptr(x), int(x.dtype == np.float16), b, t * h * w,
+                              _ptr(np.ascontiguousarray(std, np.float32)), _ptr(np.ascontiguousarray(mean, np.float32)),
+                              _ptr(out))
     return out
 
 

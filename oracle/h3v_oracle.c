@@ -682,6 +682,21 @@ API void ora_residual_downsample_pack(const uint16_t* x, const uint16_t* r, cons
             }
 }
 
+/* Pixel finalisation (reference opt/fp16_finalize.py:24-54, FMA disabled at
+ * launch): contiguous [B, 3, T, H, W] of fp16 (is_f16) or fp32 decoded pixels ->
+ * fp32 v = fp32(x) * std[c] + mean[c] (two roundings), then v < 0 -> 0,
+ * v > 1 -> 1; NaN and an in-range -0 pass through unchanged. */
+API void ora_finalize_pixels(const void* x, int is_f16, int64_t b, int64_t thw, const float* std, const float* mean,
+                             float* out) {
+    for (int64_t i = 0; i < b * 3 * thw; ++i) {
+        const int c = (int)((i / thw) % 3);
+        const float xv = is_f16 ? hf(((const uint16_t*)x)[i]) : ((const float*)x)[i];
+        const float m = xv * std[c];
+        const float v = m + mean[c];
+        out[i] = v < 0.0f ? 0.0f : (v > 1.0f ? 1.0f : v);
+    }
+}
+
 API int ora_num_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -29,7 +29,7 @@ def ops(pkg):
     """Namespace with every operator module of the package."""
     names = ["kitchen_int8", "int8_swiglu_fused", "int8_ffn_up_fused", "int8_norm_quant", "int8_norm1_quant",
              "decoder_fused_qk_rope", "decoder_block0_norm", "decoder_final_norm", "encoder_int8",
-             "encoder_int8_norm", "encoder_int8_integration"]
+             "encoder_int8_norm", "encoder_int8_integration", "fp16_finalize"]
 
     class _Ops:
         pass

@@ -386,3 +386,52 @@ def test_residual_pack_single_fp16_rounding(oracle):
     b = np.full((8,), 2.0 ** -11, np.float16)
     y = oracle.residual_downsample_pack(x, r, b)
     assert (y[2:] == np.float16(1.0 + 2.0 ** -10)).all()
+
+
+# ---------------------------------------------------------------------------
+# decoder pixel finalisation (opt/fp16_finalize.py)
+# ---------------------------------------------------------------------------
+
+def test_finalize_channel_mapping_exact(oracle):
+    # small integers x power-of-two scales are exact: the values pin the channel index alone
+    b, t, h, w = 2, 3, 2, 5
+    x = RNG.integers(0, 4, size=(b, 3, t, h, w)).astype(np.float16)
+    std = np.float32([2.0 ** -3, 2.0 ** -4, 2.0 ** -5])
+    y = oracle.finalize_pixels(x, std, np.zeros(3, np.float32))
+    assert np.array_equal(y, x.astype(np.float32) * std.reshape(1, 3, 1, 1, 1))
+
+
+def test_finalize_two_roundings_not_fma(oracle):
+    # x*s = 1 + 2^-10 + 2^-14 + 2^-23 + 2^-24 + 2^-33 rounds up to 1 + 2^-10 + 2^-14 + 2^-22 in fp32;
+    # adding m = -1 then gives 2^-10 + 2^-14 + 2^-22.  A fused multiply-add would keep
+    # 2^-10 + 2^-14 + 2^-23 + 2^-24 + 2^-33 (exact in fp32).
+    x = np.full((1, 3, 1, 1, 8), 1.0 + 2.0 ** -10, np.float16)
+    s = np.float32(1.0 + 2.0 ** -14 + 2.0 ** -23)
+    std = np.full(3, s, np.float32)
+    mean = np.full(3, -1.0, np.float32)
+    y = oracle.finalize_pixels(x, std, mean)
+    two = 2.0 ** -10 + 2.0 ** -14 + 2.0 ** -22
+    fused = 2.0 ** -10 + 2.0 ** -14 + 2.0 ** -23 + 2.0 ** -24 + 2.0 ** -33
+    assert (y == np.float32(two)).all() and np.float32(fused) != np.float32(two)
+
+
+def test_finalize_clamp_nan_and_signed_zero(oracle):
+    vals = np.float32([-5.0, -0.0, 0.0, 0.25, 1.0, 1.5, np.inf, -np.inf, np.nan, 2.0 ** -149])
+    x = np.zeros((1, 3, 1, 1, vals.size), np.float32)
+    x[0, :, 0, 0, :] = vals
+    # mean = -0 keeps every product unchanged (-0 + -0 = -0, x + -0 = x), so the clamp's own
+    # treatment of -0 shows; the comparisons must neither flip it nor swallow NaN
+    y = oracle.finalize_pixels(x, np.ones(3, np.float32), np.full(3, -0.0, np.float32))[0, 0, 0, 0]
+    expect = np.float32([0.0, -0.0, 0.0, 0.25, 1.0, 1.0, 1.0, 0.0, np.nan, 2.0 ** -149])
+    assert np.isnan(y[8]) and np.array_equal(np.delete(y, 8).view(np.uint32), np.delete(expect, 8).view(np.uint32))
+
+
+@pytest.mark.parametrize("dtype", [np.float16, np.float32])
+def test_finalize_against_numpy_float32(oracle, dtype):
+    x = (RNG.standard_normal((2, 3, 3, 4, 7)) * 2).astype(dtype)
+    std = np.float32([0.229, 0.224, 0.225])
+    mean = np.float32([0.485, 0.456, 0.406])
+    prod = x.astype(np.float32) * std.reshape(1, 3, 1, 1, 1)        # numpy rounds each float32 op once
+    v = prod + mean.reshape(1, 3, 1, 1, 1)
+    expect = np.where(v < 0, np.float32(0), np.where(v > 1, np.float32(1), v)).astype(np.float32)
+    assert np.array_equal(oracle.finalize_pixels(x, std, mean), expect)

@@ -91,6 +91,7 @@ def _bare_runtime(rt, core):
     r.latents_mean = torch.zeros((1, 24, 1, 1, 1), dtype=torch.float16)
     r.latents_std = torch.ones_like(r.latents_mean)
     r.int8_decode = r.int8_encode = False
+    r.decode_fusions = False
     r.log_calls = False
     r._img_mean = torch.tensor(rt._IMG_MEAN).reshape(1, 3, 1, 1, 1)
     r._img_std = torch.tensor(rt._IMG_STD).reshape(1, 3, 1, 1, 1)
@@ -119,6 +120,56 @@ def test_decode_padding_and_output_buffer_contract(rt):
     r.int8_decode = True
     with pytest.raises(RuntimeError, match="FP16 latent"):
         r.decode(torch.zeros((1, 24, 2, 2, 4)))
+
+
+def test_decode_fusions_finalize_path_matches_eager(rt, pkg, monkeypatch):
+    """Reference tests/test_fp16_finalize.py:30-46: with decode_fusions the pixel finalisation goes
+    through opt.fp16_finalize.finalize_pixels (patched here with the eager formula, as the reference
+    test does), and both paths give the same pixels and honour the output-buffer contract."""
+    fin = importlib.import_module(f"{pkg.__name__}.opt.fp16_finalize")
+    calls = []
+
+    def eager(x, std, mean, out=None):
+        calls.append(out is not None)
+        y = (x.float() * std + mean).clamp_(0, 1)
+        if out is not None:
+            out.copy_(y)
+            return out
+        return y
+
+    monkeypatch.setattr(fin, "finalize_pixels", eager)
+    r = _bare_runtime(rt, _DecodeCore())
+    with torch.inference_mode():
+        for int8, t in ((i, t) for i in (False, True) for t in (1, 2, 7)):
+            r.int8_decode = int8
+            z = torch.randn((1, 24, t, 2, 4), dtype=torch.float16)
+            r.decode_fusions = False
+            reference = r.decode(z)
+            r.decode_fusions = True
+            actual = r.decode(z)
+            assert torch.equal(actual, reference)
+            for out in (torch.empty_like(reference), torch.empty_like(reference).half(),
+                        torch.empty((*reference.shape[:-2], 4, 2)).transpose(-1, -2)):
+                assert r.decode(z, output_buffer=out) is out
+                assert torch.equal(out, reference.to(out.dtype))
+    # a matching contiguous fp32 buffer is written in place by the kernel; others get a copy
+    assert True in calls and False in calls
+
+
+def test_finalize_guards(pkg):
+    """Reference tests/test_fp16_finalize.py:21-28: metadata guards raise ValueError before any launch,
+    and a CPU tensor is refused (there is no eager fallback)."""
+    fin = importlib.import_module(f"{pkg.__name__}.opt.fp16_finalize")
+    x = torch.zeros((1, 3, 2, 4, 4), dtype=torch.float16)
+    v = torch.ones(3)
+    fin.validate(x, v, v)
+    with pytest.raises(ValueError, match="gfx950"):
+        fin.finalize_pixels(x, v, v)
+    for a, b, c, o in [(x[:, :2], v, v, None), (x.double(), v, v, None), (x, v.half(), v, None),
+                       (x, v, v, torch.empty_like(x)), (x[:, :, :0], v, v, None),
+                       (x, v, v, torch.empty((1, 3, 2, 4, 4)).transpose(-1, -2))]:
+        with pytest.raises(ValueError):
+            fin.validate(a, b, c, o)
 
 
 def test_decode_output_shape(rt):
