@@ -48,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_selftest_fast_div": [_P, _P],
     "h3v_probe_mfma_rate": [_P, _I64, _P, _I64, _I, _I, _P, _P, _P],
     "h3v_finalize_pixels": [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
+    "h3v_attention_d64": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
 }
 # entry points with a non-int result
 SPECIAL: dict[str, tuple] = {

@@ -1,0 +1,249 @@
+// Scaled-dot-product attention for head_dim 64 (fp16 in and out, fp32 softmax
+// and accumulation), non-causal, no mask: the decoder attention of the H3 VAE
+// that the reference hands to the model's `perform_attention` (flash attention
+// on NVIDIA) between the fused QK-RMSNorm-RoPE and the INT8 attention-out
+// linear (opt/decoder_fused_qk_rope.py:66-74, `FusedQKAttention.forward`).
+//
+//   O[q, :] = sum_k softmax_k(scale * Q[q, :] . K[k, :]) V[k, :]
+//
+// q, k, v, o are [batch, tokens, heads, 64] with arbitrary token and head
+// strides (in elements; the 64 dims contiguous), so v can be the strided
+// slice of the QKV projection and q, k the QK-RoPE outputs, with no copies.
+//
+// One workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
+// 32 queries.  Keys and values stream in blocks of 64 through LDS:
+//
+//   S = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = the wave's
+//                 Q fragments (registers, loaded once).  In the 32 x 32 result
+//                 layout lane l holds query l % 32 and keys 8g + 4(l / 32) + e
+//                 (g, e = 0..3) of each 32-key half, so a query's 64 keys sit
+//                 in lanes l and l ^ 32 (32 each): the row max and sum are
+//                 in-lane reductions plus one exchange.
+//   online softmax in fp32 (exp2 with the scale folded into log2 e)
+//   O^T += V^T . P^T   A = V^T rows from LDS (V is written transposed), B = P
+//                 in fp16: one v_permlane32_swap per dword pair turns the S
+//                 layout into the MFMA's 8 consecutive keys per lane.
+//
+// LDS: K [64 keys][64 dims] and V^T [64 dims][64 keys] fp16, 128-byte rows
+// whose 16-byte chunks are XOR-swizzled by (row >> 1) & 7, so the 16-lane
+// fragment reads hit 16 distinct 4-bank groups.  The next block's K and V
+// are loaded into registers while the current one is computed.
+#include "h3v_common.hpp"
+#include "h3v_abi.hpp"
+
+namespace h3v {
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 64;        // head dim
+constexpr int kBQ = 128;      // queries per workgroup
+constexpr int kBK = 64;       // keys per block
+constexpr int kThreads = 256;
+
+struct AttnParams {
+    const uint16_t* q;
+    const uint16_t* k;
+    const uint16_t* v;
+    uint16_t* o;
+    int64_t q_ts, q_hs, k_ts, k_hs, v_ts, v_hs, o_ts, o_hs;
+    int tokens;
+    float c;   // scale * log2(e)
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+__device__ __forceinline__ float wave_pair_max(float v) { return __builtin_fmaxf(v, __shfl_xor(v, 32, 64)); }
+
+__global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kBK * kD];   // [key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kBK];   // [dim][key]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int n = p.tokens;
+    const int64_t row0 = (int64_t)b * n;                 // first token row of this batch item
+    const int qi = blockIdx.x * kBQ + wave * 32 + (lane & 31);
+    const int hi = lane >> 5;                           // which 8 of a 16-wide k chunk this lane holds
+
+    // the wave's Q fragments: query qi, dims 16 kc + 8 hi .. + 7
+    half8 qf[4];
+    {
+        const int qr = qi < n ? qi : n - 1;
+        const uint16_t* src = p.q + (row0 + qr) * p.q_ts + h * p.q_hs + 8 * hi;
+#pragma unroll
+        for (int kc = 0; kc < 4; ++kc) qf[kc] = *reinterpret_cast<const half8*>(src + 16 * kc);
+    }
+
+    // cooperative K / V block loads: 64 keys x 8 chunks of 8 dims = 512 chunks, two per thread
+    u32x4 kreg[2], vreg[2];
+    auto load_block = [&](int kb0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + kThreads * i;
+            const int key = c >> 3, dch = c & 7;             // K: consecutive threads walk a key row
+            const int kr = kb0 + key < n ? kb0 + key : n - 1;
+            kreg[i] = *reinterpret_cast<const u32x4*>(p.k + (row0 + kr) * p.k_ts + h * p.k_hs + 8 * dch);
+            const int vkey = c & 63, vdch = c >> 6;         // V: consecutive threads walk keys (transposed store)
+            const int vr = kb0 + vkey < n ? kb0 + vkey : n - 1;
+            vreg[i] = *reinterpret_cast<const u32x4*>(p.v + (row0 + vr) * p.v_ts + h * p.v_hs + 8 * vdch);
+        }
+    };
+    auto store_block = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int c = tid + kThreads * i;
+            const int key = c >> 3, dch = c & 7;
+            *reinterpret_cast<u32x4*>(ks + key * kD + 8 * swz(key, dch)) = kreg[i];
+            const int vkey = c & 63, vdch = c >> 6;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int d = 8 * vdch + e;
+                const uint32_t w = vreg[i][e >> 1];
+                vt[d * kBK + 8 * swz(d, vkey >> 3) + (vkey & 7)] = (uint16_t)(e & 1 ? w >> 16 : w & 0xffff);
+            }
+        }
+    };
+
+    f32x16 oacc[2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db) oacc[db] = f32x16{};
+    float m_run = -__builtin_inff();
+    float l_run = 0.0f;
+
+    const int nblk = (n + kBK - 1) / kBK;
+    load_block(0);
+    for (int j = 0; j < nblk; ++j) {
+        const int kb0 = j * kBK;
+        __syncthreads();                                  // every wave is done with the previous block
+        store_block();
+        __syncthreads();
+        if (j + 1 < nblk) load_block(kb0 + kBK);          // next block in flight during this one
+
+        // S = K . Q^T for the 64 keys of the block (two 32-key halves)
+        f32x16 s[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            s[kh] = f32x16{};
+            const int row = 32 * kh + (lane & 31);
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) {
+                const half8 a = *reinterpret_cast<const half8*>(ks + row * kD + 8 * swz(row, 2 * kc + hi));
+                s[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kc], s[kh], 0, 0, 0);
+            }
+        }
+        // keys past the end (last block only): -inf
+        if (kb0 + kBK > n) {
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = kb0 + 32 * kh + 8 * (r >> 2) + 4 * hi + (r & 3);
+                    if (key >= n) s[kh][r] = -__builtin_inff();
+                }
+        }
+        // online softmax (raw-score units; the exponent folds in scale * log2 e)
+        float mloc = s[0][0];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) mloc = __builtin_fmaxf(mloc, s[kh][r]);
+        const float m_new = __builtin_fmaxf(m_run, wave_pair_max(mloc));
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * p.c);
+        const float mc = m_new * p.c;
+        m_run = m_new;
+        float lsum = 0.0f;
+        uint32_t pk[2][8];                                // P in fp16: [half][g * 2 + dword]
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float e4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][4 * g + e], p.c, -mc));
+                    lsum += e4[e];
+                }
+                pk[kh][2 * g] = (uint32_t)f2h(e4[0]) | ((uint32_t)f2h(e4[1]) << 16);
+                pk[kh][2 * g + 1] = (uint32_t)f2h(e4[2]) | ((uint32_t)f2h(e4[3]) << 16);
+            }
+        l_run = l_run * alpha + lsum;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+
+        // O^T += V^T . P^T over four 16-key chunks
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int kh = c >> 1, g0 = 2 * (c & 1);
+            // lane < 32 needs keys 16c + 0..7 (its own group g0 + the partner's), lane >= 32
+            // keys 16c + 8..15 (the partner's group g0 + 1 + its own)
+            const auto x0 = __builtin_amdgcn_permlane32_swap(pk[kh][2 * g0], pk[kh][2 * g0 + 2], false, false);
+            const auto x1 = __builtin_amdgcn_permlane32_swap(pk[kh][2 * g0 + 1], pk[kh][2 * g0 + 3], false, false);
+            const u32x4 bw = {x0[0], x1[0], x0[1], x1[1]};
+            const half8 bop = __builtin_bit_cast(half8, bw);
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                const int row = 32 * db + (lane & 31);
+                const half8 a = *reinterpret_cast<const half8*>(vt + row * kBK + 8 * swz(row, 2 * c + hi));
+                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop, oacc[db], 0, 0, 0);
+            }
+        }
+    }
+
+    // normalise and store: lane l holds query qi, dims 32 db + 8 g + 4 hi + e
+    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+    const float inv = 1.0f / l_tot;
+    if (qi < n) {
+        uint16_t* dst = p.o + (row0 + qi) * p.o_ts + h * p.o_hs + 4 * hi;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                u16x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = f2h(oacc[db][4 * g + e] * inv);
+                *reinterpret_cast<u16x4*>(dst + 32 * db + 8 * g) = v;
+            }
+    }
+}
+
+}  // namespace
+}  // namespace h3v
+
+using namespace h3v;
+
+extern "C" int h3v_attention_d64(const uint16_t* q, int64_t q_token_stride, int64_t q_head_stride, const uint16_t* k,
+                                 int64_t k_token_stride, int64_t k_head_stride, const uint16_t* v,
+                                 int64_t v_token_stride, int64_t v_head_stride, uint16_t* o, int64_t o_token_stride,
+                                 int64_t o_head_stride, int64_t batch, int64_t tokens, int64_t heads, float scale,
+                                 hipStream_t stream) {
+    const char* what = "h3v_attention_d64";
+    H3V_REQUIRE(q && k && v && o, "%s: null pointer argument", what);
+    H3V_REQUIRE(batch > 0 && tokens > 0 && heads > 0, "%s: batch, tokens and heads must be positive", what);
+    H3V_REQUIRE(batch <= 65535 && heads <= 65535 && tokens <= (1 << 24), "%s: shape out of range", what);
+    H3V_REQUIRE(scale > 0.0f && scale < 1e30f, "%s: scale must be positive and finite", what);
+    const int64_t strides[8] = {q_token_stride, q_head_stride, k_token_stride, k_head_stride,
+                                v_token_stride, v_head_stride, o_token_stride, o_head_stride};
+    for (int i = 0; i < 8; ++i)
+        H3V_REQUIRE(strides[i] > 0 && strides[i] % 8 == 0, "%s: token/head strides must be positive multiples of 8 "
+                    "elements (16-byte rows)", what);
+    H3V_REQUIRE(aligned(q, 16) && aligned(k, 16) && aligned(v, 16) && aligned(o, 8),
+                "%s: q, k, v must be 16-byte and o 8-byte aligned", what);
+    AttnParams p;
+    p.q = q; p.k = k; p.v = v; p.o = o;
+    p.q_ts = q_token_stride; p.q_hs = q_head_stride;
+    p.k_ts = k_token_stride; p.k_hs = k_head_stride;
+    p.v_ts = v_token_stride; p.v_hs = v_head_stride;
+    p.o_ts = o_token_stride; p.o_hs = o_head_stride;
+    p.tokens = (int)tokens;
+    p.c = scale * 1.4426950408889634f;
+    dim3 grid((unsigned)((tokens + kBQ - 1) / kBQ), (unsigned)heads, (unsigned)batch);
+    hipLaunchKernelGGL(fmha_d64, grid, dim3(kThreads), 0, stream, p);
+    return launch_status(what);
+}

@@ -5,6 +5,13 @@ Mirror of opt/decoder_fused_qk_rope.py in fishelegs/ComfyUI-H3VAE-PyOpt.
 rows (64 dims) are RMS-normalised in FP32 without affine and rounded to FP16,
 then the first 48 dims get rotate-half RoPE with FP16-rounded products summed
 in FP32; dims 48..63 pass through.
+
+The attention between the fused QK-RoPE and the output projection, which the
+reference hands to the model's ``perform_attention`` (:66-74), runs as
+``h3v_attention_d64`` (``attention_d64`` below): q and k straight from the
+QK-RoPE outputs and v as the strided slice of the QKV projection, no copies.
+Calls that carry ``pack_info`` (packed-sequence masks of the model code) keep
+the model's own attention.
 """
 from __future__ import annotations
 
@@ -44,10 +51,48 @@ def _fake(x, cos, sin, heads, eps, rows):
     return x.new_empty(shape), x.new_empty(shape)
 
 
+def _check_attention(q, k, v):
+    if not (q.ndim == 4 and q.shape == k.shape == v.shape and q.shape[-1] == 64):
+        raise ValueError("attention_d64 requires q, k, v of one shape [B, N, H, 64]")
+    if not (q.dtype == k.dtype == v.dtype == torch.float16) or not (q.device == k.device == v.device):
+        raise ValueError("attention_d64 requires FP16 q, k, v on one device")
+    b, n, h, _ = q.shape
+    if b == 0 or n == 0 or h == 0:
+        raise ValueError("attention_d64 requires a nonempty input")
+    for t in (q, k, v):
+        st = t.stride()
+        if st[3] != 1 or st[1] % 8 or st[2] % 8 or st[1] <= 0 or st[2] <= 0 or (b > 1 and st[0] != n * st[1]):
+            raise ValueError("attention_d64 requires contiguous head dims, token/head strides that are multiples of 8 "
+                             "and the batch stride tokens * token stride")
+        if t.data_ptr() % 16:
+            raise ValueError("attention_d64 requires 16-byte aligned q, k, v")
+
+
+@torch.library.custom_op("h3vae_decoder::attention_d64", mutates_args=(), device_types="cuda")
+def attention_d64(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> torch.Tensor:
+    """softmax(scale * q k^T) v per (batch, head): q, k, v [B, N, H, 64] fp16 (strided) -> [B, N, H, 64]."""
+    _check_attention(q, k, v)
+    if not (0.0 < scale < 1e30):
+        raise ValueError("attention_d64 requires a positive finite scale")
+    _hip.require_gfx950(q.device, "attention_d64")
+    b, n, h, d = q.shape
+    o = torch.empty((b, n, h, d), device=q.device, dtype=q.dtype)
+    _hip.call("h3v_attention_d64", _hip.ptr(q), q.stride(1), q.stride(2), _hip.ptr(k), k.stride(1), k.stride(2),
+              _hip.ptr(v), v.stride(1), v.stride(2), _hip.ptr(o), o.stride(1), o.stride(2), b, n, h, float(scale),
+              _hip.stream(q.device))
+    return o
+
+
+@attention_d64.register_fake
+def _fake_attention(q, k, v, scale):
+    _check_attention(q, k, v)
+    return q.new_empty(q.shape)
+
+
 class FusedQKAttention(torch.nn.Module):
     """Attention wrapper: to_qkv -> fused QK norm/RoPE -> attention -> to_out."""
 
-    def __init__(self, original, rows=8):
+    def __init__(self, original, rows=8, native_attention=True):
         super().__init__()
         if (getattr(original, "spatial_parallel", False) or not isinstance(original.norm_q, torch.nn.RMSNorm)
                 or not isinstance(original.norm_k, torch.nn.RMSNorm)):
@@ -57,6 +102,7 @@ class FusedQKAttention(torch.nn.Module):
             raise ValueError("expected head=64 and unaffined equal-eps QK norms")
         self.original = original
         self.rows = rows
+        self.native_attention = bool(native_attention)
 
     def forward(self, x, rotary_pos_emb=None, pack_info=None):
         if rotary_pos_emb is None:
@@ -66,15 +112,20 @@ class FusedQKAttention(torch.nn.Module):
         qkv = a.to_qkv(x)
         q, k = qk_rope(qkv, *rotary_pos_emb, a.heads, a.norm_q.eps, self.rows)
         v = qkv.view(b, n, a.heads, 3 * a.dim_head)[..., 2 * a.dim_head:]
-        y = a.perform_attention(q, k, v, pack_info or {})
+        if self.native_attention and not pack_info:
+            y = attention_d64(q, k, v, a.dim_head ** -0.5)
+        else:
+            y = a.perform_attention(q, k, v, pack_info or {})
         return a.to_out(y.reshape(b, n, -1))
 
 
-def clone_with_qk_fusion(raw, rows=8):
+def clone_with_qk_fusion(raw, rows=8, native_attention=True):
     """Copy the decoder's module containers with every attention wrapped in FusedQKAttention.
 
     Weights are shared read-only and the original decoder is left intact
-    (reference opt/decoder_fused_qk_rope.py:76-89).
+    (reference opt/decoder_fused_qk_rope.py:76-89).  ``native_attention=False``
+    keeps the model's ``perform_attention`` for every call (the reference's
+    behaviour); the default runs ``attention_d64`` when no ``pack_info`` is given.
     """
     if raw.training or os.environ.get("MINIMAX_H3_VAE_DECODER_VIT_FP32_NORM", "1").lower() in ("0", "false", "no",
                                                                                                "off"):
@@ -85,7 +136,7 @@ def clone_with_qk_fusion(raw, rows=8):
     for block in raw.transformer_blocks:
         new = copy.copy(block)
         new._modules = block._modules.copy()
-        new.attn = FusedQKAttention(block.attn, rows).eval()
+        new.attn = FusedQKAttention(block.attn, rows, native_attention).eval()
         blocks.append(new)
     decoder.transformer_blocks = torch.nn.ModuleList(blocks)
     return decoder

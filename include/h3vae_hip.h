@@ -62,6 +62,20 @@ int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* 
  * SiLU over every fp16 argument.  All three are zero on a correct build. */
 int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream);
 
+/* ---- decoder attention (head_dim 64) --------------------------------------
+ * Replaces the model's `perform_attention` (flash attention) called from
+ * opt/decoder_fused_qk_rope.py:66-74 (`FusedQKAttention.forward`) between the
+ * fused QK-RoPE and the attention-out linear.  Non-causal, unmasked:
+ *   o[b, t, h, :] = sum_s softmax_s(scale * q[b, t, h, :] . k[b, s, h, :]) v[b, s, h, :]
+ * q, k, v, o: fp16 [batch, tokens, heads, 64] with the given token and head
+ * strides in elements (multiples of 8; the 64 dims contiguous; batch stride =
+ * tokens * token stride), so q/k can be the QK-RoPE outputs and v the strided
+ * slice of the QKV projection.  fp32 softmax and accumulation, fp16 output. */
+int h3v_attention_d64(const uint16_t* q, int64_t q_token_stride, int64_t q_head_stride, const uint16_t* k,
+                      int64_t k_token_stride, int64_t k_head_stride, const uint16_t* v, int64_t v_token_stride,
+                      int64_t v_head_stride, uint16_t* o, int64_t o_token_stride, int64_t o_head_stride,
+                      int64_t batch, int64_t tokens, int64_t heads, float scale, hipStream_t stream);
+
 /* ---- decoder edge: pixel finalisation ------------------------------------
  * Replaces opt/fp16_finalize.py:24-54 (`finalize_pixels`, its Triton kernel).
  * x: decoded pixels [batch, 3, frames, height, width], fp16 (x_is_f16 = 1,

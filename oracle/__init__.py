@@ -345,4 +345,23 @@ def finalize_pixels(x, std, mean):
     return out
 
 
+def attention(q, k, v, scale, queries=None):
+    """Decoder attention in float64: softmax(scale * q k^T) v per (batch, head).
+
+    q, k, v: [B, N, H, D] (any float dtype, converted exactly to float64).  `queries` optionally
+    selects query token indices (all keys are always used).  Returns float64 [B, len(queries), H, D].
+    The kernels' fp16 softmax weights and fp32 accumulation are compared against it with a tolerance.
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    if queries is not None:
+        q = q[:, np.asarray(queries)]
+    s = np.einsum("bqhd,bkhd->bhqk", q, k) * float(scale)
+    s -= s.max(axis=-1, keepdims=True)
+    w = np.exp(s)
+    w /= w.sum(axis=-1, keepdims=True)
+    return np.einsum("bhqk,bkhd->bqhd", w, v)
+
+
 __all__ = [name for name in dir() if not name.startswith("_")]

@@ -133,8 +133,9 @@ def test_prefix_runs_all_int8_blocks(int8_prefix):
 
 # -- decoder ---------------------------------------------------------------------------------------------
 
-def _int8_decoder(mods, raw):
-    dec = mods["decoder_fused_qk_rope"].clone_with_qk_fusion(raw, 8)
+def _int8_decoder(mods, raw, native_attention=False):
+    # by default the model's perform_attention (the architecture's "sum" stand-in) keeps the chain bit-exact
+    dec = mods["decoder_fused_qk_rope"].clone_with_qk_fusion(raw, 8, native_attention=native_attention)
     mods["kitchen_int8"].install_kitchen_int8_ffn(dec, mode="INT8both", require_cuda=True)
     dec = mods["int8_attention_out"].from_raw_decoder(dec, warps=8)
     return mods["int8_norm1_quant"].clone_norm1_quant_decoder(dec, enabled=True)
@@ -198,7 +199,9 @@ def test_decoder_carry_chain_matches_oracle(mods, oracle, dim, hidden, depth, ba
     assert_bitwise(y, want, "decoder carry chain")
 
 
-def test_decoder_int8_close_to_fp16_model(mods):
+@pytest.mark.parametrize("native_attention", [False, True])
+def test_decoder_int8_close_to_fp16_model(mods, native_attention):
+    """The INT8 decoder (with the model's SDPA, or with h3v_attention_d64) against the fp16 model."""
     torch.manual_seed(3)
     raw = h3_arch.H3Decoder(dim=1024, hidden=2048, depth=3).half().to(DEV).eval()
     gen = torch.Generator().manual_seed(9)
@@ -206,7 +209,7 @@ def test_decoder_int8_close_to_fp16_model(mods):
     cos, sin = (t.to(DEV) for t in h3_arch.rope_tables(2, 200))
     with torch.inference_mode():
         ref = raw(x, (cos, sin), {})
-        y = _int8_decoder(mods, raw)(x, (cos, sin), {})
+        y = _int8_decoder(mods, raw, native_attention)(x, (cos, sin), {})
         torch.cuda.synchronize()
     assert torch.isfinite(y).all()
     rel = (y.float() - ref.float()).norm() / ref.float().norm()

@@ -435,3 +435,39 @@ def test_finalize_against_numpy_float32(oracle, dtype):
     v = prod + mean.reshape(1, 3, 1, 1, 1)
     expect = np.where(v < 0, np.float32(0), np.where(v > 1, np.float32(1), v)).astype(np.float32)
     assert np.array_equal(oracle.finalize_pixels(x, std, mean), expect)
+
+
+# ---------------------------------------------------------------------------
+# decoder attention (float64 restatement)
+# ---------------------------------------------------------------------------
+
+def test_attention_uniform_weights_closed_form(oracle):
+    # q = 0: every key gets weight 1/N, so the output is the mean of the values
+    b, n, h, d = 2, 37, 3, 64
+    q = np.zeros((b, n, h, d))
+    k = RNG.standard_normal((b, n, h, d))
+    v = RNG.standard_normal((b, n, h, d))
+    o = oracle.attention(q, k, v, 0.125)
+    assert np.allclose(o, np.broadcast_to(v.mean(axis=1, keepdims=True), o.shape), rtol=0, atol=1e-12)
+
+
+def test_attention_one_hot_selects_a_value_row(oracle):
+    # orthogonal keys, query = 40 x key j: weight of j is 1 / (1 + 15 e^-40) -> v[j] to 1e-15
+    n, d = 16, 64
+    k = np.zeros((1, n, 1, d))
+    k[0, np.arange(n), 0, np.arange(n)] = 1.0
+    v = RNG.standard_normal((1, n, 1, d))
+    q = 40.0 * k[:, [5, 11]]
+    o = oracle.attention(q, k, v, 1.0)
+    assert np.allclose(o[0, :, 0], v[0, [5, 11], 0], rtol=0, atol=1e-12)
+
+
+def test_attention_against_torch_sdpa_float64(oracle):
+    torch = pytest.importorskip("torch")
+    b, n, h, d = 2, 29, 4, 64
+    q, k, v = (RNG.standard_normal((b, n, h, d)) for _ in range(3))
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        *(torch.from_numpy(t).permute(0, 2, 1, 3) for t in (q, k, v)), scale=0.125).permute(0, 2, 1, 3).numpy()
+    assert np.allclose(oracle.attention(q, k, v, 0.125), ref, rtol=1e-12, atol=1e-12)
+    sub = oracle.attention(q, k, v, 0.125, queries=[0, 7, 28])
+    assert np.array_equal(sub, oracle.attention(q, k, v, 0.125)[:, [0, 7, 28]])
