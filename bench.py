@@ -34,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 
 INT8_PEAK_TOPS = 5033.2  # 256 CU x 8192 int8 ops/clk x 2.4 GHz (dense)
 HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6  # 256 CU x 4096 fp16 flops/clk x 2.4 GHz (dense MFMA)
 
 # H3 shapes
 ENC_CALLS = 224            # 28 tiles x 8 clips
@@ -282,6 +283,10 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
         return {"us": round(us, 2), "tops": round(ops / us / 1e6, 1), "frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4),
                 "bound": "mfma", "ops": ops}
 
+    def fp16_mfma(us, flops):
+        return {"us": round(us, 2), "tflops": round(flops / us / 1e6, 1),
+                "frac": round(flops / us / 1e6 / FP16_PEAK_TFLOPS, 4), "bound": "mfma", "flops": flops}
+
     def hbm(us, nbytes):
         return {"us": round(us, 2), "gbs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
                 "bound": "hbm", "bytes": nbytes}
@@ -376,6 +381,24 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
         t_f = timed(lambda: call("h3v_finalize_pixels", p(px), 1, 4, 28, 256, 256,
                                  ctypes.cast(pstrides, ctypes.c_void_p), p(pstd), p(pmean), p(pout), stream))
         out["edge_finalize_pixels_4x3x28x256x256"] = {"finalize_pixels": hbm(t_f, px.numel() * 6)}
+
+        # decoder attention (head_dim 64): h3v_attention_d64 and torch's SDPA on the same inputs, q/k from the
+        # QK-RoPE layout [B, N, H, 64] and v the strided slice of the QKV projection
+        def attention_case(b, n, heads):
+            qkv_t = randn(b, n, heads * 192)
+            qa, ka = randn(b, n, heads, 64), randn(b, n, heads, 64)
+            va = qkv_t.view(b, n, heads, 192)[..., 128:]
+            oa = torch.empty((b, n, heads, 64), device=dev, dtype=f16)
+            t_a = timed(lambda: call("h3v_attention_d64", p(qa), qa.stride(1), qa.stride(2), p(ka), ka.stride(1),
+                                     ka.stride(2), p(va), va.stride(1), va.stride(2), p(oa), oa.stride(1), oa.stride(2),
+                                     b, n, heads, 0.125, stream))
+            qt, kt, vt = qa.transpose(1, 2), ka.transpose(1, 2), va.transpose(1, 2)
+            t_s = timed(lambda: F.scaled_dot_product_attention(qt, kt, vt.contiguous(), scale=0.125))
+            flops = 4 * b * heads * n * n * 64
+            return {"h3v_attention_d64": fp16_mfma(t_a, flops), "torch_sdpa_incl_v_copy": fp16_mfma(t_s, flops)}
+
+        out["attention_h3_4x1797x32x64"] = attention_case(4, 1797, 32)
+        out["attention_cfg4_1x16384x16x64"] = attention_case(1, 16384, 16)
     torch.cuda.synchronize()
     return out
 

@@ -19,7 +19,8 @@
 //                 (g, e = 0..3) of each 32-key half, so a query's 64 keys sit
 //                 in lanes l and l ^ 32 (32 each): the row max and sum are
 //                 in-lane reductions plus one exchange.
-//   online softmax in fp32 (exp2 with the scale folded into log2 e)
+//   online softmax in fp32 (exp2 with the scale folded into log2 e); the row
+//                 sums add the fp16-rounded weights that the P.V product uses
 //   O^T += V^T . P^T   A = V^T rows from LDS (V is written transposed), B = P
 //                 in fp16: one v_permlane32_swap per dword pair turns the S
 //                 layout into the MFMA's 8 consecutive keys per lane.
@@ -56,6 +57,14 @@ struct AttnParams {
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
 __device__ __forceinline__ float wave_pair_max(float v) { return __builtin_fmaxf(v, __shfl_xor(v, 32, 64)); }
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// two fp32 -> packed fp16 (round to nearest even), one v_cvt_pk_f16_f32
+__device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+}
 
 __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
     __shared__ __attribute__((aligned(16))) uint16_t ks[kBK * kD];   // [key][dim]
@@ -164,18 +173,23 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
             for (int g = 0; g < 4; ++g) {
                 float e4[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][4 * g + e], p.c, -mc));
-                    lsum += e4[e];
-                }
-                pk[kh][2 * g] = (uint32_t)f2h(e4[0]) | ((uint32_t)f2h(e4[1]) << 16);
-                pk[kh][2 * g + 1] = (uint32_t)f2h(e4[2]) | ((uint32_t)f2h(e4[3]) << 16);
+                for (int e = 0; e < 4; ++e) e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][4 * g + e], p.c, -mc));
+                pk[kh][2 * g] = pack_f16x2(e4[0], e4[1]);
+                pk[kh][2 * g + 1] = pack_f16x2(e4[2], e4[3]);
+                // the row sum adds the fp16 weights the P.V product uses, two per v_dot2_f32_f16
+                const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+                lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[kh][2 * g]), one, lsum, false);
+                lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[kh][2 * g + 1]), one, lsum, false);
             }
         l_run = l_run * alpha + lsum;
+        // alpha is exactly 1 where the running maximum did not move; skip the rescale
+        // when that holds for every lane (most blocks once the maximum has settled)
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
+            for (int db = 0; db < 2; ++db)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+                for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        }
 
         // O^T += V^T . P^T over four 16-key chunks
 #pragma unroll
