@@ -48,6 +48,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_selftest_fast_div": [_P, _P],
     "h3v_probe_mfma_rate": [_P, _I64, _P, _I64, _I, _I, _P, _P, _P],
     "h3v_finalize_pixels": [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
+    "h3v_gn_norm_pack_f16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "h3v_attention_d64": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
 }
 # entry points with a non-int result
@@ -56,6 +57,7 @@ SPECIAL: dict[str, tuple] = {
     "h3v_last_error": (ctypes.c_char_p, []),
     "h3v_gn_norm_pack_workspace_floats": (ctypes.c_int64, [_I, _I, _I]),
     "h3v_probe_mfma_ops_per_block": (ctypes.c_int64, [_I]),
+    "h3v_gn_norm_pack_f16_workspace_floats": (ctypes.c_int64, [_I, _I, _I, _I, _I]),
 }
 
 

@@ -204,22 +204,14 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
 // the group's channels then form the absmax candidates.
 constexpr int kMergeBatch = 1024;
 
-__global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
-                                               const uint32_t* __restrict__ vmax, const uint32_t* __restrict__ vmin,
-                                               const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
-                                               int hw, int nchunk, int c, float eps, float* __restrict__ stats,
-                                               uint32_t* __restrict__ amax_bits) {
-    __shared__ float sa[kMergeBatch];
-    __shared__ float sm[kMergeBatch];
-    __shared__ float ms[2];
-    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-    const int cg = c / kGroups;
+// Chan merge of one group's chunk partials (chunks of `chunk` pixels, the last
+// one short) by one wave: the terms of both sums are formed by all lanes and
+// lane 0 adds them in chunk order, so the result is the sequential merge of
+// _merge.  ms[0] = mean, ms[1] = rstd on return (after a barrier).
+__device__ void gn_merge_group(const float* __restrict__ pa, const float* __restrict__ pm, int hw, int nchunk,
+                               int chunk, int cg, float eps, float* sa, float* sm, float* ms) {
+    const int tid = threadIdx.x;
     const float total = (float)(hw * cg);
-    const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
-    const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
-
-    // The terms of both sums are formed by all lanes; lane 0 adds them in chunk
-    // order, so the result is the sequential merge of _merge.
     // pass 1: mean = (sum_j avg_j * n_j) / N
     float san = 0.0f;
     for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
@@ -227,7 +219,7 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
         __syncthreads();
         for (int i = tid; i < nb; i += 64) {
             const int jj = j0 + i;
-            const int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
+            const int cnt = hw - jj * chunk < chunk ? hw - jj * chunk : chunk;
             sa[i] = pa[jj] * (float)(cnt * cg);
         }
         __syncthreads();
@@ -246,7 +238,7 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
         __syncthreads();
         for (int i = tid; i < nb; i += 64) {
             const int jj = j0 + i;
-            const int cnt = hw - jj * kChunk < kChunk ? hw - jj * kChunk : kChunk;
+            const int cnt = hw - jj * chunk < chunk ? hw - jj * chunk : chunk;
             const float dl = pa[jj] - mean;
             const float nj = (float)(cnt * cg);
             sm[i] = pm[jj] + (nj * dl) * dl;
@@ -260,12 +252,30 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
     if (tid == 0) {
         float var = sv / total;
         if (var < 0.0f) var = 0.0f;
-        const float rstd = rsqrt_rn(var + eps);
-        stats[(t * kGroups + g) * 2] = mean;
-        stats[(t * kGroups + g) * 2 + 1] = rstd;
-        ms[1] = rstd;
+        ms[1] = rsqrt_rn(var + eps);
     }
     __syncthreads();
+}
+
+__global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
+                                               const uint32_t* __restrict__ vmax, const uint32_t* __restrict__ vmin,
+                                               const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+                                               int hw, int nchunk, int c, float eps, float* __restrict__ stats,
+                                               uint32_t* __restrict__ amax_bits) {
+    __shared__ float sa[kMergeBatch];
+    __shared__ float sm[kMergeBatch];
+    __shared__ float ms[2];
+    const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const int cg = c / kGroups;
+    const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
+    const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
+
+    gn_merge_group(pa, pm, hw, nchunk, kChunk, cg, eps, sa, sm, ms);
+    if (tid == 0) {
+        stats[(t * kGroups + g) * 2] = ms[0];
+        stats[(t * kGroups + g) * 2 + 1] = ms[1];
+    }
+    const float mean = ms[0];
     // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map
     float cand = 0.0f;
     if (tid < cg) {
@@ -457,6 +467,220 @@ void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
                        d, h, w, amax_bits, lut, q, scale);
 }
 
+// ---------------------------------------------------------------------------
+// fp16-output producer of the encoder suffix (opt/encoder_fused_batched_norm.py
+// :15-66, `batched_temporal_norm_pack`): per-frame GroupNorm(32) statistics of
+// every (batch item, frame), then y = fp16(SiLU(fp16(((v - mean) * rstd) *
+// gamma + beta))) into fp16 NDHWC [B, D+2, H+2, W+2, C], two zero frames and a
+// reflect border per batch item.  C in {128, 256, 512, 1024}.
+//
+// Statistics order (shared with the CPU oracle's gn_stats): TPP threads per
+// pixel, C/8 of them up to C = 256 and one per group above; each thread covers
+// CPT = C/TPP channels (GPT whole groups), sums a group's channels left to
+// right per pixel and adds the pixel sums of its pixels pl, pl+PL, ... of the
+// chunk (PL = 256/TPP); lanes combine by the halving tree.  Chunks hold 256
+// pixels up to C = 256 and 65536/C above, so a thread's slice of a chunk stays
+// in 64-128 VGPRs for both passes.  For C <= 256 this is gn_partial's order.
+// ---------------------------------------------------------------------------
+template <int C>
+struct GnGeom {
+    static constexpr int CG = C / kGroups;
+    static constexpr int CPT = C <= 256 ? 8 : CG;
+    static constexpr int TPP = C / CPT;
+    static constexpr int PL = kNT / TPP;
+    static constexpr int CHUNK = C <= 256 ? kChunk : 65536 / C;
+    static constexpr int STEPS = CHUNK / PL;
+    static constexpr int GPT = CPT / CG;
+    static constexpr int NV = CPT / 8;
+    static_assert(TPP * PL == kNT && STEPS * PL == CHUNK && GPT >= 1, "statistics geometry");
+};
+
+int gn_chunk(int c) { return c <= 256 ? kChunk : 65536 / c; }
+
+template <int C, bool PRE_BIAS>
+__global__ __launch_bounds__(kNT) void gn_stats_partial(const uint16_t* __restrict__ x,
+                                                        const uint16_t* __restrict__ pre_bias, int hw, int nchunk,
+                                                        float* __restrict__ part_avg, float* __restrict__ part_m2) {
+    using G = GnGeom<C>;
+    __shared__ float red[G::PL][kGroups];
+    __shared__ float avg_s[kGroups];
+    const int j = blockIdx.x, t = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int cv = tid % G::TPP, pl = tid / G::TPP;
+    const int p0 = j * G::CHUNK;
+    const int npix = hw - p0 < G::CHUNK ? hw - p0 : G::CHUNK;
+    const uint16_t* base = x + ((int64_t)t * hw + p0) * C + cv * G::CPT;
+
+    float pb[G::CPT];
+#pragma unroll
+    for (int e = 0; e < G::CPT; ++e) pb[e] = PRE_BIAS ? h2f(pre_bias[cv * G::CPT + e]) : 0.0f;
+    u16x8 xr[G::STEPS][G::NV];
+#pragma unroll
+    for (int s = 0; s < G::STEPS; ++s) {
+        const int p = pl + s * G::PL;
+        if (p < npix)
+#pragma unroll
+            for (int u = 0; u < G::NV; ++u) xr[s][u] = *reinterpret_cast<const u16x8*>(base + (int64_t)p * C + 8 * u);
+    }
+    auto load = [&](int s, float* v) {
+#pragma unroll
+        for (int u = 0; u < G::NV; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[8 * u + e] = h2f(xr[s][u][e]);
+        if constexpr (PRE_BIAS) {
+#pragma unroll
+            for (int e = 0; e < G::CPT; ++e) v[e] = rt16(v[e] + pb[e]);
+        }
+    };
+    float ls[G::GPT];
+#pragma unroll
+    for (int gi = 0; gi < G::GPT; ++gi) ls[gi] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < G::STEPS; ++s) {
+        const int p = pl + s * G::PL;
+        if (p >= npix) break;
+        float v[G::CPT];
+        load(s, v);
+#pragma unroll
+        for (int gi = 0; gi < G::GPT; ++gi) {
+            float ps = v[gi * G::CG];
+#pragma unroll
+            for (int i = 1; i < G::CG; ++i) ps = ps + v[gi * G::CG + i];
+            ls[gi] = ls[gi] + ps;
+        }
+    }
+#pragma unroll
+    for (int gi = 0; gi < G::GPT; ++gi) red[pl][cv * G::GPT + gi] = ls[gi];
+    __syncthreads();
+    if (tid < kGroups) {
+        for (int off = G::PL / 2; off >= 1; off >>= 1)
+            for (int i = 0; i < off; ++i) red[i][tid] = red[i][tid] + red[i + off][tid];
+        avg_s[tid] = red[0][tid] / (float)(npix * G::CG);
+    }
+    __syncthreads();
+    float a[G::GPT], lm[G::GPT];
+#pragma unroll
+    for (int gi = 0; gi < G::GPT; ++gi) {
+        a[gi] = avg_s[cv * G::GPT + gi];
+        lm[gi] = 0.0f;
+    }
+#pragma unroll
+    for (int s = 0; s < G::STEPS; ++s) {
+        const int p = pl + s * G::PL;
+        if (p >= npix) break;
+        float v[G::CPT];
+        load(s, v);
+#pragma unroll
+        for (int gi = 0; gi < G::GPT; ++gi) {
+            float dv = v[gi * G::CG] - a[gi];
+            float pm = dv * dv;
+#pragma unroll
+            for (int i = 1; i < G::CG; ++i) {
+                dv = v[gi * G::CG + i] - a[gi];
+                pm = pm + dv * dv;
+            }
+            lm[gi] = lm[gi] + pm;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int gi = 0; gi < G::GPT; ++gi) red[pl][cv * G::GPT + gi] = lm[gi];
+    __syncthreads();
+    if (tid < kGroups) {
+        for (int off = G::PL / 2; off >= 1; off >>= 1)
+            for (int i = 0; i < off; ++i) red[i][tid] = red[i][tid] + red[i + off][tid];
+        const int64_t dst = ((int64_t)t * kGroups + tid) * nchunk + j;
+        part_avg[dst] = avg_s[tid];
+        part_m2[dst] = red[0][tid];
+    }
+}
+
+__global__ __launch_bounds__(64) void gn_stats_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
+                                                     int hw, int nchunk, int chunk, int c, float eps,
+                                                     float* __restrict__ stats) {
+    __shared__ float sa[kMergeBatch];
+    __shared__ float sm[kMergeBatch];
+    __shared__ float ms[2];
+    const int g = blockIdx.x, t = blockIdx.y;
+    const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
+    const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
+    gn_merge_group(pa, pm, hw, nchunk, chunk, c / kGroups, eps, sa, sm, ms);
+    if (threadIdx.x == 0) {
+        stats[(t * kGroups + g) * 2] = ms[0];
+        stats[(t * kGroups + g) * 2 + 1] = ms[1];
+    }
+}
+
+// One block per padded output row (batch item, padded frame, padded row): the
+// source row follows from the row index alone; the 256 threads stride the row
+// in steps that are a multiple of C/8, so each keeps one 8-channel slice.
+template <int C, bool PRE_BIAS>
+__global__ __launch_bounds__(kNT) void norm_pack_f16(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ pre_bias,
+                                                     const uint16_t* __restrict__ gamma,
+                                                     const uint16_t* __restrict__ beta, const float* __restrict__ stats,
+                                                     int d, int h, int w, uint16_t* __restrict__ y) {
+    constexpr int CG = C / kGroups;
+    constexpr int TPP = C / 8;
+    constexpr int NG = 8 / CG > 1 ? 8 / CG : 1;   // groups touched by one 8-channel slice
+    static_assert(kNT % TPP == 0, "threads stride whole pixels");
+    const int hp = h + 2, wp = w + 2;
+    const int row = blockIdx.x;                     // (b * (d + 2) + tp) * hp + ii
+    const int ii = row % hp;
+    const int bt2 = row / hp;
+    const int tp = bt2 % (d + 2), b = bt2 / (d + 2);
+    const int t = tp - 2;
+    const int rowvec = wp * TPP;
+    uint16_t* dst = y + (int64_t)row * rowvec * 8;
+    if (t < 0) {   // causal zero frames
+        for (int j = threadIdx.x; j < rowvec; j += kNT) *reinterpret_cast<u16x8*>(dst + (int64_t)j * 8) = u16x8{};
+        return;
+    }
+    const int cv = threadIdx.x % TPP;
+    float gm[8], btv[8], pb[8] = {};
+    load8(gamma + cv * 8, gm);
+    load8(beta + cv * 8, btv);
+    if constexpr (PRE_BIAS) load8(pre_bias + cv * 8, pb);
+    const int frame = b * d + t;
+    const int g0 = cv * 8 / CG;
+    float mean[NG], rstd[NG];
+#pragma unroll
+    for (int k = 0; k < NG; ++k) {
+        mean[k] = stats[(frame * kGroups + g0 + k) * 2];
+        rstd[k] = stats[(frame * kGroups + g0 + k) * 2 + 1];
+    }
+    const uint16_t* src = x + ((int64_t)frame * h + reflect(ii - 1, h)) * w * C + cv * 8;
+    for (int j = threadIdx.x; j < rowvec; j += kNT) {
+        const u16x8 xv = *reinterpret_cast<const u16x8*>(src + (int64_t)reflect(j / TPP - 1, w) * C);
+        u16x8 out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float ve = h2f(xv[e]);
+            if constexpr (PRE_BIAS) ve = rt16(ve + pb[e]);
+            const int k = (NG > 1) ? e / CG : 0;
+            const float z = rt16(((ve - mean[k]) * rstd[k]) * gm[e] + btv[e]);
+            out[e] = f2h(silu_fast(z));
+        }
+        *reinterpret_cast<u16x8*>(dst + (int64_t)j * 8) = out;
+    }
+}
+
+template <int C, bool PB>
+void launch_f16(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta, float eps,
+                int batch, int d, int h, int w, uint16_t* y, float* stats, float* ws, hipStream_t stream) {
+    const int hw = h * w, frames = batch * d;
+    const int chunk = GnGeom<C>::CHUNK;
+    const int nchunk = (hw + chunk - 1) / chunk;
+    float* part_avg = ws;
+    float* part_m2 = ws + (int64_t)frames * nchunk * kGroups;
+    hipLaunchKernelGGL((gn_stats_partial<C, PB>), dim3(nchunk, frames), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk,
+                       part_avg, part_m2);
+    hipLaunchKernelGGL(gn_stats_merge, dim3(kGroups, frames), dim3(64), 0, stream, part_avg, part_m2, hw, nchunk, chunk,
+                       C, eps, stats);
+    hipLaunchKernelGGL((norm_pack_f16<C, PB>), dim3(batch * (d + 2) * (h + 2)), dim3(kNT), 0, stream, x, pre_bias, gamma,
+                       beta, stats, d, h, w, y);
+}
+
 }  // namespace
 }  // namespace h3v
 
@@ -490,6 +714,39 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
         if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
         else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
     }
+    return launch_status(what);
+}
+
+int64_t h3v_gn_norm_pack_f16_workspace_floats(int batch, int c, int d, int h, int w) {
+    if (batch <= 0 || d <= 0 || h <= 0 || w <= 0 || (c != 128 && c != 256 && c != 512 && c != 1024)) return -1;
+    const int chunk = gn_chunk(c);
+    return 2 * (int64_t)batch * d * kGroups * (((int64_t)h * w + chunk - 1) / chunk);
+}
+
+int h3v_gn_norm_pack_f16(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta,
+                         float eps, int batch, int c, int d, int h, int w, uint16_t* y, float* stats, float* workspace,
+                         hipStream_t stream) {
+    const char* what = "h3v_gn_norm_pack_f16";
+    H3V_REQUIRE(x && gamma && beta && y && stats && workspace, "%s: null pointer argument", what);
+    H3V_REQUIRE(c == 128 || c == 256 || c == 512 || c == 1024, "%s: C must be 128, 256, 512 or 1024 (got %d)", what, c);
+    H3V_REQUIRE(batch >= 1 && d >= 1 && h >= 2 && w >= 2, "%s: requires B, D >= 1 and H, W >= 2", what);
+    H3V_REQUIRE((int64_t)batch * c * (d + 2) * (h + 2) * (w + 2) < ((int64_t)1 << 31) &&
+                    (int64_t)batch * (d + 2) * (h + 2) < ((int64_t)1 << 31),
+                "%s: padded output exceeds int32 index range", what);
+    H3V_REQUIRE(eps > 0.0f, "%s: eps must be positive", what);
+    H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(beta, 16) && (!pre_bias || aligned(pre_bias, 16)) &&
+                    aligned(y, 16) && aligned(workspace, 16),
+                "%s: x, gamma, beta, pre_bias, y and workspace need 16-byte alignment", what);
+#define H3V_F16_CASE(CC)                                                                                            \
+    if (c == CC) {                                                                                                  \
+        if (pre_bias) launch_f16<CC, true>(x, pre_bias, gamma, beta, eps, batch, d, h, w, y, stats, workspace, stream); \
+        else launch_f16<CC, false>(x, pre_bias, gamma, beta, eps, batch, d, h, w, y, stats, workspace, stream);       \
+    }
+    H3V_F16_CASE(128)
+    H3V_F16_CASE(256)
+    H3V_F16_CASE(512)
+    H3V_F16_CASE(1024)
+#undef H3V_F16_CASE
     return launch_status(what);
 }
 

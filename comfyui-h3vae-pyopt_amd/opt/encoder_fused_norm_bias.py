@@ -11,14 +11,17 @@ not applied in its epilogue; it is folded into the second producer as
 ``pre_bias`` (v = fp16(v + bias) before the statistics).  The block input
 (or its ``nin_shortcut`` projection) is added last.
 
-Without INT8 wrappers (the FP16 encoder mode, outside the INT8 hot path) the
-same producers run as PyTorch GPU ops; nothing in this file ever falls back
-from the INT8 path to them.
+Without INT8 wrappers (the FP16 encoder mode) the same producers emit fp16
+through ``h3v_gn_norm_pack_f16`` (one fused statistics + pack launch
+sequence) and the convolutions run in FP16; nothing in this file ever falls
+back from the INT8 path to them.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
+
+from .. import _hip
 
 
 def _check_channel_vectors(x, *vectors):
@@ -29,28 +32,39 @@ def _check_channel_vectors(x, *vectors):
             raise ValueError("Expected contiguous FP16 channel vectors on input device")
 
 
-def fused_temporal_norm_pad(x, weight, bias, eps, pre_bias=None):
-    """FP16 encoder mode: per-frame GroupNorm(32), SiLU, 2 causal zero frames + reflect pad 1.
+def norm_pack_f16(x, weight, bias, eps, pre_bias=None):
+    """Per-frame GroupNorm(32) + SiLU + 2 causal zero frames + reflect pad 1, fp16 out (``h3v_gn_norm_pack_f16``).
 
-    -> fp16 [1, C, D+2, H+2, W+2] channels-last-3d.  PyTorch ops on the GPU.
+    x: fp16 [B, C, D, H, W] whose batch and time are adjacent frame spans (B == 1, or
+    x.stride(0) == D * x.stride(2)); it is made channels-last-3d if it is not.  Statistics are
+    per (batch item, frame).  -> fp16 [B, C, D+2, H+2, W+2] channels-last-3d.
+    """
+    b, c, d, h, w = x.shape
+    _hip.require_gfx950(x.device, "norm_pack_f16")
+    if not x.is_contiguous(memory_format=torch.channels_last_3d):
+        x = x.contiguous(memory_format=torch.channels_last_3d)
+    y = torch.empty((b, c, d + 2, h + 2, w + 2), device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
+    stats = torch.empty((b * d, 32, 2), device=x.device, dtype=torch.float32)
+    ws = torch.empty(int(_hip.lib().h3v_gn_norm_pack_f16_workspace_floats(b, c, d, h, w)), device=x.device,
+                     dtype=torch.float32)
+    _hip.call("h3v_gn_norm_pack_f16", _hip.ptr(x), _hip.ptr(pre_bias), _hip.ptr(weight), _hip.ptr(bias), float(eps),
+              b, c, d, h, w, _hip.ptr(y), _hip.ptr(stats), _hip.ptr(ws), _hip.stream(x.device))
+    return y
+
+
+def fused_temporal_norm_pad(x, weight, bias, eps, pre_bias=None):
+    """FP16 encoder mode producer (reference opt/encoder_fused_temporal_norm.py:83-99 and
+    opt/encoder_fused_norm_bias.py:14-39): batch one, C divisible by 32 (kernel: 128 ... 1024).
+
+    -> fp16 [1, C, D+2, H+2, W+2] channels-last-3d, one ``h3v_gn_norm_pack_f16`` call.
     """
     b, c, d, h, w = x.shape
     if b != 1 or x.dtype != torch.float16 or c % 32 or min(h, w) < 2:
         raise ValueError("Validated scope: batch-one FP16, C divisible by 32, spatial >=2")
+    if c not in (128, 256, 512, 1024):
+        raise ValueError("Validated scope: C in 128, 256, 512, 1024")
     _check_channel_vectors(x, weight, bias, *(() if pre_bias is None else (pre_bias,)))
-    v = x.float()
-    if pre_bias is not None:
-        v = (v + pre_bias.float().view(1, c, 1, 1, 1)).half().float()
-    g = v.view(1, 32, c // 32, d, h, w)
-    mean = g.mean(dim=(2, 4, 5), keepdim=True)
-    var = g.var(dim=(2, 4, 5), unbiased=False, keepdim=True)
-    z = ((g - mean) * torch.rsqrt(var + eps)).view(1, c, d, h, w)
-    z = (z * weight.float().view(1, c, 1, 1, 1) + bias.float().view(1, c, 1, 1, 1)).half().float()
-    z = (z / (1.0 + torch.exp(-z))).half()
-    z = F.pad(z, (1, 1, 1, 1, 0, 0), mode="reflect")
-    y = torch.zeros((b, c, d + 2, h + 2, w + 2), device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
-    y[:, :, 2:] = z
-    return y
+    return norm_pack_f16(x, weight, bias, eps, pre_bias)
 
 
 @torch.library.custom_op("h3vae_encoder::temporal_norm_pack", mutates_args=(), device_types="cuda")

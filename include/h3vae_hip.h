@@ -62,6 +62,22 @@ int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* 
  * SiLU over every fp16 argument.  All three are zero on a correct build. */
 int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream);
 
+/* ---- encoder suffix / FP16 mode: GroupNorm + SiLU + pad producer, fp16 out ----
+ * Replaces opt/encoder_fused_batched_norm.py:15-66 (`batched_temporal_norm_pack`,
+ * its _partial/_merge/_normalize_pack_batched kernels) and, for batch one,
+ * opt/encoder_fused_temporal_norm.py:83-99 / opt/encoder_fused_norm_bias.py:14-39.
+ * x: fp16 NDHWC [batch * d, h, w, c] (batch and time adjacent), c in
+ * {128, 256, 512, 1024}; optional pre_bias [c] (v = fp16(v + pre_bias) first).
+ * Per-frame GroupNorm(32) statistics of every (batch item, frame) -> stats fp32
+ * [batch * d, 32, 2] (mean, rstd); y: fp16 NDHWC [batch, d+2, h+2, w+2, c] =
+ * fp16(SiLU(fp16(((v - mean) * rstd) * gamma + beta))), two zero frames and a
+ * reflect border of 1 per batch item.  workspace: fp32
+ * [h3v_gn_norm_pack_f16_workspace_floats(batch, c, d, h, w)] (chunk partials). */
+int64_t h3v_gn_norm_pack_f16_workspace_floats(int batch, int c, int d, int h, int w);
+int h3v_gn_norm_pack_f16(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta,
+                         float eps, int batch, int c, int d, int h, int w, uint16_t* y, float* stats, float* workspace,
+                         hipStream_t stream);
+
 /* ---- decoder attention (head_dim 64) --------------------------------------
  * Replaces the model's `perform_attention` (flash attention) called from
  * opt/decoder_fused_qk_rope.py:66-74 (`FusedQKAttention.forward`) between the

@@ -386,8 +386,9 @@ API void ora_conv3d_acc(const int8_t* qx, const int8_t* qw, int32_t* acc,
 /*
  * x: fp16 NDHWC [D, H, W, C] (batch one).  Optional pre_bias: v = fp16(v + b[c]).
  * Fixed order (shared with csrc/gn_pack.hip):
- *   chunks of 256 pixels; inside a chunk, "pixel lane" pl = 0..PL-1 with
- *   PL = 256 / (C/8) owns pixels pl, pl+PL, ...; for each group (cg = C/32
+ *   chunks of 256 pixels (65536 / C for C > 256); inside a chunk, "pixel lane"
+ *   pl = 0..PL-1 with PL = 256 / TPP (TPP = C/8 threads per pixel for C <= 256,
+ *   32 above: one per group) owns pixels pl, pl+PL, ...; for each group (cg = C/32
  *   channels) the lane sums channel values left to right per pixel, then adds
  *   that pixel sum to its running sum; lanes combine by the halving tree
  *   (off = PL/2 .. 1).  avg = S / n.  Second pass the same with
@@ -409,10 +410,11 @@ API void ora_gn_stats(const uint16_t* x, const uint16_t* pre_bias, int d, int h,
                       float eps, float* stats) {
     int hw = h * w;
     int cg = c / GN_GROUPS;
-    int tpp = c / 8;
+    int tpp = c <= 256 ? c / 8 : 32;
+    int chunk = c <= 256 ? GN_CHUNK : 65536 / c;
     int pl_n = 256 / tpp;
-    int steps = GN_CHUNK / pl_n;
-    int nchunk = (hw + GN_CHUNK - 1) / GN_CHUNK;
+    int steps = chunk / pl_n;
+    int nchunk = (hw + chunk - 1) / chunk;
     #pragma omp parallel for schedule(static)
     for (int t = 0; t < d; ++t) {
         float* avg = (float*)malloc(sizeof(float) * (size_t)nchunk * GN_GROUPS);
@@ -420,8 +422,8 @@ API void ora_gn_stats(const uint16_t* x, const uint16_t* pre_bias, int d, int h,
         int* cnt = (int*)malloc(sizeof(int) * (size_t)nchunk);
         float lanes[256];
         for (int j = 0; j < nchunk; ++j) {
-            int p0 = j * GN_CHUNK;
-            int npix = hw - p0 < GN_CHUNK ? hw - p0 : GN_CHUNK;
+            int p0 = j * chunk;
+            int npix = hw - p0 < chunk ? hw - p0 : chunk;
             cnt[j] = npix;
             for (int g = 0; g < GN_GROUPS; ++g) {
                 float n = (float)(npix * cg);

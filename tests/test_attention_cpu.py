@@ -35,3 +35,21 @@ def test_attention_fake_shape_and_strided_v(qk):
     q = torch.empty(2, 9, 3, 64, dtype=torch.float16, device="meta")
     out = torch.ops.h3vae_decoder.attention_d64(q, q, v, 0.125)
     assert out.shape == (2, 9, 3, 64) and out.is_contiguous()
+
+
+def test_batched_norm_pack_guards_on_meta(pkg):
+    """Reference opt/encoder_fused_batched_norm.py:37-49 scope checks, raised by the op's fake as well."""
+    bn = importlib.import_module(f"{pkg.__name__}.opt.encoder_fused_batched_norm")
+    op = torch.ops.h3vae_encoder.batched_temporal_norm_pack
+    c = 256
+    x = torch.empty(4, c, 3, 8, 8, dtype=torch.float16, device="meta").contiguous(memory_format=torch.channels_last_3d)
+    v = torch.empty(c, dtype=torch.float16, device="meta")
+    y = op(x, None, v, v, 1e-6)
+    assert y.shape == (4, c, 5, 10, 10) and y.is_contiguous(memory_format=torch.channels_last_3d)
+    with pytest.raises(ValueError, match="B=1/3/4"):
+        op(x[:2], None, v, v, 1e-6)
+    with pytest.raises(ValueError, match="adjacent"):
+        op(x.contiguous(), None, v, v, 1e-6)
+    with pytest.raises(ValueError, match="channel vectors"):
+        op(x, v[:8], v, v, 1e-6)
+    assert bn.fused_suffix is not None
