@@ -399,6 +399,28 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
 
         out["attention_h3_4x1797x32x64"] = attention_case(4, 1797, 32)
         out["attention_cfg4_1x16384x16x64"] = attention_case(1, 16384, 16)
+
+        # encoder suffix FP16 3x3x3 convs of a staged batch of 4 clips (the producer's padded channels-last
+        # output, two causal zero frames per clip): h3v_conv3d_f16 and the model's F.conv3d on the same
+        # operands; flops count the dense reduction (the kernel also skips the causal-zero taps)
+        def suffix_conv_case(b, c, d, hw):
+            xs = randn(b, c, d + 2, hw + 2, hw + 2).contiguous(memory_format=torch.channels_last_3d)
+            xs[:, :, :2] = 0
+            ws = randn(c, c, 3, 3, 3, scale=(27 * c) ** -0.5)
+            wsp = ws.permute(0, 2, 3, 4, 1).reshape(c, -1).contiguous()
+            bs = randn(c, scale=0.1)
+            ys = torch.empty((b, c, d, hw, hw), device=dev, dtype=f16).contiguous(memory_format=torch.channels_last_3d)
+            t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), p(ys), b, c, d + 2, hw + 2, hw + 2, c, 1,
+                                     stream))
+            t_t = timed(lambda: F.conv3d(xs, ws, bs))
+            xn = xs.contiguous()
+            t_n = timed(lambda: F.conv3d(xn, ws, bs))
+            flops = 2 * b * d * hw * hw * c * 27 * c
+            return {"h3v_conv3d_f16": fp16_mfma(t_c, flops), "torch_conv3d": fp16_mfma(t_t, flops),
+                    "torch_conv3d_ncdhw": fp16_mfma(t_n, flops)}
+
+        out["suffix_conv_f16_4x256x9x64x64"] = suffix_conv_case(4, 256, 9, 64)
+        out["suffix_conv_f16_4x512x5x32x32"] = suffix_conv_case(4, 512, 5, 32)
     torch.cuda.synchronize()
     return out
 

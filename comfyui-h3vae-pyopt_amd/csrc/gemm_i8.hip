@@ -33,7 +33,12 @@ namespace h3v {
 namespace {
 
 enum class AMode { Gemm, Conv };
-enum class Epi { Dequant, SwiGLU, Int32 };
+// Dequant: fp16(fma(fp32(acc) * sx, sw, bias)); SwiGLU: paired gate/up then SiLU(gate) * up;
+// Int32: raw accumulators; F16Bias: fp16 operands with fp32 accumulators, fp16(acc + bias).
+enum class Epi { Dequant, SwiGLU, Int32, F16Bias };
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 struct GemmParams {
     const int8_t* a;
@@ -223,9 +228,10 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 // int32 accumulators of the workgroup's BM x BN tile at (m0, n0), weight tile
 // tn, is dequantized (or stored raw) to the output.  LDS_BYTES of LDS (the
 // operand rings, idle by now) stage the fp16 tile.
-template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP>
-__device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM / WGM / 32][BN / WGN / 32],
+template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, typename AccV>
+__device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM / WGM / 32][BN / WGN / 32],
                                            int8_t* smem, int m0, int n0, int tn) {
+    static_assert((EP == Epi::F16Bias) == std::is_same<AccV, f32x16>::value, "fp32 accumulators with F16Bias only");
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -286,7 +292,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM /
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
             const int row = m0 + wm * WM + i * 32 + mrow;
-            sxr[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
+            sxr[i] = (EP != Epi::F16Bias && row < p.M) ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
         }
         // one instantiation per bias presence (uniform per launch)
         auto convert = [&](auto hb) {
@@ -295,7 +301,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM /
         // latency overlaps it: FN * 4 quads (SwiGLU: FN / 2 * 4 gate/up pairs)
         constexpr int NQ = FN * 4;
         int qc[NQ], ql[NQ];
-        f32x4 qsw[NQ];
+        f32x4 qsw[NQ] = {};
         u16x4 qb[NQ];
         if constexpr (EP == Epi::SwiGLU) {
 #pragma unroll
@@ -318,7 +324,25 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM /
                     ql[j * 4 + q4] = p.N;
                 }
         }
-        load_cols<NQ, HB>(p, qc, ql, qsw, qb);
+        if constexpr (EP == Epi::F16Bias) {
+            // bias only: clamped columns, one 8-byte load per quad when aligned
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+                if constexpr (HB) {
+                    if (p.vec_epi) {
+                        const int cc = qc[q] < ql[q] - 4 ? qc[q] : ql[q] - 4;
+                        qb[q] = *reinterpret_cast<const u16x4*>(p.bias + cc);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) qb[q][e] = p.bias[qc[q] + e < ql[q] ? qc[q] + e : ql[q] - 1];
+                    }
+                } else {
+                    qb[q] = u16x4{0, 0, 0, 0};
+                }
+            }
+        } else {
+            load_cols<NQ, HB>(p, qc, ql, qsw, qb);
+        }
         lds_barrier();   // every wave has finished reading operand fragments
         if constexpr (EP == Epi::SwiGLU) {
 #pragma unroll
@@ -351,7 +375,14 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, v16i (&acc)[BM /
                     for (int i = 0; i < FM; ++i) {
                         u16x4 v;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]));
+                        for (int e = 0; e < 4; ++e) {
+                            if constexpr (EP == Epi::F16Bias) {
+                                const float a = acc[i][j][q4 * 4 + e];
+                                v[e] = f2h(HB ? a + h2f(qb[q][e]) : a);
+                            } else {
+                                v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]));
+                            }
+                        }
                         put(wm * WM + i * 32 + mrow, tc, v);
                     }
                 }
@@ -631,8 +662,13 @@ constexpr int halo_lds_bytes(int wo) {
 // halves are swapped when (px >> 3) & 1, which keeps the 16-lane fragment
 // reads (16 consecutive pixels, one half) on 16 distinct 16-byte bank groups.
 // Weight rows (tap, n) are swizzled the same way by (n >> 3) & 1.
-template <int WO, Epi EP>
+// ES = 1: int8 operands, v_mfma_i32_32x32x32_i8, int32 accumulators (32 channels per 32-byte slice);
+// ES = 2: fp16 operands, v_mfma_f32_32x32x16_f16, fp32 accumulators (16 channels per slice).  Both
+// MFMAs read 16 bytes per lane in the same row / k-half layout, so staging and fragments are shared.
+template <int WO, Epi EP, int ES = 1>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
+    static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
+    using Acc = std::conditional_t<ES == 1, v16i, f32x16>;
     constexpr int BM = 512, BN = 128, WGM = 4, WGN = 2, NWD = 4;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -645,7 +681,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int STAGE = HB + WB;
     constexpr int NH = HB / 1024 / NWD, NWT = WB / 1024 / NWD; // DMA instructions per issuing wave and stage
     constexpr int LDS = 2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2;
-    static_assert(WO == 64 || WO == 128 || WO == 256, "output width");
+    static_assert(WO == 32 || WO == 64 || WO == 128 || WO == 256, "output width");
     static_assert(LDS <= 163840, "LDS");
     static_assert(LDS == halo_lds_bytes(WO), "host and kernel LDS sizes");
     static_assert(NH + NWT < 64, "outstanding DMA must fit vmcnt");
@@ -670,10 +706,11 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     const int oh0 = rb * RO;
     const int m0 = (fr * p.Ho + oh0) * WO;
     const int n0 = tn * BN;
-    const int CQ = p.C / 32;
+    const int CB = p.C * ES;                                  // bytes per pixel
+    const int CQ = CB / 32;                                   // 32-byte channel slices
     const int kd0 = (p.causal_skip && od < 2) ? 2 - od : 0;
-    const int nst = (3 - kd0) * CQ;                           // even: C % 64 == 0
-    const uint32_t frame_bytes = (uint32_t)p.Hp * p.Wp * p.C;
+    const int nst = (3 - kd0) * CQ;                           // even: C * ES % 64 == 0
+    const uint32_t frame_bytes = (uint32_t)p.Hp * p.Wp * CB;
 
     const bool dma_wave = wave < NWD;
     const int dw = dma_wave ? wave : 0;
@@ -682,7 +719,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     // per-lane DMA source offsets; the stage adds kd and the channel slice as the uniform offset
     uint32_t hoff[NH], woff[NWT];
     {
-        const uint32_t tile_base = (uint32_t)(((int64_t)(bi * p.Dp + od) * p.Hp + oh0) * p.Wp * p.C);
+        const uint32_t tile_base = (uint32_t)(((int64_t)(bi * p.Dp + od) * p.Hp + oh0) * p.Wp * CB);
 #pragma unroll
         for (int j = 0; j < NH; ++j) {
             const int s16 = (dw + NWD * j) * 64 + lane;       // 16-byte slot of the window buffer
@@ -692,7 +729,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
             // padding slots load a valid in-window pixel; they are never read
             if (hr >= HR) hr = HR - 1;
             if (px > WO + 1) px = WO + 1;
-            hoff[j] = tile_base + (uint32_t)((hr * p.Wp + px) * p.C + half * 16);
+            hoff[j] = tile_base + (uint32_t)((hr * p.Wp + px) * CB + half * 16);
         }
 #pragma unroll
         for (int j = 0; j < NWT; ++j) {
@@ -700,14 +737,14 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
             const int row = s16 >> 1;                         // tap * 128 + n
             const int t9 = row >> 7, n = row & 127;
             const int half = (s16 & 1) ^ ((n >> 3) & 1);
-            woff[j] = (uint32_t)(n0 + n) * (uint32_t)p.K + (uint32_t)(t9 * p.C + half * 16);
+            woff[j] = (uint32_t)(n0 + n) * (uint32_t)(p.K * ES) + (uint32_t)(t9 * CB + half * 16);
         }
     }
     auto issue = [&](int kd, int cq, int slot) {
         if (!dma_wave) return;
         int8_t* base = smem + slot * STAGE;
         const uint32_t sh = (uint32_t)kd * frame_bytes + (uint32_t)cq * 32;
-        const uint32_t sw = (uint32_t)(kd * 9 * p.C + cq * 32);
+        const uint32_t sw = (uint32_t)(kd * 9 * CB + cq * 32);
 #pragma unroll
         for (int j = 0; j < NH; ++j) lds_dma16(ra, hoff[j], sh, base + (dw + NWD * j) * 1024);
 #pragma unroll
@@ -736,11 +773,11 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
         baddr[j] = HB + n * 32 + ((fhi ^ ((n >> 3) & 1)) << 4);
     }
 
-    v16i acc[FM][FN];
+    Acc acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+        for (int j = 0; j < FN; ++j) acc[i][j] = Acc{};
 
     auto load_frags = [&](int slot, int t9, v4i (&af)[FM], v4i (&bf)[FN]) {
         const int8_t* s = smem + slot * STAGE;
@@ -754,8 +791,13 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (ES == 1)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, bf[j]),
+                                                                      __builtin_bit_cast(half8, af[i]), acc[i][j], 0, 0, 0);
+            }
     };
 
     // stage s covers depth tap kd0 + s / CQ and channel slice s % CQ; the issue
@@ -889,16 +931,16 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     return launch_status(what);
 }
 
-// Stride-1 3x3x3 convolution through conv3_halo_i8: requires C % 64 == 0,
-// N % 128 == 0, Wo in {64, 128, 256} and Ho a multiple of 512 / Wo.
-bool halo_conv_fits(const GemmParams& p) {
+// Stride-1 3x3x3 convolution through conv3_halo_i8 with ES-byte elements: requires
+// C * ES % 64 == 0, N % 128 == 0, Wo in {32, 64, 128, 256} and Ho a multiple of 512 / Wo.
+bool halo_conv_fits(const GemmParams& p, int es = 1) {
     const bool shape = p.KH == 3 && p.KW == 3 && p.K == 27 * p.C && p.SD == 1 && p.SH == 1 && p.SW == 1 &&
-                       p.C % 64 == 0 && p.N % 128 == 0 && (p.Wo == 64 || p.Wo == 128 || p.Wo == 256) &&
-                       p.Ho % (512 / p.Wo) == 0;
-    return shape && aligned(p.a, 16) && aligned(p.b, 16) && (int64_t)p.Hp * p.Wp * p.C * 3 < ((int64_t)1 << 31);
+                       (p.C * es) % 64 == 0 && p.N % 128 == 0 &&
+                       (p.Wo == 32 || p.Wo == 64 || p.Wo == 128 || p.Wo == 256) && p.Ho % (512 / p.Wo) == 0;
+    return shape && aligned(p.a, 16) && aligned(p.b, 16) && (int64_t)p.Hp * p.Wp * p.C * es * 3 < ((int64_t)1 << 31);
 }
 
-template <int WO, Epi EP>
+template <int WO, Epi EP, int ES = 1>
 int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.tiles_m = p.M / 512;
     p.tiles_n = p.N / 128;
@@ -906,8 +948,8 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
     p.conv_tpf = 0;
     const int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
-    const int64_t a_bytes = (int64_t)(p.M / ((int64_t)p.Do * p.Ho * p.Wo)) * p.Dp * p.Hp * p.Wp * p.C;
-    const int64_t b_bytes = (int64_t)p.N * p.K;
+    const int64_t a_bytes = (int64_t)(p.M / ((int64_t)p.Do * p.Ho * p.Wo)) * p.Dp * p.Hp * p.Wp * p.C * ES;
+    const int64_t b_bytes = (int64_t)p.N * p.K * ES;
     if (a_bytes >= ((int64_t)1 << 32) || b_bytes >= ((int64_t)1 << 31))
         return fail(H3V_EINVAL, "%s: an operand exceeds the 32-bit offset range (%lld, %lld bytes)", what,
                     (long long)a_bytes, (long long)b_bytes);
@@ -915,7 +957,7 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.b_bytes = (uint32_t)b_bytes;
     constexpr int lds = halo_lds_bytes(WO);
     static_assert(lds <= 163840, "LDS exceeds 160 KB");
-    auto kernel = &conv3_halo_i8<WO, EP>;
+    auto kernel = &conv3_halo_i8<WO, EP, ES>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, lds,
@@ -951,7 +993,8 @@ int run_conv(GemmParams p, hipStream_t stream, const char* what) {
     if (halo_conv_fits(p)) {
         if (p.Wo == 256) return launch_halo<256, EP>(p, stream, what);
         if (p.Wo == 128) return launch_halo<128, EP>(p, stream, what);
-        return launch_halo<64, EP>(p, stream, what);
+        if (p.Wo == 64) return launch_halo<64, EP>(p, stream, what);
+        return launch_halo<32, EP>(p, stream, what);
     }
     if (al && p.C % 128 == 0) {
         if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, EP>(p, stream, what);
@@ -1056,6 +1099,27 @@ int h3v_conv3d_i8(const int8_t* qx, const float* x_scale, const int8_t* qw, cons
     p.a = qx; p.b = qw; p.sx = x_scale; p.sx_stride = 0; p.sw = w_scale; p.bias = bias; p.out = out;
     p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
     return run_conv<Epi::Dequant>(p, stream, what);
+}
+
+int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int batch, int cin,
+                    int d, int h, int wd, int cout, int causal_skip, hipStream_t stream) {
+    const char* what = "h3v_conv3d_f16";
+    H3V_REQUIRE(x && w && out, "%s: null pointer argument", what);
+    GemmParams p{};
+    int rc = fill_conv(p, what, batch, cin, d, h, wd, cout, 3, 3, 3, 1, 1, 1);
+    if (rc) return rc;
+    p.a = reinterpret_cast<const int8_t*>(x);
+    p.b = reinterpret_cast<const int8_t*>(w);
+    p.bias = bias;
+    p.out = out;
+    p.causal_skip = causal_skip ? 1 : 0;
+    H3V_REQUIRE(halo_conv_fits(p, 2), "%s: requires Cin %% 32 == 0, Cout %% 128 == 0, an output width of 32, 64, 128 or "
+                "256, an output height that is a multiple of 512 / width and 16-byte aligned x and w (got Cin %d, Cout "
+                "%d, output %dx%d)", what, cin, cout, p.Ho, p.Wo);
+    if (p.Wo == 256) return launch_halo<256, Epi::F16Bias, 2>(p, stream, what);
+    if (p.Wo == 128) return launch_halo<128, Epi::F16Bias, 2>(p, stream, what);
+    if (p.Wo == 64) return launch_halo<64, Epi::F16Bias, 2>(p, stream, what);
+    return launch_halo<32, Epi::F16Bias, 2>(p, stream, what);
 }
 
 int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,

@@ -24,8 +24,11 @@ Differences from the reference runtime, all deliberate:
 * No tracing compiler: ``compile_decoder`` / ``compile_encoder`` are accepted
   and recorded but nothing is handed to torch.compile; the hot operators are
   already single hand-written kernels.
-* The FP16 encoder suffix runs as the model's own modules
-  (``EncoderSuffix``) rather than a fused-normalisation variant.
+* The FP16 encoder suffix is the reference's clip-batched ``fused_suffix``
+  (all stages): per-frame GroupNorm/SiLU/pad producers as
+  ``h3v_gn_norm_pack_f16`` and the 3x3x3 stride-1 convolutions that fit as
+  ``h3v_conv3d_f16``; downsample, shortcut and conv_out convolutions stay the
+  model's.
 """
 from __future__ import annotations
 
@@ -199,7 +202,8 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         from .opt.decoder_fused_qk_rope import clone_with_qk_fusion
         from .opt.encoder_fused_norm_next import next_fused_prefix
         from .opt.encoder_internal_padding import replace_selected
-        from .opt.encoder_staged_batch import EncoderSuffix, encode_staged
+        from .opt.encoder_fused_batched_norm import fused_suffix
+        from .opt.encoder_staged_batch import encode_staged
         self._encode_staged = encode_staged
 
         if core is None:
@@ -241,7 +245,7 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         quant = core.quant_conv.to(memory_format=torch.channels_last_3d)
         replace_selected(enc, ["down.0.downsample.conv"])
         prefix = next_fused_prefix(enc, "extend_bias_pack")
-        suffix = EncoderSuffix(enc, quant, 2)
+        suffix = fused_suffix(enc, quant, all_stages=True)
         metadata = None
         if int8_encode:
             from .opt.encoder_int8_integration import install_int8_encoder_prefix

@@ -78,6 +78,20 @@ int h3v_gn_norm_pack_f16(const uint16_t* x, const uint16_t* pre_bias, const uint
                          float eps, int batch, int c, int d, int h, int w, uint16_t* y, float* stats, float* workspace,
                          hipStream_t stream);
 
+/* FP16 3x3x3 stride-1 valid convolution of a padded input (the model's FP16
+ * encoder convs after the producer above: opt/encoder_fused_batched_norm.py
+ * :70-72,83-86, F.conv3d on cuDNN in the reference).  x: fp16 NDHWC
+ * [batch, d, h, wd, cin] (already padded: causal frames and reflect border);
+ * w: fp16 [cout, 27 * cin] packed (kd, kh, kw, c) with c fastest; bias: fp16
+ * [cout] (nullable); out: fp16 NDHWC [batch, d-2, h-2, wd-2, cout] =
+ * fp16(sum fp32 + bias) with fp32 accumulation on v_mfma_f32_32x32x16_f16.
+ * causal_skip: output frames 0 and 1 of each batch item skip the depth taps
+ * that read the two leading zero frames.  Requires cin % 32 == 0, cout % 128
+ * == 0, an output width of 32, 64, 128 or 256 and an output height that is a
+ * multiple of 512 / width (one tile = whole rows of one frame). */
+int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int batch, int cin,
+                   int d, int h, int wd, int cout, int causal_skip, hipStream_t stream);
+
 /* ---- decoder attention (head_dim 64) --------------------------------------
  * Replaces the model's `perform_attention` (flash attention) called from
  * opt/decoder_fused_qk_rope.py:66-74 (`FusedQKAttention.forward`) between the

@@ -43,11 +43,13 @@ CASES = [
     (128, 128, (1, 128, 5, 17, 33), (3, 3, 3), (1, 2, 2)),
     (128, 128, (1, 128, 3, 10, 18), (1, 3, 3), (1, 1, 1)),
     (64, 128, (2, 64, 4, 6, 70), (3, 3, 3), (1, 1, 1)),
-    # window-in-LDS kernel (stride 1, C % 64 == 0, N % 128 == 0, Wo in {64, 128, 256})
+    # window-in-LDS kernel (stride 1, C % 64 == 0, N % 128 == 0, Wo in {32, 64, 128, 256})
     (64, 128, (1, 64, 4, 4, 258), (3, 3, 3), (1, 1, 1)),
     (128, 256, (2, 128, 4, 10, 66), (3, 3, 3), (1, 1, 1)),
     (128, 128, (1, 128, 5, 6, 130), (3, 3, 3), (1, 1, 1)),
     (256, 128, (1, 256, 3, 6, 130), (3, 3, 3), (1, 1, 1)),
+    (128, 128, (1, 128, 4, 18, 34), (3, 3, 3), (1, 1, 1)),     # output width 32
+    (256, 256, (3, 256, 5, 18, 34), (3, 3, 3), (1, 1, 1)),
 ]
 
 

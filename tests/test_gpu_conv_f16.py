@@ -1,0 +1,154 @@
+"""GPU parity: the FP16 window-in-LDS 3x3x3 convolution (h3v_conv3d_f16, ``conv3d_f16``) of the encoder
+suffix against a float64 CPU convolution of the same fp16 operands.
+
+Tolerance: the kernel multiplies fp16 operands exactly, sums in fp32 on the matrix cores, adds the fp16
+bias in fp32 and rounds once to fp16, so |y - ref| <= ulp16(ref) + 2^-20 * sum|x * w| per output (one
+fp16 rounding plus the fp32 summation error with a 16x margin).  A dropped or misplaced tap moves an
+output by about one product |x * w| ~ sum|x * w| / K, far outside that bound."""
+from __future__ import annotations
+
+import importlib
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+import h3_arch
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def bn(pkg):
+    return importlib.import_module(f"{pkg.__name__}.opt.encoder_fused_batched_norm")
+
+
+def _operands(b, c, d, h, w, cout, with_bias, seed, causal_zero=True):
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(b, c, d, h, w, generator=gen).half()
+    if causal_zero:
+        x[:, :, :2] = 0                                # the producer's two causal zero frames per item
+    wt = (torch.randn(cout, c, 3, 3, 3, generator=gen) * (27 * c) ** -0.5).half()
+    bias = (0.5 * torch.randn(cout, generator=gen)).half() if with_bias else None
+    return x, wt, bias
+
+
+def _reference(x, wt, bias):
+    ref = F.conv3d(x.double(), wt.double(), None if bias is None else bias.double())
+    mag = F.conv3d(x.double().abs(), wt.double().abs())
+    return ref, mag
+
+
+def _assert_close(y, ref, mag):
+    y = y.detach().cpu().double()
+    exp = torch.floor(torch.log2(ref.abs().clamp_min(2.0 ** -14)))
+    ulp = torch.pow(2.0, exp - 10)
+    bound = ulp + 2.0 ** -20 * mag
+    err = (y - ref).abs()
+    bad = err > bound
+    assert not bool(bad.any()), (f"{int(bad.sum())} of {bad.numel()} outputs outside the bound; worst excess "
+                                 f"{float((err - bound).max()):.3e}")
+
+
+def _run(bn, x, wt, bias, causal_skip):
+    xd = x.to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    wp = bn.pack_conv_weight_f16(wt.to(DEV))
+    bd = None if bias is None else bias.to(DEV)
+    with torch.inference_mode():
+        y = bn.conv3d_f16(xd, wp, bd, causal_skip)
+    torch.cuda.synchronize()
+    return y
+
+
+# (batch, Cin, D, H, W, Cout): output widths 32 / 64 / 128 / 256, one and several items, Cin 32..512
+CASES = [
+    (1, 32, 4, 18, 34, 128, True),
+    (3, 256, 5, 10, 66, 128, True),
+    (2, 128, 4, 6, 130, 256, False),
+    (1, 64, 3, 4, 258, 128, True),
+    (4, 512, 3, 18, 34, 256, True),
+    (4, 256, 6, 34, 34, 512, False),
+]
+
+
+@pytest.mark.parametrize("b,c,d,h,w,cout,with_bias", CASES)
+def test_conv3d_f16_matches_float64(bn, b, c, d, h, w, cout, with_bias):
+    print(f"conv3d_f16 B={b} C={c} D={d} {h}x{w} Cout={cout} bias={with_bias}", flush=True)
+    x, wt, bias = _operands(b, c, d, h, w, cout, with_bias, seed=b * 1000 + c + d + h + w + cout)
+    y = _run(bn, x, wt, bias, causal_skip=True)
+    assert y.shape == (b, cout, d - 2, h - 2, w - 2) and y.dtype == torch.float16
+    assert y.is_contiguous(memory_format=torch.channels_last_3d)
+    ref, mag = _reference(x, wt, bias)
+    _assert_close(y, ref, mag)
+    # the causal skip drops only taps on zero frames: the full reduction gives the same values
+    y_full = _run(bn, x, wt, bias, causal_skip=False)
+    assert torch.equal(y_full, y)
+
+
+def test_conv3d_f16_nonzero_leading_frames_without_skip(bn):
+    """causal_skip=False reads every depth tap: leading frames that are not zero take part."""
+    x, wt, bias = _operands(2, 64, 5, 10, 66, 128, True, seed=5, causal_zero=False)
+    y = _run(bn, x, wt, bias, causal_skip=False)
+    ref, mag = _reference(x, wt, bias)
+    _assert_close(y, ref, mag)
+
+
+def test_conv3d_f16_matches_torch_fp16(bn):
+    """Same operands through the model's FP16 F.conv3d on the GPU (its own accumulation order)."""
+    x, wt, bias = _operands(3, 256, 6, 18, 66, 256, True, seed=17)
+    y = _run(bn, x, wt, bias, causal_skip=True).float()
+    ref = F.conv3d(x.to(DEV), wt.to(DEV), bias.to(DEV)).float()
+    rel = (y - ref).norm() / ref.norm()
+    assert rel < 1e-3, float(rel)
+
+
+def test_conv3d_f16_rejects_unfit_shapes(bn):
+    x, wt, bias = _operands(1, 64, 3, 6, 66, 128, True, seed=1)
+    xd = x.to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    with pytest.raises(ValueError, match="Cout % 128"):
+        bn.conv3d_f16(xd, bn.pack_conv_weight_f16(wt[:64].to(DEV)), bias[:64].to(DEV), True)
+    x2 = torch.zeros(1, 64, 3, 6, 50, dtype=torch.float16, device=DEV).contiguous(memory_format=torch.channels_last_3d)
+    with pytest.raises(ValueError, match="output width"):
+        bn.conv3d_f16(x2, bn.pack_conv_weight_f16(wt.to(DEV)), None, True)
+    with pytest.raises(ValueError, match="packed"):
+        bn.conv3d_f16(xd, wt.to(DEV).reshape(128, -1)[:, :100].contiguous(), None, True)
+
+
+@pytest.mark.parametrize("cin,cout,hw", [(256, 256, 32), (256, 512, 64)])
+def test_batched_residual_block_with_native_convs(bn, cin, cout, hw):
+    """Clips batched through BatchedResidualBlock, whose convs now fit h3v_conv3d_f16, == the model's
+    ResnetBlock3D clip by clip (FP16 tolerance: different reduction orders for statistics and convs)."""
+    torch.manual_seed(cin + cout + hw)
+    block = h3_arch.ResnetBlock3D(cin, cout).half().to(DEV).eval()
+    gen = torch.Generator().manual_seed(hw)
+    x = torch.randn(4, cin, 5, hw, hw, generator=gen).half().to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    batched = bn.BatchedResidualBlock(block)
+    probe = torch.zeros(1, cin, 7, hw + 2, hw + 2, dtype=torch.float16, device=DEV)
+    assert bn.conv3d_f16_fits(probe, block.conv1.weight, (1, 1, 1))
+    with torch.inference_mode():
+        ref = torch.cat([block(x[i:i + 1]) for i in range(4)])
+        y = batched(x)
+        torch.cuda.synchronize()
+    rel = (y.float() - ref.float()).norm() / ref.float().norm()
+    assert rel < 5e-3, float(rel)
+
+
+def test_batched_suffix_all_stages_matches_model_suffix(pkg, bn):
+    """The runtime's suffix (BatchedSuffix over every suffix stage, norm_out and conv_out) on a staged batch of
+    4 clips == the model's own suffix modules clip by clip, at the tile-256 suffix shape [4, 256, 9, 64, 64]."""
+    staged = importlib.import_module(f"{pkg.__name__}.opt.encoder_staged_batch")
+    torch.manual_seed(7)
+    enc = h3_arch.H3Encoder().half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
+    quant = torch.nn.Conv3d(48, 48, 1).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn(4, 256, 9, 64, 64, generator=gen).half().to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    model = staged.EncoderSuffix(enc, quant, 2)
+    fused = bn.fused_suffix(enc, quant, all_stages=True)
+    with torch.inference_mode():
+        ref = torch.cat([model(x[i:i + 1]) for i in range(4)])
+        y = fused(x)
+        torch.cuda.synchronize()
+    assert y.shape == ref.shape == (4, 48, 9, 64, 64)
+    rel = (y.float() - ref.float()).norm() / ref.float().norm()
+    assert rel < 5e-3, float(rel)
