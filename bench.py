@@ -400,27 +400,35 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
         out["attention_h3_4x1797x32x64"] = attention_case(4, 1797, 32)
         out["attention_cfg4_1x16384x16x64"] = attention_case(1, 16384, 16)
 
-        # encoder suffix FP16 3x3x3 convs of a staged batch of 4 clips (the producer's padded channels-last
-        # output, two causal zero frames per clip): h3v_conv3d_f16 and the model's F.conv3d on the same
-        # operands; flops count the dense reduction (the kernel also skips the causal-zero taps)
-        def suffix_conv_case(b, c, d, hw):
-            xs = randn(b, c, d + 2, hw + 2, hw + 2).contiguous(memory_format=torch.channels_last_3d)
-            xs[:, :, :2] = 0
-            ws = randn(c, c, 3, 3, 3, scale=(27 * c) ** -0.5)
-            wsp = ws.permute(0, 2, 3, 4, 1).reshape(c, -1).contiguous()
-            bs = randn(c, scale=0.1)
-            ys = torch.empty((b, c, d, hw, hw), device=dev, dtype=f16).contiguous(memory_format=torch.channels_last_3d)
-            t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), p(ys), b, c, d + 2, hw + 2, hw + 2, c, 1,
-                                     stream))
-            t_t = timed(lambda: F.conv3d(xs, ws, bs))
+        # FP16 encoder convs outside the INT8 path (h3v_conv3d_f16) and the model's F.conv3d on the same padded
+        # channels-last operands (and on an NCDHW copy): suffix 3x3x3 convs of a staged batch of 4 clips after
+        # the producer (two causal zero frames per clip: the kernel skips those taps; flops count the dense
+        # reduction), the two prefix downsample convs and a nin_shortcut projection
+        def fp16_conv_case(b, cin, cout, dp, hp, wp, k, stride, causal):
+            xs = randn(b, cin, dp, hp, wp).contiguous(memory_format=torch.channels_last_3d)
+            if causal:
+                xs[:, :, :2] = 0
+            ws = randn(cout, cin, k, k, k, scale=(k ** 3 * cin) ** -0.5)
+            wsp = ws.permute(0, 2, 3, 4, 1).reshape(cout, -1).contiguous()
+            bs = randn(cout, scale=0.1)
+            do, ho, wo = (dp - k) // stride[0] + 1, (hp - k) // stride[1] + 1, (wp - k) // stride[2] + 1
+            ys = torch.empty((b, cout, do, ho, wo), device=dev, dtype=f16).contiguous(
+                memory_format=torch.channels_last_3d)
+            t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), p(ys), b, cin, dp, hp, wp, cout, k, k, k,
+                                     *stride, int(causal), stream))
+            t_t = timed(lambda: F.conv3d(xs, ws, bs, stride=stride))
             xn = xs.contiguous()
-            t_n = timed(lambda: F.conv3d(xn, ws, bs))
-            flops = 2 * b * d * hw * hw * c * 27 * c
+            t_n = timed(lambda: F.conv3d(xn, ws, bs, stride=stride))
+            flops = 2 * b * do * ho * wo * cout * k ** 3 * cin
             return {"h3v_conv3d_f16": fp16_mfma(t_c, flops), "torch_conv3d": fp16_mfma(t_t, flops),
                     "torch_conv3d_ncdhw": fp16_mfma(t_n, flops)}
 
-        out["suffix_conv_f16_4x256x9x64x64"] = suffix_conv_case(4, 256, 9, 64)
-        out["suffix_conv_f16_4x512x5x32x32"] = suffix_conv_case(4, 512, 5, 32)
+        out["suffix_conv_f16_4x256x9x64x64"] = fp16_conv_case(4, 256, 256, 11, 66, 66, 3, (1, 1, 1), True)
+        out["suffix_conv_f16_4x512x5x32x32"] = fp16_conv_case(4, 512, 512, 7, 34, 34, 3, (1, 1, 1), True)
+        out["suffix_conv_f16_4x1024x5x16x16"] = fp16_conv_case(4, 1024, 1024, 7, 18, 18, 3, (1, 1, 1), True)
+        out["downsample0_f16_128x17x256x256_s122"] = fp16_conv_case(1, 128, 128, 19, 258, 258, 3, (1, 2, 2), False)
+        out["downsample1_f16_256x17x128x128_s222"] = fp16_conv_case(1, 256, 256, 19, 129, 129, 3, (2, 2, 2), False)
+        out["nin_shortcut_f16_128to256x17x128x128"] = fp16_conv_case(1, 128, 256, 17, 128, 128, 1, (1, 1, 1), False)
     torch.cuda.synchronize()
     return out
 

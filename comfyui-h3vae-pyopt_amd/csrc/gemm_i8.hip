@@ -541,11 +541,15 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         for (int j = 0; j < B_PW; ++j) lds_dma16(rb, boff[j], (uint32_t)kb * BK, sb + (dw * B_PW + j) * 1024);
     };
 
-    v16i acc[FM][FN];
+    // F16Bias: fp16 operands with p.C and p.K given in bytes (2 per element), so every k
+    // offset above stays a byte offset; v_mfma_f32_32x32x16_f16 reads the same 16 bytes per
+    // lane as the int8 instruction and accumulates in fp32.
+    using Acc = std::conditional_t<EP == Epi::F16Bias, f32x16, v16i>;
+    Acc acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = v16i{};
+        for (int j = 0; j < FN; ++j) acc[i][j] = Acc{};
 
     // fragment addressing: lane reads row (lane & 31) of a 32-row block, 16-byte
     // k-chunk (lane >> 5) + 2*ks of the K step
@@ -570,8 +574,13 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-            for (int j = 0; j < FN; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < FN; ++j) {
+                if constexpr (EP == Epi::F16Bias)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, bf[j]),
+                                                                       __builtin_bit_cast(half8, af[i]), acc[i][j], 0, 0, 0);
+                else
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+            }
     };
 
     // Prologue: fill both rings (B before A per stage), then wait for stage 0.
@@ -1102,24 +1111,35 @@ int h3v_conv3d_i8(const int8_t* qx, const float* x_scale, const int8_t* qw, cons
 }
 
 int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int batch, int cin,
-                    int d, int h, int wd, int cout, int causal_skip, hipStream_t stream) {
+                   int d, int h, int wd, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                   hipStream_t stream) {
     const char* what = "h3v_conv3d_f16";
     H3V_REQUIRE(x && w && out, "%s: null pointer argument", what);
     GemmParams p{};
-    int rc = fill_conv(p, what, batch, cin, d, h, wd, cout, 3, 3, 3, 1, 1, 1);
+    int rc = fill_conv(p, what, batch, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw);
     if (rc) return rc;
     p.a = reinterpret_cast<const int8_t*>(x);
     p.b = reinterpret_cast<const int8_t*>(w);
     p.bias = bias;
     p.out = out;
-    p.causal_skip = causal_skip ? 1 : 0;
-    H3V_REQUIRE(halo_conv_fits(p, 2), "%s: requires Cin %% 32 == 0, Cout %% 128 == 0, an output width of 32, 64, 128 or "
-                "256, an output height that is a multiple of 512 / width and 16-byte aligned x and w (got Cin %d, Cout "
-                "%d, output %dx%d)", what, cin, cout, p.Ho, p.Wo);
-    if (p.Wo == 256) return launch_halo<256, Epi::F16Bias, 2>(p, stream, what);
-    if (p.Wo == 128) return launch_halo<128, Epi::F16Bias, 2>(p, stream, what);
-    if (p.Wo == 64) return launch_halo<64, Epi::F16Bias, 2>(p, stream, what);
-    return launch_halo<32, Epi::F16Bias, 2>(p, stream, what);
+    p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
+    H3V_REQUIRE(cin % 32 == 0 && aligned(x, 16) && aligned(w, 16),
+                "%s: requires Cin %% 32 == 0 and 16-byte aligned x and w (got Cin %d)", what, cin);
+    if (halo_conv_fits(p, 2)) {
+        if (p.Wo == 256) return launch_halo<256, Epi::F16Bias, 2>(p, stream, what);
+        if (p.Wo == 128) return launch_halo<128, Epi::F16Bias, 2>(p, stream, what);
+        if (p.Wo == 64) return launch_halo<64, Epi::F16Bias, 2>(p, stream, what);
+        return launch_halo<32, Epi::F16Bias, 2>(p, stream, what);
+    }
+    // implicit GEMM with channels and reduction counted in bytes
+    p.C = cin * 2;
+    p.K = p.K * 2;
+    if (p.C % 128 == 0) {
+        if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+    }
+    if (p.N <= 128) return launch_tiled<512, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
+    return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
 }
 
 int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,

@@ -49,10 +49,63 @@ __global__ __launch_bounds__(kThreads) void residual_downsample_pack_kernel(
     out[i] = y;
 }
 
+// Causal/reflect pack of an fp16 NDHWC tensor [B, D, H, W, C] into
+// [B, D + front, H + top + bottom, W + left + right, C]: `front` zero frames per
+// item, then the frames with the spatial border reflected (index -p -> p,
+// H - 1 + p -> H - 1 - p).  One thread per 8 channels of one output pixel.
+__global__ __launch_bounds__(kThreads) void causal_reflect_pack_kernel(
+    const u16x8* __restrict__ x, u16x8* __restrict__ out, uint32_t cv, uint32_t d, uint32_t h, uint32_t w,
+    uint32_t front, uint32_t top, uint32_t left, uint32_t dp, uint32_t hp, uint32_t wp, uint64_t nvec) {
+    const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= nvec) return;
+    const uint32_t c8 = (uint32_t)(i % cv);
+    uint64_t p = i / cv;
+    const uint32_t wo = (uint32_t)(p % wp);
+    p /= wp;
+    const uint32_t ho = (uint32_t)(p % hp);
+    p /= hp;
+    const uint32_t to = (uint32_t)(p % dp);
+    const uint32_t b = (uint32_t)(p / dp);
+    u16x8 y;
+    if (to < front) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = 0;
+    } else {
+        const int hs0 = (int)ho - (int)top, ws0 = (int)wo - (int)left;
+        const int hs = hs0 < 0 ? -hs0 : (hs0 >= (int)h ? 2 * ((int)h - 1) - hs0 : hs0);
+        const int ws = ws0 < 0 ? -ws0 : (ws0 >= (int)w ? 2 * ((int)w - 1) - ws0 : ws0);
+        const uint64_t src = ((((uint64_t)b * d + (to - front)) * h + (uint32_t)hs) * w + (uint32_t)ws) * cv + c8;
+        y = x[src];
+    }
+    out[i] = y;
+}
+
 }  // namespace
 }  // namespace h3v
 
 using namespace h3v;
+
+extern "C" int h3v_causal_reflect_pack(const uint16_t* x, uint16_t* out, int batch, int c, int d, int h, int w,
+                                       int front, int top, int bottom, int left, int right, hipStream_t stream) {
+    const char* what = "causal_reflect_pack";
+    H3V_REQUIRE(x && out, "%s: null pointer", what);
+    H3V_REQUIRE(batch > 0 && c > 0 && c % 8 == 0 && d > 0 && h > 0 && w > 0,
+                "%s: need positive sizes and channels a multiple of 8 (got B %d, C %d, %dx%dx%d)", what, batch, c, d,
+                h, w);
+    H3V_REQUIRE(front >= 0 && top >= 0 && bottom >= 0 && left >= 0 && right >= 0 && top < h && bottom < h &&
+                left < w && right < w, "%s: reflect padding must be smaller than the padded dimension", what);
+    H3V_REQUIRE(aligned(x, 16) && aligned(out, 16), "%s: buffers must be 16-byte aligned", what);
+    const uint32_t dp = (uint32_t)(d + front), hp = (uint32_t)(h + top + bottom), wp = (uint32_t)(w + left + right);
+    const uint64_t nvec = (uint64_t)batch * dp * hp * wp * (uint32_t)(c / 8);
+    H3V_REQUIRE(nvec < ((uint64_t)1 << 40), "%s: tensor too large", what);
+    const uint64_t blocks = (nvec + kThreads - 1) / kThreads;
+    H3V_REQUIRE(blocks <= 0x7fffffffu, "%s: tensor too large", what);
+    hipLaunchKernelGGL(causal_reflect_pack_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream,
+                       reinterpret_cast<const u16x8*>(x), reinterpret_cast<u16x8*>(out), (uint32_t)(c / 8),
+                       (uint32_t)d, (uint32_t)h, (uint32_t)w, (uint32_t)front, (uint32_t)top, (uint32_t)left, dp, hp,
+                       wp, nvec);
+    return launch_status(what);
+}
 
 extern "C" int h3v_residual_downsample_pack(const uint16_t* x, const uint16_t* residual, const uint16_t* bias,
                                             uint16_t* out, int c, int d, int h, int w, hipStream_t stream) {

@@ -1,0 +1,192 @@
+"""FP16 encoder convolutions on the matrix cores (``h3v_conv3d_f16``).
+
+The reference runs every FP16 convolution of the encoder outside the INT8
+path as ``F.conv3d`` (cuDNN): the 3x3x3 convs after the fp16 producers
+(opt/encoder_fused_batched_norm.py:83,94,96; opt/encoder_fused_norm_bias.py
+:135,139; opt/encoder_fused_temporal_norm.py:118), the stride-2 downsample
+after the residual pack (opt/encoder_fused_residual_pack.py:85), the stage-0
+downsample with its temporal padding folded into the call
+(opt/encoder_internal_padding.py:34), and the 1x1x1 ``nin_shortcut``
+projections.  Here they run as one HIP entry: fp16 operands, fp32
+accumulation on ``v_mfma_f32_32x32x16_f16``, ``fp16(acc + bias)`` once.
+Stride-1 3x3x3 convs whose output rows tile into 512-voxel blocks keep the
+input window of a tile in LDS; every other geometry is an implicit GEMM.
+
+Inputs are channels-last-3d and already padded; weights are packed once per
+weight tensor to [Cout, kd*kh*kw*Cin] (c fastest).  ``conv3d_f16_fits`` is the
+shape gate: convs outside it (Cin not a multiple of 32, such as conv_in with
+3 channels) keep the model's ``F.conv3d``, as in the reference.
+"""
+from __future__ import annotations
+
+from typing import List, Optional
+
+import torch
+import torch.nn.functional as F
+
+from .. import _hip
+
+
+def pack_conv_weight_f16(weight):
+    """fp16 [Cout, Cin, kd, kh, kw] -> [Cout, kd*kh*kw*Cin] with k = (kd, kh, kw, c), c fastest."""
+    if weight.ndim != 5 or weight.dtype != torch.float16:
+        raise ValueError("expected an fp16 [Cout, Cin, kd, kh, kw] weight")
+    return weight.permute(0, 2, 3, 4, 1).reshape(weight.shape[0], -1).contiguous()
+
+
+def conv3d_f16_fits(x, weight, stride):
+    """Whether h3v_conv3d_f16 takes the valid convolution of x [B, C, D, H, W] with weight at stride."""
+    if x.ndim != 5 or weight.ndim != 5 or x.dtype != torch.float16 or weight.dtype != torch.float16:
+        return False
+    b, c, d, h, w = x.shape
+    kd, kh, kw = weight.shape[2:]
+    sd, sh, sw = tuple(stride)
+    if weight.shape[1] != c or c % 32 or min(d - kd, h - kh, w - kw) < 0 or min(sd, sh, sw) < 1:
+        return False
+    m = b * ((d - kd) // sd + 1) * ((h - kh) // sh + 1) * ((w - kw) // sw + 1)
+    return x.numel() * 2 < 2 ** 32 and weight.numel() * 2 < 2 ** 31 and m < 2 ** 31
+
+
+def _check_conv(x, w_packed, bias, kernel_size, stride):
+    if x.ndim != 5 or x.dtype != torch.float16 or w_packed.dtype != torch.float16 or w_packed.ndim != 2:
+        raise ValueError("conv3d_f16 requires an fp16 [B, C, D, H, W] input and an fp16 [Cout, K] packed weight")
+    if len(kernel_size) != 3 or len(stride) != 3 or min(kernel_size) < 1 or min(stride) < 1:
+        raise ValueError("conv3d_f16 requires three positive kernel sizes and strides")
+    b, c, d, h, w = x.shape
+    kd, kh, kw = kernel_size
+    if w_packed.shape[1] != kd * kh * kw * c or not w_packed.is_contiguous():
+        raise ValueError("conv3d_f16 requires a packed [Cout, kd*kh*kw*C] weight")
+    if d < kd or h < kh or w < kw:
+        raise ValueError("conv3d_f16 requires an input at least as large as the kernel")
+    if bias is not None and (bias.shape != (w_packed.shape[0],) or bias.dtype != torch.float16
+                             or not bias.is_contiguous()):
+        raise ValueError("conv3d_f16 requires a contiguous fp16 [Cout] bias")
+    if b > 1 and not x.is_contiguous(memory_format=torch.channels_last_3d):
+        raise ValueError("conv3d_f16 requires a channels-last-3d input")
+
+
+def _out_shape(x, w_packed, kernel_size, stride):
+    b, _, d, h, w = x.shape
+    return (b, w_packed.shape[0], (d - kernel_size[0]) // stride[0] + 1, (h - kernel_size[1]) // stride[1] + 1,
+            (w - kernel_size[2]) // stride[2] + 1)
+
+
+@torch.library.custom_op("h3vae_encoder::conv3d_f16", mutates_args=(), device_types="cuda")
+def conv3d_f16(x: torch.Tensor, w_packed: torch.Tensor, bias: Optional[torch.Tensor], kernel_size: List[int],
+               stride: List[int], causal_skip: bool) -> torch.Tensor:
+    """Valid conv of a padded fp16 [B, C, D, H, W] (channels-last-3d) -> fp16 [B, Cout, Do, Ho, Wo] channels-last-3d.
+
+    causal_skip (3-deep kernels at depth stride 1) assumes two zero leading frames per item."""
+    _check_conv(x, w_packed, bias, kernel_size, stride)
+    _hip.require_gfx950(x.device, "conv3d_f16")
+    if not x.is_contiguous(memory_format=torch.channels_last_3d):
+        x = x.contiguous(memory_format=torch.channels_last_3d)
+    b, c, d, h, w = x.shape
+    out = torch.empty(_out_shape(x, w_packed, kernel_size, stride), device=x.device, dtype=x.dtype,
+                      memory_format=torch.channels_last_3d)
+    _hip.call("h3v_conv3d_f16", _hip.ptr(x), _hip.ptr(w_packed), _hip.ptr(bias), _hip.ptr(out), b, c, d, h, w,
+              w_packed.shape[0], *kernel_size, *stride, int(bool(causal_skip)), _hip.stream(x.device))
+    return out
+
+
+@conv3d_f16.register_fake
+def _fake_conv(x, w_packed, bias, kernel_size, stride, causal_skip):
+    _check_conv(x, w_packed, bias, kernel_size, stride)
+    return torch.empty(_out_shape(x, w_packed, kernel_size, stride), device=x.device, dtype=x.dtype,
+                       memory_format=torch.channels_last_3d)
+
+
+def _check_pack(x, front, pads):
+    if x.ndim != 5 or x.dtype != torch.float16 or x.shape[1] % 8 or x.numel() == 0:
+        raise ValueError("causal_reflect_pack requires a nonempty fp16 [B, C, D, H, W] input with C % 8 == 0")
+    top, bottom, left, right = pads
+    h, w = x.shape[3:]
+    if front < 0 or min(pads) < 0 or max(top, bottom) >= h or max(left, right) >= w:
+        raise ValueError("causal_reflect_pack: reflect padding must be smaller than the padded dimension")
+
+
+@torch.library.custom_op("h3vae_encoder::causal_reflect_pack", mutates_args=(), device_types="cuda")
+def causal_reflect_pack(x: torch.Tensor, front: int, top: int, bottom: int, left: int, right: int) -> torch.Tensor:
+    """fp16 [B, C, D, H, W] -> [B, C, D+front, H+top+bottom, W+left+right] channels-last-3d:
+    ``front`` zero frames per item, then x with its spatial border reflected."""
+    _check_pack(x, front, (top, bottom, left, right))
+    _hip.require_gfx950(x.device, "causal_reflect_pack")
+    x = x.contiguous(memory_format=torch.channels_last_3d)
+    b, c, d, h, w = x.shape
+    out = torch.empty((b, c, d + front, h + top + bottom, w + left + right), device=x.device, dtype=x.dtype,
+                      memory_format=torch.channels_last_3d)
+    _hip.call("h3v_causal_reflect_pack", _hip.ptr(x), _hip.ptr(out), b, c, d, h, w, front, top, bottom, left, right,
+              _hip.stream(x.device))
+    return out
+
+
+@causal_reflect_pack.register_fake
+def _fake_pack(x, front, top, bottom, left, right):
+    _check_pack(x, front, (top, bottom, left, right))
+    b, c, d, h, w = x.shape
+    return torch.empty((b, c, d + front, h + top + bottom, w + left + right), device=x.device, dtype=x.dtype,
+                       memory_format=torch.channels_last_3d)
+
+
+class _PackedWeights:
+    """Packed fp16 copies of conv weights, made once per weight tensor and version."""
+
+    def __init__(self):
+        self._cache = {}
+
+    def get(self, weight):
+        key = (weight.data_ptr(), tuple(weight.shape), weight.device)
+        hit = self._cache.get(key)
+        if hit is None or hit[0] != weight._version:
+            hit = self._cache[key] = (weight._version, pack_conv_weight_f16(weight.detach()))
+        return hit[1]
+
+
+_PACKED = _PackedWeights()
+
+
+def native_device(x):
+    """x lives on a gfx950 GPU, where these kernels run."""
+    return x.is_cuda and _hip.is_gfx950(x.device)
+
+
+def valid_conv3d(x, weight, bias, stride, causal_skip=False):
+    """Valid convolution of an already padded input: h3v_conv3d_f16 when the shape fits, else F.conv3d.
+
+    causal_skip: x holds two zero leading frames per item (the producers' causal padding)."""
+    stride = tuple(stride)
+    if native_device(x) and conv3d_f16_fits(x, weight, stride):
+        kernel = list(weight.shape[2:])
+        skip = bool(causal_skip) and kernel[0] == 3 and stride[0] == 1
+        return conv3d_f16(x, _PACKED.get(weight), bias, kernel, list(stride), skip)
+    return F.conv3d(x, weight, bias, stride=stride)
+
+
+def producer_conv3d(y, weight, bias, stride):
+    """The FP16 conv after a GroupNorm/SiLU/pad producer (two zero leading frames per item)."""
+    return valid_conv3d(y, weight, bias, stride, causal_skip=True)
+
+
+def pointwise_conv3d(x, conv):
+    """A 1x1x1 nn.Conv3d (``nin_shortcut``) on a channels-last-3d input."""
+    if (native_device(x) and tuple(conv.kernel_size) == (1, 1, 1) and tuple(conv.padding) == (0, 0, 0)
+            and tuple(conv.dilation) == (1, 1, 1) and conv.groups == 1
+            and x.is_contiguous(memory_format=torch.channels_last_3d)):
+        return valid_conv3d(x, conv.weight, conv.bias, conv.stride)
+    return conv(x)
+
+
+def padded_causal_conv3d(x, weight, bias, stride, front, top, bottom, left, right):
+    """Zero frames in front + reflect border + valid conv, the padding packed by one HIP kernel.
+
+    The output has exactly (D + front - kd) // sd + 1 frames."""
+    if native_device(x) and x.shape[1] % 8 == 0 and max(top, bottom) < x.shape[3] and max(left, right) < x.shape[4]:
+        xp = causal_reflect_pack(x, front, top, bottom, left, right)
+        if conv3d_f16_fits(xp, weight, stride):
+            return valid_conv3d(xp, weight, bias, stride, causal_skip=front == 2)
+        return F.conv3d(xp, weight, bias, stride=stride)
+    if top or bottom or left or right:
+        x = F.pad(x, (left, right, top, bottom, 0, 0), mode="reflect")
+    if front:
+        x = F.pad(x, (0, 0, 0, 0, front, 0))
+    return F.conv3d(x, weight, bias, stride=stride)

@@ -13,8 +13,9 @@ not applied in its epilogue; it is folded into the second producer as
 
 Without INT8 wrappers (the FP16 encoder mode) the same producers emit fp16
 through ``h3v_gn_norm_pack_f16`` (one fused statistics + pack launch
-sequence) and the convolutions run in FP16; nothing in this file ever falls
-back from the INT8 path to them.
+sequence) and the convolutions run in FP16 through ``h3v_conv3d_f16``
+(``producer_conv3d``; the ``nin_shortcut`` through ``pointwise_conv3d``);
+nothing in this file ever falls back from the INT8 path to them.
 """
 from __future__ import annotations
 
@@ -22,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _hip
+from .encoder_fp16_conv import pointwise_conv3d, producer_conv3d
 
 
 def _check_channel_vectors(x, *vectors):
@@ -113,7 +115,7 @@ class FusedNormPadConv(torch.nn.Module):
 
     def forward(self, x):
         y = temporal_norm_pack(x, self.norm_weight, self.norm_bias, self.eps)
-        return F.conv3d(y, self.weight, self.bias, stride=self.stride) if self.with_conv else y
+        return producer_conv3d(y, self.weight, self.bias, self.stride) if self.with_conv else y
 
 
 # The reference's opaque-op subclass has the same behaviour here (every producer is an opaque op).
@@ -142,14 +144,14 @@ class BiasFusedResidualBlock(torch.nn.Module):
                                                  self.second.eps, pre_bias=self.first.bias)
         first_input = self.first(x)
         h = (self.int8_first(first_input) if self.int8_first is not None
-             else F.conv3d(first_input, self.first.weight, None, stride=self.first.stride))
+             else producer_conv3d(first_input, self.first.weight, None, self.first.stride))
         second_input = bias_temporal_norm_pack(h, self.first.bias, self.second.norm_weight,
                                                self.second.norm_bias, self.second.eps)
         return (self.int8_second(second_input) if self.int8_second is not None
-                else F.conv3d(second_input, self.second.weight, second_bias, stride=self.second.stride))
+                else producer_conv3d(second_input, self.second.weight, second_bias, self.second.stride))
 
     def forward(self, x, zq=None):
         if zq is not None:
             raise ValueError("Unconditional inference only")
         h = self._residual_body(x, self.second.bias)
-        return (self.shortcut(x) if self.shortcut is not None else x) + h
+        return (pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x) + h

@@ -5,7 +5,7 @@ Mirror of opt/encoder_fused_residual_pack.py in fishelegs/ComfyUI-H3VAE-PyOpt.
 y = fp16(residual + (x + bias)) with fp32 adds and one rounding, written into
 the padded NDHWC input of the stride-(2,2,2) downsample convolution.
 ``ResidualDownsampleBlock`` (:63-85) runs the INT8 residual body, the pack
-and the FP16 downsample convolution.
+and the FP16 stride-(2,2,2) downsample convolution (``h3v_conv3d_f16``).
 """
 from __future__ import annotations
 
@@ -13,6 +13,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _hip
+from .encoder_fp16_conv import valid_conv3d
 from .encoder_fused_norm_bias import BiasFusedResidualBlock
 
 
@@ -71,4 +72,4 @@ class ResidualDownsampleBlock(BiasFusedResidualBlock):
         # second.bias is added by the pack, not by the second convolution
         h = self._residual_body(x, None)
         h = residual_downsample_pack(h, x, self.second.bias)
-        return F.conv3d(h, self.down_weight, self.down_bias, stride=(2, 2, 2))
+        return valid_conv3d(h, self.down_weight, self.down_bias, (2, 2, 2))

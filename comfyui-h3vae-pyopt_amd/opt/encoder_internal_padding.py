@@ -4,12 +4,16 @@ Mirror of opt/encoder_internal_padding.py in fishelegs/ComfyUI-H3VAE-PyOpt.
 The spatial reflect pad stays explicit; the left-only causal zero frames are
 requested from the convolution as symmetric temporal padding and the extra
 tail outputs are dropped.  Used for ``down.0.downsample.conv``, an FP16
-layer outside the INT8 path.
+layer outside the INT8 path.  On gfx950 the zero frames and the reflect
+border are written by one pack kernel (``h3v_causal_reflect_pack``) and the
+convolution runs as ``h3v_conv3d_f16`` over exactly the kept outputs.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn.functional as F
+
+from .encoder_fp16_conv import native_device, padded_causal_conv3d
 
 
 class ImplicitTemporalPadConv3d(torch.nn.Module):
@@ -31,6 +35,8 @@ class ImplicitTemporalPadConv3d(torch.nn.Module):
         left = 2 * self.padding[0] if depth > 1 else self.kernel_size[0] - 1
         output_depth = (depth + left - self.kernel_size[0]) // self.stride[0] + 1
         ph, pw = self.padding[1:]
+        if self.pad_mode == "reflect" and native_device(x):
+            return padded_causal_conv3d(x, self.weight, self.bias, self.stride, left, ph, ph, pw, pw)
         if ph or pw:
             x = F.pad(x, (pw, pw, ph, ph, 0, 0), mode=self.pad_mode)
         y = F.conv3d(x, self.weight, self.bias, stride=self.stride, padding=(left, 0, 0))

@@ -78,19 +78,24 @@ int h3v_gn_norm_pack_f16(const uint16_t* x, const uint16_t* pre_bias, const uint
                          float eps, int batch, int c, int d, int h, int w, uint16_t* y, float* stats, float* workspace,
                          hipStream_t stream);
 
-/* FP16 3x3x3 stride-1 valid convolution of a padded input (the model's FP16
- * encoder convs after the producer above: opt/encoder_fused_batched_norm.py
- * :70-72,83-86, F.conv3d on cuDNN in the reference).  x: fp16 NDHWC
- * [batch, d, h, wd, cin] (already padded: causal frames and reflect border);
- * w: fp16 [cout, 27 * cin] packed (kd, kh, kw, c) with c fastest; bias: fp16
- * [cout] (nullable); out: fp16 NDHWC [batch, d-2, h-2, wd-2, cout] =
- * fp16(sum fp32 + bias) with fp32 accumulation on v_mfma_f32_32x32x16_f16.
- * causal_skip: output frames 0 and 1 of each batch item skip the depth taps
- * that read the two leading zero frames.  Requires cin % 32 == 0, cout % 128
- * == 0, an output width of 32, 64, 128 or 256 and an output height that is a
- * multiple of 512 / width (one tile = whole rows of one frame). */
+/* FP16 valid convolution of a padded input (the model's FP16 encoder convs:
+ * after the producers above, opt/encoder_fused_batched_norm.py:83,94,96 and
+ * opt/encoder_fused_norm_bias.py:135,139, and the downsample convs,
+ * opt/encoder_fused_residual_pack.py:85 and opt/encoder_internal_padding.py:34;
+ * F.conv3d on cuDNN in the reference).  x: fp16 NDHWC
+ * [batch, d, h, wd, cin] (already padded); w: fp16 [cout, kd*kh*kw*cin] packed
+ * (kd, kh, kw, c) with c fastest; bias: fp16 [cout] (nullable); out: fp16
+ * NDHWC [batch, do, ho, wo, cout] with do = (d - kd) / sd + 1 (likewise ho,
+ * wo) = fp16(sum fp32 + bias), fp32 accumulation on v_mfma_f32_32x32x16_f16.
+ * causal_skip (kd == 3, sd == 1 only): output frames 0 and 1 of each batch
+ * item skip the depth taps that read the two leading zero frames.  Requires
+ * cin % 32 == 0 and 16-byte aligned x and w.  Stride-1 3x3x3 convs with
+ * cout % 128 == 0, an output width of 32, 64, 128 or 256 and an output height
+ * that is a multiple of 512 / width run with the input window in LDS; others
+ * as an implicit GEMM. */
 int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int batch, int cin,
-                   int d, int h, int wd, int cout, int causal_skip, hipStream_t stream);
+                   int d, int h, int wd, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                   hipStream_t stream);
 
 /* ---- decoder attention (head_dim 64) --------------------------------------
  * Replaces the model's `perform_attention` (flash attention) called from
@@ -237,6 +242,17 @@ int h3v_qk_rope(const uint16_t* qkv, const uint16_t* cosv, const uint16_t* sinv,
  * Replaces residual_downsample_pack / _residual_pack (opt/encoder_fused_residual_pack.py:12-55). */
 int h3v_residual_downsample_pack(const uint16_t* x, const uint16_t* residual, const uint16_t* bias, uint16_t* out,
                                  int c, int d, int h, int w, hipStream_t stream);
+
+/* Causal/reflect pack ahead of an FP16 convolution whose input the model pads
+ * itself: F.pad(reflect) + the causal zero frames of CausalConv3d, as used by
+ * opt/encoder_internal_padding.py:27-35 (`ImplicitTemporalPadConv3d`, where
+ * the zero frames are the conv's temporal padding) and the model's downsample
+ * convs.  x: fp16 NDHWC [batch, d, h, w, c]; out: fp16 NDHWC
+ * [batch, d + front, h + top + bottom, w + left + right, c]: `front` zero frames
+ * per item, then x with the spatial border reflected (-p -> p, h-1+p -> h-1-p).
+ * c % 8 == 0, each reflect pad smaller than its dimension, 16-byte aligned. */
+int h3v_causal_reflect_pack(const uint16_t* x, uint16_t* out, int batch, int c, int d, int h, int w, int front,
+                            int top, int bottom, int left, int right, hipStream_t stream);
 
 #ifdef __cplusplus
 }

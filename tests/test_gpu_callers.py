@@ -7,8 +7,9 @@
   residual+norm1+QKV for blocks 1.., and the final residual LayerNorm.
 
 The FP16 layers outside the INT8 path (nin_shortcut, downsample convs, and
-attention itself) are evaluated by the same PyTorch call on identical inputs
-on both sides.  The decoder chain test uses the elementwise attention
+attention itself) are evaluated by the same call (h3v_conv3d_f16 through
+opt/encoder_fp16_conv.py; their own parity is in test_gpu_conv_f16.py) on
+identical inputs on both sides.  The decoder chain test uses the elementwise attention
 stand-in of tests/h3_arch.py so every value stays checkable bit for bit.
 """
 from __future__ import annotations
@@ -32,7 +33,7 @@ DEV = torch.device("cuda:0")
 def mods(pkg):
     names = ["int8_qkv", "int8_attention_out", "int8_norm1_quant", "decoder_fused_qk_rope", "kitchen_int8",
              "encoder_fused_norm_bias", "encoder_fused_residual_pack", "encoder_fused_norm_next",
-             "encoder_int8_integration", "decoder_block0_norm", "decoder_final_norm"]
+             "encoder_int8_integration", "decoder_block0_norm", "decoder_final_norm", "encoder_fp16_conv"]
     return {n: importlib.import_module(f"{pkg.__name__}.opt.{n}") for n in names}
 
 
@@ -78,7 +79,7 @@ def _oracle_body(oracle, block, x_nd):
 
 
 @pytest.mark.parametrize("where", [(0, 0, 128, 16), (0, 1, 128, 16), (1, 0, 128, 8)])
-def test_bias_fused_block_matches_oracle(int8_prefix, oracle, where):
+def test_bias_fused_block_matches_oracle(int8_prefix, mods, oracle, where):
     stage, index, cin, hw = where
     print(f"BiasFusedResidualBlock stage={stage} block={index}", flush=True)
     _, prefix = int8_prefix
@@ -87,7 +88,8 @@ def test_bias_fused_block_matches_oracle(int8_prefix, oracle, where):
     x = _cl(torch.randn(1, cin, 5, hw, hw, generator=gen).half().to(DEV))
     with torch.inference_mode():
         y = block(x)
-        shortcut = block.shortcut(x) if block.shortcut is not None else x
+        shortcut = (mods["encoder_fp16_conv"].pointwise_conv3d(x, block.shortcut) if block.shortcut is not None
+                    else x)
         torch.cuda.synchronize()
     h2 = _oracle_body(oracle, block, ndhwc(x)[0])
     want = (ndhwc(shortcut)[0].astype(np.float32) + h2.astype(np.float32)).astype(np.float16)
@@ -104,8 +106,8 @@ def test_residual_downsample_block_matches_oracle(int8_prefix, mods, oracle):
         y = block(x)
         body = block._residual_body(x, None)
         pk = mods["encoder_fused_residual_pack"].residual_downsample_pack(body, x, block.second.bias)
-        # the FP16 downsample conv on the very same tensor (MIOpen's algorithm choice depends on strides)
-        conv = F.conv3d(pk, block.down_weight, block.down_bias, stride=(2, 2, 2))
+        # the FP16 downsample conv on the very same tensor
+        conv = mods["encoder_fp16_conv"].valid_conv3d(pk, block.down_weight, block.down_bias, (2, 2, 2))
         torch.cuda.synchronize()
     h2 = _oracle_body(oracle, block, ndhwc(x)[0])
     assert_bitwise(ndhwc(body)[0], h2, "residual body")

@@ -24,6 +24,11 @@ def bn(pkg):
     return importlib.import_module(f"{pkg.__name__}.opt.encoder_fused_batched_norm")
 
 
+@pytest.fixture(scope="module")
+def fc(pkg):
+    return importlib.import_module(f"{pkg.__name__}.opt.encoder_fp16_conv")
+
+
 def _operands(b, c, d, h, w, cout, with_bias, seed, causal_zero=True):
     gen = torch.Generator().manual_seed(seed)
     x = torch.randn(b, c, d, h, w, generator=gen).half()
@@ -51,12 +56,12 @@ def _assert_close(y, ref, mag):
                                  f"{float((err - bound).max()):.3e}")
 
 
-def _run(bn, x, wt, bias, causal_skip):
+def _run(fc, x, wt, bias, causal_skip, stride=(1, 1, 1)):
     xd = x.to(DEV).contiguous(memory_format=torch.channels_last_3d)
-    wp = bn.pack_conv_weight_f16(wt.to(DEV))
+    wp = fc.pack_conv_weight_f16(wt.to(DEV))
     bd = None if bias is None else bias.to(DEV)
     with torch.inference_mode():
-        y = bn.conv3d_f16(xd, wp, bd, causal_skip)
+        y = fc.conv3d_f16(xd, wp, bd, list(wt.shape[2:]), list(stride), causal_skip)
     torch.cuda.synchronize()
     return y
 
@@ -73,50 +78,117 @@ CASES = [
 
 
 @pytest.mark.parametrize("b,c,d,h,w,cout,with_bias", CASES)
-def test_conv3d_f16_matches_float64(bn, b, c, d, h, w, cout, with_bias):
+def test_conv3d_f16_matches_float64(fc, b, c, d, h, w, cout, with_bias):
     print(f"conv3d_f16 B={b} C={c} D={d} {h}x{w} Cout={cout} bias={with_bias}", flush=True)
     x, wt, bias = _operands(b, c, d, h, w, cout, with_bias, seed=b * 1000 + c + d + h + w + cout)
-    y = _run(bn, x, wt, bias, causal_skip=True)
+    y = _run(fc, x, wt, bias, causal_skip=True)
     assert y.shape == (b, cout, d - 2, h - 2, w - 2) and y.dtype == torch.float16
     assert y.is_contiguous(memory_format=torch.channels_last_3d)
     ref, mag = _reference(x, wt, bias)
     _assert_close(y, ref, mag)
     # the causal skip drops only taps on zero frames: the full reduction gives the same values
-    y_full = _run(bn, x, wt, bias, causal_skip=False)
+    y_full = _run(fc, x, wt, bias, causal_skip=False)
     assert torch.equal(y_full, y)
 
 
-def test_conv3d_f16_nonzero_leading_frames_without_skip(bn):
+def test_conv3d_f16_nonzero_leading_frames_without_skip(fc):
     """causal_skip=False reads every depth tap: leading frames that are not zero take part."""
     x, wt, bias = _operands(2, 64, 5, 10, 66, 128, True, seed=5, causal_zero=False)
-    y = _run(bn, x, wt, bias, causal_skip=False)
+    y = _run(fc, x, wt, bias, causal_skip=False)
     ref, mag = _reference(x, wt, bias)
     _assert_close(y, ref, mag)
 
 
-def test_conv3d_f16_matches_torch_fp16(bn):
+def test_conv3d_f16_matches_torch_fp16(fc):
     """Same operands through the model's FP16 F.conv3d on the GPU (its own accumulation order)."""
     x, wt, bias = _operands(3, 256, 6, 18, 66, 256, True, seed=17)
-    y = _run(bn, x, wt, bias, causal_skip=True).float()
+    y = _run(fc, x, wt, bias, causal_skip=True).float()
     ref = F.conv3d(x.to(DEV), wt.to(DEV), bias.to(DEV)).float()
     rel = (y - ref).norm() / ref.norm()
     assert rel < 1e-3, float(rel)
 
 
-def test_conv3d_f16_rejects_unfit_shapes(bn):
-    x, wt, bias = _operands(1, 64, 3, 6, 66, 128, True, seed=1)
-    xd = x.to(DEV).contiguous(memory_format=torch.channels_last_3d)
-    with pytest.raises(ValueError, match="Cout % 128"):
-        bn.conv3d_f16(xd, bn.pack_conv_weight_f16(wt[:64].to(DEV)), bias[:64].to(DEV), True)
-    x2 = torch.zeros(1, 64, 3, 6, 50, dtype=torch.float16, device=DEV).contiguous(memory_format=torch.channels_last_3d)
-    with pytest.raises(ValueError, match="output width"):
-        bn.conv3d_f16(x2, bn.pack_conv_weight_f16(wt.to(DEV)), None, True)
+def test_conv3d_f16_rejects_unfit_shapes(fc):
+    x = torch.zeros(1, 16, 3, 6, 66, dtype=torch.float16, device=DEV).contiguous(memory_format=torch.channels_last_3d)
+    w = torch.zeros(128, 27 * 16, dtype=torch.float16, device=DEV)
+    with pytest.raises(ValueError, match="Cin % 32"):
+        fc.conv3d_f16(x, w, None, [3, 3, 3], [1, 1, 1], True)
+    x2 = torch.zeros(1, 64, 3, 6, 66, dtype=torch.float16, device=DEV).contiguous(memory_format=torch.channels_last_3d)
     with pytest.raises(ValueError, match="packed"):
-        bn.conv3d_f16(xd, wt.to(DEV).reshape(128, -1)[:, :100].contiguous(), None, True)
+        fc.conv3d_f16(x2, w[:, :100].contiguous(), None, [3, 3, 3], [1, 1, 1], True)
+
+
+# implicit-GEMM path: (batch, Cin, D, H, W, Cout, kernel, stride) -- strides, 1x1x1, Cout not a multiple of
+# 128, widths the window kernel does not take, Cin 32 (64-byte reduction steps) and Cout > 128 (256 x 256 tiles)
+GEMM_CASES = [
+    (1, 128, 19, 34, 34, 128, (3, 3, 3), (1, 2, 2)),       # stage-0 downsample geometry, reduced
+    (1, 256, 19, 17, 17, 256, (3, 3, 3), (2, 2, 2)),       # stage-1 downsample after the residual pack
+    (2, 64, 5, 10, 50, 64, (3, 3, 3), (1, 1, 1)),          # Wo 48, Cout 64
+    (1, 32, 4, 9, 21, 96, (3, 3, 3), (1, 1, 1)),
+    (3, 256, 4, 8, 8, 512, (1, 1, 1), (1, 1, 1)),          # nin_shortcut
+    (1, 128, 3, 20, 20, 200, (3, 3, 3), (1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("b,c,d,h,w,cout,kernel,stride", GEMM_CASES)
+def test_conv3d_f16_implicit_gemm_matches_float64(fc, b, c, d, h, w, cout, kernel, stride):
+    print(f"conv3d_f16 implicit GEMM B={b} C={c} D={d} {h}x{w} Cout={cout} k={kernel} s={stride}", flush=True)
+    gen = torch.Generator().manual_seed(c + d + h + w + cout + sum(stride))
+    x = torch.randn(b, c, d, h, w, generator=gen).half()
+    wt = (torch.randn(cout, c, *kernel, generator=gen) * (c * kernel[0] * kernel[1] * kernel[2]) ** -0.5).half()
+    bias = (0.5 * torch.randn(cout, generator=gen)).half()
+    y = _run(fc, x, wt, bias, causal_skip=False, stride=stride)
+    ref = F.conv3d(x.double(), wt.double(), bias.double(), stride=stride)
+    mag = F.conv3d(x.double().abs(), wt.double().abs(), stride=stride)
+    assert y.shape == ref.shape
+    _assert_close(y, ref, mag)
+
+
+def test_conv3d_f16_implicit_gemm_causal_skip(fc):
+    """Stride-1 convs outside the window kernel skip the zero depth taps per tile with the same values."""
+    x, wt, bias = _operands(2, 64, 6, 10, 50, 64, True, seed=9)
+    y = _run(fc, x, wt, bias, causal_skip=True)
+    assert torch.equal(y, _run(fc, x, wt, bias, causal_skip=False))
+    ref, mag = _reference(x, wt, bias)
+    _assert_close(y, ref, mag)
+
+
+@pytest.mark.parametrize("shape,pads", [((1, 128, 5, 16, 16), (2, 1, 1, 1, 1)), ((4, 256, 3, 7, 9), (2, 0, 1, 0, 1)),
+                                        ((2, 64, 1, 3, 4), (0, 2, 2, 3, 3))])
+def test_causal_reflect_pack_matches_torch_pad(fc, shape, pads):
+    front, top, bottom, left, right = pads
+    gen = torch.Generator().manual_seed(sum(shape))
+    x = torch.randn(*shape, generator=gen).half()
+    with torch.inference_mode():
+        y = fc.causal_reflect_pack(x.to(DEV).contiguous(memory_format=torch.channels_last_3d), *pads)
+        torch.cuda.synchronize()
+    want = F.pad(F.pad(x.float(), (left, right, top, bottom, 0, 0), mode="reflect"), (0, 0, 0, 0, front, 0)).half()
+    assert y.is_contiguous(memory_format=torch.channels_last_3d)
+    assert torch.equal(y.cpu(), want)
+
+
+def test_stage0_downsample_matches_model(pkg, fc):
+    """down.0.downsample.conv through ImplicitTemporalPadConv3d (pack + conv3d_f16) == the model's CausalConv3d
+    within the fp16 bound, against a float64 run of the model's own padding."""
+    ip = importlib.import_module(f"{pkg.__name__}.opt.encoder_internal_padding")
+    torch.manual_seed(3)
+    down = h3_arch.Downsample(128, (1, 2, 2), (1, 1, 1)).half().to(DEV).eval()
+    conv = ip.ImplicitTemporalPadConv3d(down.conv)
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(1, 128, 5, 32, 32, generator=gen).half()
+    with torch.inference_mode():
+        y = conv(x.to(DEV).contiguous(memory_format=torch.channels_last_3d))
+        torch.cuda.synchronize()
+    xp = F.pad(F.pad(x.double(), (1, 1, 1, 1, 0, 0), mode="reflect"), (0, 0, 0, 0, 2, 0))
+    w64, b64 = down.conv.weight.detach().cpu().double(), down.conv.bias.detach().cpu().double()
+    ref = F.conv3d(xp, w64, b64, stride=(1, 2, 2))
+    mag = F.conv3d(xp.abs(), w64.abs(), stride=(1, 2, 2))
+    assert y.shape == ref.shape == (1, 128, 5, 16, 16)
+    _assert_close(y, ref, mag)
 
 
 @pytest.mark.parametrize("cin,cout,hw", [(256, 256, 32), (256, 512, 64)])
-def test_batched_residual_block_with_native_convs(bn, cin, cout, hw):
+def test_batched_residual_block_with_native_convs(bn, fc, cin, cout, hw):
     """Clips batched through BatchedResidualBlock, whose convs now fit h3v_conv3d_f16, == the model's
     ResnetBlock3D clip by clip (FP16 tolerance: different reduction orders for statistics and convs)."""
     torch.manual_seed(cin + cout + hw)
@@ -125,7 +197,7 @@ def test_batched_residual_block_with_native_convs(bn, cin, cout, hw):
     x = torch.randn(4, cin, 5, hw, hw, generator=gen).half().to(DEV).contiguous(memory_format=torch.channels_last_3d)
     batched = bn.BatchedResidualBlock(block)
     probe = torch.zeros(1, cin, 7, hw + 2, hw + 2, dtype=torch.float16, device=DEV)
-    assert bn.conv3d_f16_fits(probe, block.conv1.weight, (1, 1, 1))
+    assert fc.conv3d_f16_fits(probe, block.conv1.weight, (1, 1, 1))
     with torch.inference_mode():
         ref = torch.cat([block(x[i:i + 1]) for i in range(4)])
         y = batched(x)

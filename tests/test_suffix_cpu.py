@@ -1,5 +1,5 @@
-"""CPU checks of the encoder suffix's FP16 conv routing: the packed weight layout the kernel reads, the
-shape gate that picks h3v_conv3d_f16 over the model's F.conv3d, and the op's host-side guards."""
+"""CPU checks of the FP16 encoder conv routing: the packed weight layout the kernel reads, the shape
+gate that picks h3v_conv3d_f16 over the model's F.conv3d, and the ops' host-side guards (meta tensors)."""
 from __future__ import annotations
 
 import importlib
@@ -9,49 +9,79 @@ import torch
 
 
 @pytest.fixture(scope="module")
-def bn(pkg):
-    return importlib.import_module(f"{pkg.__name__}.opt.encoder_fused_batched_norm")
+def fc(pkg):
+    return importlib.import_module(f"{pkg.__name__}.opt.encoder_fp16_conv")
 
 
-def test_packed_weight_layout(bn):
+def test_packed_weight_layout(fc):
     gen = torch.Generator().manual_seed(2)
     w = torch.randn(5, 7, 3, 3, 3, generator=gen).half()
-    p = bn.pack_conv_weight_f16(w)
+    p = fc.pack_conv_weight_f16(w)
     assert p.shape == (5, 27 * 7) and p.is_contiguous()
     for o, c, kd, kh, kw in [(0, 0, 0, 0, 0), (4, 6, 2, 2, 2), (2, 3, 1, 0, 2), (3, 5, 0, 2, 1)]:
         assert p[o, ((kd * 3 + kh) * 3 + kw) * 7 + c] == w[o, c, kd, kh, kw]
+    w1 = torch.randn(4, 6, 1, 1, 1, generator=gen).half()
+    assert torch.equal(fc.pack_conv_weight_f16(w1), w1.reshape(4, 6))
     with pytest.raises(ValueError):
-        bn.pack_conv_weight_f16(w.float())
+        fc.pack_conv_weight_f16(w.float())
     with pytest.raises(ValueError):
-        bn.pack_conv_weight_f16(w[:, :, :1])
+        fc.pack_conv_weight_f16(w[0])
 
 
-@pytest.mark.parametrize("shape,cout,stride,fits", [
-    ((4, 256, 19, 66, 66), 256, (1, 1, 1), True),      # suffix stage at tile 256: 64 x 64
-    ((4, 512, 11, 34, 34), 512, (1, 1, 1), True),      # 32 x 32
-    ((4, 1024, 7, 18, 18), 1024, (1, 1, 1), False),    # 16 x 16: model conv
-    ((4, 256, 19, 66, 66), 48, (1, 1, 1), False),      # conv_out to the latent moments
-    ((4, 256, 19, 66, 66), 256, (1, 2, 2), False),
-    ((1, 16, 5, 66, 66), 128, (1, 1, 1), False),       # Cin % 32
-    ((1, 32, 5, 14, 66), 128, (1, 1, 1), False),       # Ho = 12 not a multiple of 8 at Wo 64
+@pytest.mark.parametrize("shape,cout,kernel,stride,fits", [
+    ((4, 256, 19, 66, 66), 256, 3, (1, 1, 1), True),      # suffix stage at tile 256: 64 x 64
+    ((4, 1024, 7, 18, 18), 1024, 3, (1, 1, 1), True),     # 16 x 16 stage (implicit GEMM)
+    ((4, 256, 19, 66, 66), 48, 3, (1, 1, 1), True),       # conv_out to the latent moments
+    ((1, 128, 19, 258, 258), 128, 3, (1, 2, 2), True),    # stage-0 downsample
+    ((1, 256, 19, 129, 129), 256, 3, (2, 2, 2), True),    # stage-1 downsample
+    ((1, 128, 17, 128, 128), 256, 1, (1, 1, 1), True),    # nin_shortcut
+    ((1, 3, 19, 258, 258), 128, 3, (1, 1, 1), False),     # conv_in: 3 channels
+    ((1, 16, 5, 66, 66), 128, 3, (1, 1, 1), False),       # Cin % 32
+    ((1, 32, 2, 66, 66), 128, 3, (1, 1, 1), False),       # shallower than the kernel
 ])
-def test_fits_gate(bn, shape, cout, stride, fits):
+def test_fits_gate(fc, shape, cout, kernel, stride, fits):
     x = torch.empty(shape, dtype=torch.float16, device="meta")
-    w = torch.empty((cout, shape[1], 3, 3, 3), dtype=torch.float16, device="meta")
-    assert bn.conv3d_f16_fits(x, w, stride) is fits
+    w = torch.empty((cout, shape[1], kernel, kernel, kernel), dtype=torch.float16, device="meta")
+    assert fc.conv3d_f16_fits(x, w, stride) is fits
+    assert fc.conv3d_f16_fits(x.float(), w, stride) is False
 
 
-def test_conv_op_guards_on_meta(bn):
+def test_conv_op_guards_on_meta(fc):
     x = torch.empty((2, 64, 5, 6, 66), dtype=torch.float16, device="meta").contiguous(
         memory_format=torch.channels_last_3d)
     w = torch.empty((128, 27 * 64), dtype=torch.float16, device="meta")
-    y = bn.conv3d_f16(x, w, None, True)
+    y = fc.conv3d_f16(x, w, None, [3, 3, 3], [1, 1, 1], True)
     assert y.shape == (2, 128, 3, 4, 64) and y.is_contiguous(memory_format=torch.channels_last_3d)
+    assert fc.conv3d_f16(x, w, None, [3, 3, 3], [1, 2, 2], False).shape == (2, 128, 3, 2, 32)
     with pytest.raises(ValueError, match="packed"):
-        bn.conv3d_f16(x, w[:, :100], None, True)
+        fc.conv3d_f16(x, w[:, :100], None, [3, 3, 3], [1, 1, 1], True)
     with pytest.raises(ValueError, match="channels-last"):
-        bn.conv3d_f16(x.contiguous(), w, None, True)
+        fc.conv3d_f16(x.contiguous(), w, None, [3, 3, 3], [1, 1, 1], True)
     with pytest.raises(ValueError, match="bias"):
-        bn.conv3d_f16(x, w, torch.empty(64, dtype=torch.float16, device="meta"), True)
+        fc.conv3d_f16(x, w, torch.empty(64, dtype=torch.float16, device="meta"), [3, 3, 3], [1, 1, 1], True)
     with pytest.raises(ValueError, match="fp16"):
-        bn.conv3d_f16(x.float(), w, None, True)
+        fc.conv3d_f16(x.float(), w, None, [3, 3, 3], [1, 1, 1], True)
+    with pytest.raises(ValueError, match="strides"):
+        fc.conv3d_f16(x, w, None, [3, 3, 3], [1, 0, 1], True)
+
+
+def test_pack_op_guards_on_meta(fc):
+    x = torch.empty((1, 128, 5, 16, 16), dtype=torch.float16, device="meta")
+    y = fc.causal_reflect_pack(x, 2, 1, 1, 1, 1)
+    assert y.shape == (1, 128, 7, 18, 18) and y.is_contiguous(memory_format=torch.channels_last_3d)
+    with pytest.raises(ValueError, match="smaller"):
+        fc.causal_reflect_pack(x, 2, 16, 0, 0, 0)
+    with pytest.raises(ValueError, match="C % 8"):
+        fc.causal_reflect_pack(x[:, :12], 2, 1, 1, 1, 1)
+
+
+def test_cpu_tensors_keep_the_model_convs(fc):
+    """Off the GPU the routing helpers are the model's own F.conv3d / F.pad calls."""
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(1, 32, 5, 6, 6, generator=gen)
+    w = torch.randn(64, 32, 3, 3, 3, generator=gen)
+    b = torch.randn(64, generator=gen)
+    F = torch.nn.functional
+    assert torch.equal(fc.valid_conv3d(x, w, b, (1, 2, 2)), F.conv3d(x, w, b, stride=(1, 2, 2)))
+    want = F.conv3d(F.pad(F.pad(x, (1, 1, 1, 1, 0, 0), mode="reflect"), (0, 0, 0, 0, 2, 0)), w, b, stride=(1, 2, 2))
+    assert torch.equal(fc.padded_causal_conv3d(x, w, b, (1, 2, 2), 2, 1, 1, 1, 1), want)
