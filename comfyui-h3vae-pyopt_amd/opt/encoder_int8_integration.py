@@ -131,12 +131,15 @@ class Int8FusedValidConv3d(nn.Module):
         self.fuse_norm = False
 
     def _apply(self, fn, recurse=True):
-        # module.to(device, dtype) must keep INT8 weights, FP32 scales and the FP16 bias.
+        # module.to(device, dtype) must keep INT8 weights, FP32 scales and the FP16 bias bit for bit.
+        # The reference (opt/encoder_int8_integration.py:268-282) keeps a copy of the scale only; its
+        # bias goes through the requested dtype and back, which rounds it on a bf16 move.
         original_scale = self.weight_scale.detach().clone()
+        original_bias = self.bias.detach().clone()
         result = super()._apply(fn, recurse=recurse)
         self.qweight.data = self.qweight.data.to(device=self.qweight.device, dtype=torch.int8)
         self.weight_scale.data = original_scale.to(device=self.weight_scale.device, dtype=torch.float32)
-        self.bias.data = self.bias.data.to(device=self.bias.device, dtype=torch.float16)
+        self.bias.data = original_bias.to(device=self.bias.device, dtype=torch.float16)
         return result
 
     def forward_norm(self, x, norm_weight, norm_bias, eps, pre_bias=None):
