@@ -26,8 +26,10 @@ from .encoder_staged_batch import EncoderSuffix
 
 def _validate(x, pre_bias, weight, bias):
     b, c, d, h, w = x.shape
-    if b not in (1, 3, 4) or c not in (256, 512, 1024) or min(h, w) < 2 or x.dtype != torch.float16:
-        raise ValueError("Supported: FP16 B=1/3/4 C=256/512/1024 H/W>=2")
+    # B = 2 is accepted here: the reference's check (B in 1/3/4) rejects the batch of two clips that
+    # encode_staged forms for 2 mod 4 clips at staged batch 4 (and for every batch at staged batch 2).
+    if b not in (1, 2, 3, 4) or c not in (256, 512, 1024) or min(h, w) < 2 or x.dtype != torch.float16:
+        raise ValueError("Supported: FP16 B=1..4 C=256/512/1024 H/W>=2")
     if b > 1 and x.stride(0) != d * x.stride(2):
         raise ValueError("Batch and time must be contiguous adjacent frame spans")
     if (b * c * (d + 2) * (h + 2) * (w + 2) >= 2 ** 31

@@ -46,8 +46,10 @@ def test_batched_norm_pack_guards_on_meta(pkg):
     v = torch.empty(c, dtype=torch.float16, device="meta")
     y = op(x, None, v, v, 1e-6)
     assert y.shape == (4, c, 5, 10, 10) and y.is_contiguous(memory_format=torch.channels_last_3d)
-    with pytest.raises(ValueError, match="B=1/3/4"):
-        op(x[:2], None, v, v, 1e-6)
+    assert op(x[:2], None, v, v, 1e-6).shape == (2, c, 5, 10, 10)     # two clips: accepted (the reference raises)
+    x5 = torch.empty(5, c, 3, 8, 8, dtype=torch.float16, device="meta").contiguous(memory_format=torch.channels_last_3d)
+    with pytest.raises(ValueError, match="B=1..4"):
+        op(x5, None, v, v, 1e-6)
     with pytest.raises(ValueError, match="adjacent"):
         op(x.contiguous(), None, v, v, 1e-6)
     with pytest.raises(ValueError, match="channel vectors"):

@@ -75,8 +75,13 @@ def test_batched_op_layouts_and_guards(bn, oracle):
     want, _ = _oracle(oracle, x, gamma, beta, None, b, 1e-6)
     assert_bitwise(np_(y.permute(0, 2, 3, 4, 1)), want, "batched op")
     g, be = gamma.to(DEV), beta.to(DEV)
-    with pytest.raises(ValueError, match="B=1/3/4"):
-        bn.batched_temporal_norm_pack(xd[:2], None, g, be, 1e-6)
+    with pytest.raises(ValueError, match="B=1..4"):
+        bn.batched_temporal_norm_pack(torch.cat([xd, xd[:1]]), None, g, be, 1e-6)
+    # two clips (the reference rejects B = 2, which its own staged encode produces)
+    with torch.inference_mode():
+        y2 = bn.batched_temporal_norm_pack(xd[:2], None, g, be, 1e-6)
+    torch.cuda.synchronize()
+    assert_bitwise(np_(y2.permute(0, 2, 3, 4, 1)), want[:2], "batched op, two clips")
     with pytest.raises(ValueError, match="adjacent"):
         bn.batched_temporal_norm_pack(xd.contiguous(), None, g, be, 1e-6)     # NCDHW: time not adjacent to batch
     with pytest.raises(ValueError, match="channel vectors"):
