@@ -80,10 +80,77 @@ __global__ __launch_bounds__(kThreads) void causal_reflect_pack_kernel(
     out[i] = y;
 }
 
+// Tap-folded pack for a 3x3x3 convolution with few input channels (the encoder's conv_in, C = 3):
+// out[b, t', h, w, (kh * 3 + kw) * C + c] = x[b, t' - front, reflect(h + kh - 1), reflect(w + kw - 1), c]
+// for t' >= front, 0 for t' < front and for the channels 9C .. CF-1.  The 3x3x3 conv over x becomes a
+// 3x1x1 conv over out (K = 3 * CF), which the matrix-core conv runs without padding C to 32 per tap.
+// One thread per output pixel: CF / 8 16-byte stores.
+template <int C, int CF>
+__global__ __launch_bounds__(kThreads) void tap_fold_pack_kernel(const uint16_t* __restrict__ x,
+                                                                 u16x8* __restrict__ out, uint32_t d, uint32_t h,
+                                                                 uint32_t w, uint32_t front, uint32_t dp,
+                                                                 uint64_t npix) {
+    static_assert(9 * C <= CF && CF % 8 == 0, "folded channels");
+    const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (i >= npix) return;
+    const uint32_t wo = (uint32_t)(i % w);
+    uint64_t p = i / w;
+    const uint32_t ho = (uint32_t)(p % h);
+    p /= h;
+    const uint32_t to = (uint32_t)(p % dp);
+    const uint32_t b = (uint32_t)(p / dp);
+    uint16_t v[CF];
+#pragma unroll
+    for (int e = 0; e < CF; ++e) v[e] = 0;
+    if (to >= front) {
+        const uint64_t frame = ((uint64_t)b * d + (to - front)) * h;
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+            const int hs0 = (int)ho + kh - 1;
+            const int hs = hs0 < 0 ? -hs0 : (hs0 >= (int)h ? 2 * ((int)h - 1) - hs0 : hs0);
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+                const int ws0 = (int)wo + kw - 1;
+                const int ws = ws0 < 0 ? -ws0 : (ws0 >= (int)w ? 2 * ((int)w - 1) - ws0 : ws0);
+                const uint16_t* src = x + ((frame + (uint32_t)hs) * w + (uint32_t)ws) * C;
+#pragma unroll
+                for (int ch = 0; ch < C; ++ch) v[(kh * 3 + kw) * C + ch] = src[ch];
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < CF / 8; ++q) {
+        u16x8 y;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = v[q * 8 + e];
+        out[i * (CF / 8) + q] = y;
+    }
+}
+
 }  // namespace
 }  // namespace h3v
 
 using namespace h3v;
+
+extern "C" int h3v_tap_fold_pack(const uint16_t* x, uint16_t* out, int batch, int c, int d, int h, int w, int front,
+                                 int cf, hipStream_t stream) {
+    const char* what = "tap_fold_pack";
+    H3V_REQUIRE(x && out, "%s: null pointer", what);
+    H3V_REQUIRE(cf == 32 && c >= 1 && c <= 3, "%s: needs C in 1..3 and 32 folded channels (got C %d, %d)", what, c,
+                cf);
+    H3V_REQUIRE(batch > 0 && d > 0 && h >= 2 && w >= 2 && front >= 0,
+                "%s: need positive sizes and H, W >= 2 (got B %d, %dx%dx%d)", what, batch, d, h, w);
+    H3V_REQUIRE(aligned(out, 16), "%s: output must be 16-byte aligned", what);
+    const uint32_t dp = (uint32_t)(d + front);
+    const uint64_t npix = (uint64_t)batch * dp * h * w;
+    H3V_REQUIRE(npix < ((uint64_t)1 << 36), "%s: tensor too large", what);
+    const uint64_t blocks = (npix + kThreads - 1) / kThreads;
+    H3V_REQUIRE(blocks <= 0x7fffffffu, "%s: tensor too large", what);
+    auto kernel = c == 1 ? tap_fold_pack_kernel<1, 32> : (c == 2 ? tap_fold_pack_kernel<2, 32> : tap_fold_pack_kernel<3, 32>);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, x, reinterpret_cast<u16x8*>(out),
+                       (uint32_t)d, (uint32_t)h, (uint32_t)w, (uint32_t)front, dp, npix);
+    return launch_status(what);
+}
 
 extern "C" int h3v_causal_reflect_pack(const uint16_t* x, uint16_t* out, int batch, int c, int d, int h, int w,
                                        int front, int top, int bottom, int left, int right, hipStream_t stream) {

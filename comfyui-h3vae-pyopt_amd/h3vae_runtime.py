@@ -27,8 +27,11 @@ Differences from the reference runtime, all deliberate:
 * The FP16 encoder suffix is the reference's clip-batched ``fused_suffix``
   (all stages): per-frame GroupNorm/SiLU/pad producers as
   ``h3v_gn_norm_pack_f16`` and the 3x3x3 stride-1 convolutions that fit as
-  ``h3v_conv3d_f16``; downsample, shortcut and conv_out convolutions stay the
-  model's.
+  ``h3v_conv3d_f16``.
+* The other FP16 encoder convolutions (conv_in, the prefix downsamples, the
+  ``nin_shortcut`` projections, conv_out) also run as ``h3v_conv3d_f16``
+  where the reference calls cuDNN; conv_in is routed through the same
+  internal-padding wrapper as ``down.0.downsample.conv``.
 """
 from __future__ import annotations
 
@@ -244,6 +247,12 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         enc = core.encoder.to(memory_format=torch.channels_last_3d)
         quant = core.quant_conv.to(memory_format=torch.channels_last_3d)
         replace_selected(enc, ["down.0.downsample.conv"])
+        try:
+            # conv_in (3 channels) through the tap-folded native conv; a conv_in that is not a causal
+            # reflect-padded CausalConv3d stays the model's
+            replace_selected(enc, ["conv_in"])
+        except ValueError:
+            pass
         prefix = next_fused_prefix(enc, "extend_bias_pack")
         suffix = fused_suffix(enc, quant, all_stages=True)
         metadata = None

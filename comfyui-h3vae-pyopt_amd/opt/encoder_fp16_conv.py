@@ -14,8 +14,10 @@ input window of a tile in LDS; every other geometry is an implicit GEMM.
 
 Inputs are channels-last-3d and already padded; weights are packed once per
 weight tensor to [Cout, kd*kh*kw*Cin] (c fastest).  ``conv3d_f16_fits`` is the
-shape gate: convs outside it (Cin not a multiple of 32, such as conv_in with
-3 channels) keep the model's ``F.conv3d``, as in the reference.
+shape gate (Cin a multiple of 32).  ``conv_in`` (3 input channels, a model
+layer the reference leaves alone) runs through ``padded_causal_conv3d`` too:
+its 3x3 spatial taps and channels are folded into 32 channels by one pack
+kernel (``h3v_tap_fold_pack``), leaving a 3x1x1 conv with K = 96.
 """
 from __future__ import annotations
 
@@ -23,6 +25,7 @@ from typing import List, Optional
 
 import torch
 import torch.nn.functional as F
+from torch.utils.weak import WeakIdKeyDictionary
 
 from .. import _hip
 
@@ -32,6 +35,16 @@ def pack_conv_weight_f16(weight):
     if weight.ndim != 5 or weight.dtype != torch.float16:
         raise ValueError("expected an fp16 [Cout, Cin, kd, kh, kw] weight")
     return weight.permute(0, 2, 3, 4, 1).reshape(weight.shape[0], -1).contiguous()
+
+
+def fold_conv_weight_f16(weight, cf=32):
+    """fp16 [Cout, C, 3, 3, 3] (9C <= cf) -> [Cout, 3 * cf]: k = (kd, (kh*3 + kw)*C + c), zero beyond 9C."""
+    if weight.ndim != 5 or weight.dtype != torch.float16 or tuple(weight.shape[2:]) != (3, 3, 3) or 9 * weight.shape[1] > cf:
+        raise ValueError("expected an fp16 [Cout, C, 3, 3, 3] weight with 9 * C <= folded channels")
+    o, c = weight.shape[:2]
+    folded = weight.new_zeros((o, 3, cf))
+    folded[:, :, :9 * c] = weight.permute(0, 2, 3, 4, 1).reshape(o, 3, 9 * c)
+    return folded.reshape(o, 3 * cf).contiguous()
 
 
 def conv3d_f16_fits(x, weight, stride):
@@ -128,21 +141,57 @@ def _fake_pack(x, front, top, bottom, left, right):
                        memory_format=torch.channels_last_3d)
 
 
-class _PackedWeights:
-    """Packed fp16 copies of conv weights, made once per weight tensor and version."""
+def _check_fold(x, front):
+    if x.ndim != 5 or x.dtype != torch.float16 or not 1 <= x.shape[1] <= 3 or x.numel() == 0:
+        raise ValueError("tap_fold_pack requires a nonempty fp16 [B, C, D, H, W] input with C in 1..3")
+    if min(x.shape[3:]) < 2 or front < 0:
+        raise ValueError("tap_fold_pack requires H, W >= 2 and front >= 0")
 
-    def __init__(self):
-        self._cache = {}
+
+@torch.library.custom_op("h3vae_encoder::tap_fold_pack", mutates_args=(), device_types="cuda")
+def tap_fold_pack(x: torch.Tensor, front: int) -> torch.Tensor:
+    """fp16 [B, C<=3, D, H, W] -> [B, 32, D+front, H, W] channels-last-3d: channel (kh*3 + kw)*C + c holds the
+    (kh, kw) tap of the reflect-padded input (a 3x3x3 conv over x = a 3x1x1 conv over this)."""
+    _check_fold(x, front)
+    _hip.require_gfx950(x.device, "tap_fold_pack")
+    x = x.contiguous(memory_format=torch.channels_last_3d)
+    b, c, d, h, w = x.shape
+    out = torch.empty((b, 32, d + front, h, w), device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
+    _hip.call("h3v_tap_fold_pack", _hip.ptr(x), _hip.ptr(out), b, c, d, h, w, front, 32, _hip.stream(x.device))
+    return out
+
+
+@tap_fold_pack.register_fake
+def _fake_fold(x, front):
+    _check_fold(x, front)
+    b, _, d, h, w = x.shape
+    return torch.empty((b, 32, d + front, h, w), device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
+
+
+class _PackedWeights:
+    """Packed fp16 copies of conv weights, one per live weight tensor.
+
+    Keyed by the tensor object (weakly: a copy lives as long as its weight), stamped with
+    the storage address, device, dtype, shape and in-place version, so a module move or an
+    in-place load repacks.  Inference tensors carry no version counter: their in-place
+    updates (inside inference mode) are not seen."""
+
+    def __init__(self, pack=pack_conv_weight_f16):
+        self._cache = WeakIdKeyDictionary()
+        self._pack = pack
 
     def get(self, weight):
-        key = (weight.data_ptr(), tuple(weight.shape), weight.device)
-        hit = self._cache.get(key)
-        if hit is None or hit[0] != weight._version:
-            hit = self._cache[key] = (weight._version, pack_conv_weight_f16(weight.detach()))
+        stamp = (weight.data_ptr(), weight.device, weight.dtype, tuple(weight.shape),
+                 -1 if weight.is_inference() else weight._version)
+        hit = self._cache.get(weight)
+        if hit is None or hit[0] != stamp:
+            hit = (stamp, self._pack(weight.detach()))
+            self._cache[weight] = hit
         return hit[1]
 
 
 _PACKED = _PackedWeights()
+_FOLDED = _PackedWeights(fold_conv_weight_f16)
 
 
 def native_device(x):
@@ -180,6 +229,11 @@ def padded_causal_conv3d(x, weight, bias, stride, front, top, bottom, left, righ
     """Zero frames in front + reflect border + valid conv, the padding packed by one HIP kernel.
 
     The output has exactly (D + front - kd) // sd + 1 frames."""
+    if (native_device(x) and x.dtype == torch.float16 and weight.dtype == torch.float16 and 1 <= x.shape[1] <= 3
+            and tuple(weight.shape[1:]) == (x.shape[1], 3, 3, 3) and tuple(stride) == (1, 1, 1)
+            and (top, bottom, left, right) == (1, 1, 1, 1) and min(x.shape[3:]) >= 2):
+        xf = tap_fold_pack(x, front)
+        return conv3d_f16(xf, _FOLDED.get(weight), bias, [3, 1, 1], [1, 1, 1], front == 2)
     if native_device(x) and x.shape[1] % 8 == 0 and max(top, bottom) < x.shape[3] and max(left, right) < x.shape[4]:
         xp = causal_reflect_pack(x, front, top, bottom, left, right)
         if conv3d_f16_fits(xp, weight, stride):

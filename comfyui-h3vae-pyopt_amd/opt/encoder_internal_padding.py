@@ -3,10 +3,12 @@
 Mirror of opt/encoder_internal_padding.py in fishelegs/ComfyUI-H3VAE-PyOpt.
 The spatial reflect pad stays explicit; the left-only causal zero frames are
 requested from the convolution as symmetric temporal padding and the extra
-tail outputs are dropped.  Used for ``down.0.downsample.conv``, an FP16
-layer outside the INT8 path.  On gfx950 the zero frames and the reflect
-border are written by one pack kernel (``h3v_causal_reflect_pack``) and the
-convolution runs as ``h3v_conv3d_f16`` over exactly the kept outputs.
+tail outputs are dropped.  Used for ``down.0.downsample.conv`` (and, in this
+build's runtime, ``conv_in``), FP16 layers outside the INT8 path.  On gfx950
+the zero frames and the reflect border are written by one pack kernel
+(``h3v_causal_reflect_pack``; for conv_in's 3 channels ``h3v_tap_fold_pack``,
+which also folds the 3x3 spatial taps into 32 channels) and the convolution
+runs as ``h3v_conv3d_f16`` over exactly the kept outputs.
 """
 from __future__ import annotations
 

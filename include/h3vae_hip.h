@@ -254,6 +254,16 @@ int h3v_residual_downsample_pack(const uint16_t* x, const uint16_t* residual, co
 int h3v_causal_reflect_pack(const uint16_t* x, uint16_t* out, int batch, int c, int d, int h, int w, int front,
                             int top, int bottom, int left, int right, hipStream_t stream);
 
+/* Tap-folded pack for the encoder's conv_in (the model's CausalConv3d with 3
+ * input channels, run as F.conv3d by the reference: it is not replaced there).
+ * x: fp16 NDHWC [batch, d, h, w, c]; out: fp16 NDHWC [batch, d + front, h, w, cf]
+ * with out[.., t, i, j, (kh*3 + kw)*c + ch] = x[.., t - front, r(i + kh - 1),
+ * r(j + kw - 1), ch] (r: reflect) for t >= front and zero otherwise, channels
+ * 9c .. cf-1 zero.  The 3x3x3 conv becomes a 3x1x1 conv over cf channels
+ * (h3v_conv3d_f16).  cf == 32, c in 1..3, h, w >= 2, 16-byte aligned out. */
+int h3v_tap_fold_pack(const uint16_t* x, uint16_t* out, int batch, int c, int d, int h, int w, int front, int cf,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

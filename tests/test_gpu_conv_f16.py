@@ -167,6 +167,44 @@ def test_causal_reflect_pack_matches_torch_pad(fc, shape, pads):
     assert torch.equal(y.cpu(), want)
 
 
+@pytest.mark.parametrize("c,b,d,h,w,front", [(3, 1, 5, 16, 20, 2), (1, 2, 3, 6, 9, 2), (2, 1, 1, 4, 4, 0)])
+def test_tap_fold_pack_matches_torch(fc, c, b, d, h, w, front):
+    gen = torch.Generator().manual_seed(c + d + h)
+    x = torch.randn(b, c, d, h, w, generator=gen).half()
+    with torch.inference_mode():
+        y = fc.tap_fold_pack(x.to(DEV).contiguous(memory_format=torch.channels_last_3d), front)
+        torch.cuda.synchronize()
+    xp = F.pad(F.pad(x.float(), (1, 1, 1, 1, 0, 0), mode="reflect"), (0, 0, 0, 0, front, 0))
+    want = torch.zeros(b, 32, d + front, h, w)
+    for kh in range(3):
+        for kw in range(3):
+            want[:, (kh * 3 + kw) * c:(kh * 3 + kw + 1) * c] = xp[:, :, :, kh:kh + h, kw:kw + w]
+    assert y.is_contiguous(memory_format=torch.channels_last_3d)
+    assert torch.equal(y.cpu(), want.half())
+
+
+@pytest.mark.parametrize("d,hw", [(17, 64), (1, 32), (5, 40)])
+def test_conv_in_through_internal_padding_matches_float64(pkg, d, hw):
+    """conv_in (3 -> 128) via ImplicitTemporalPadConv3d: tap-folded pack + 3x1x1 conv3d_f16, against a float64
+    run of the model's padding and 3x3x3 conv (one image frame: two zero frames in front, as the model pads)."""
+    ip = importlib.import_module(f"{pkg.__name__}.opt.encoder_internal_padding")
+    torch.manual_seed(d + hw)
+    conv = h3_arch.CausalConv3d(3, 128).half().to(DEV).eval()
+    wrapped = ip.ImplicitTemporalPadConv3d(conv)
+    gen = torch.Generator().manual_seed(hw)
+    x = (torch.rand(1, 3, d, hw, hw, generator=gen) * 4 - 2).half()
+    with torch.inference_mode():
+        y = wrapped(x.to(DEV).contiguous(memory_format=torch.channels_last_3d))
+        model = conv(x.to(DEV))
+        torch.cuda.synchronize()
+    xp = F.pad(F.pad(x.double(), (1, 1, 1, 1, 0, 0), mode="reflect"), (0, 0, 0, 0, 2, 0))
+    w64, b64 = conv.weight.detach().cpu().double(), conv.bias.detach().cpu().double()
+    ref = F.conv3d(xp, w64, b64)
+    mag = F.conv3d(xp.abs(), w64.abs())
+    assert y.shape == ref.shape == model.shape == (1, 128, d, hw, hw)
+    _assert_close(y, ref, mag)
+
+
 def test_stage0_downsample_matches_model(pkg, fc):
     """down.0.downsample.conv through ImplicitTemporalPadConv3d (pack + conv3d_f16) == the model's CausalConv3d
     within the fp16 bound, against a float64 run of the model's own padding."""

@@ -56,8 +56,10 @@ def test_runtime_encode_matches_model_modules(rt, pkg, int8_encode, clips):
     core = _Core().eval()
     ref_enc = copy.deepcopy(core.encoder).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
     ref_quant = copy.deepcopy(core.quant_conv).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
-    runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, int8_encode=int8_encode,
-                                   encoder_staged_batch=4, log_calls=False, core=core, config=_config())
+    # the INT8 two-clip case builds the runtime under inference mode (its weights become inference tensors)
+    with torch.inference_mode(int8_encode and clips == 2):
+        runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, int8_encode=int8_encode,
+                                       encoder_staged_batch=4, log_calls=False, core=core, config=_config())
     gen = torch.Generator().manual_seed(clips)
     x = (torch.rand(1, 3, 17 * clips, 64, 64, generator=gen) * 2 - 1).half().to(DEV)
     with torch.inference_mode():

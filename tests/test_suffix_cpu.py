@@ -85,3 +85,43 @@ def test_cpu_tensors_keep_the_model_convs(fc):
     assert torch.equal(fc.valid_conv3d(x, w, b, (1, 2, 2)), F.conv3d(x, w, b, stride=(1, 2, 2)))
     want = F.conv3d(F.pad(F.pad(x, (1, 1, 1, 1, 0, 0), mode="reflect"), (0, 0, 0, 0, 2, 0)), w, b, stride=(1, 2, 2))
     assert torch.equal(fc.padded_causal_conv3d(x, w, b, (1, 2, 2), 2, 1, 1, 1, 1), want)
+
+
+def test_packed_weight_cache_tracks_tensors(fc):
+    cache = fc._PackedWeights()
+    gen = torch.Generator().manual_seed(3)
+    w = torch.nn.Parameter(torch.randn(4, 32, 3, 3, 3, generator=gen).half(), requires_grad=False)
+    p1 = cache.get(w)
+    assert cache.get(w) is p1                                  # reused while unchanged
+    with torch.no_grad():
+        w.mul_(2)                                              # in-place update (a state-dict load) repacks
+    p2 = cache.get(w)
+    assert p2 is not p1 and torch.equal(p2, fc.pack_conv_weight_f16(w.detach()))
+    other = torch.nn.Parameter(w.detach().clone() + 1, requires_grad=False)
+    assert torch.equal(cache.get(other), fc.pack_conv_weight_f16(other.detach()))
+    with torch.inference_mode():                               # weights created under inference mode
+        wi = torch.randn(4, 32, 3, 3, 3, generator=gen).half()
+        assert torch.equal(cache.get(wi), fc.pack_conv_weight_f16(wi))
+        assert cache.get(wi) is cache.get(wi)
+    n = len(cache._cache)
+    del other
+    import gc
+    gc.collect()
+    assert len(cache._cache) == n - 1                          # a copy lives only as long as its weight
+
+
+def test_folded_conv_in_weight_layout(fc):
+    gen = torch.Generator().manual_seed(4)
+    w = torch.randn(6, 3, 3, 3, 3, generator=gen).half()
+    f = fc.fold_conv_weight_f16(w)
+    assert f.shape == (6, 96) and f.is_contiguous()
+    for o, c, kd, kh, kw in [(0, 0, 0, 0, 0), (5, 2, 2, 2, 2), (3, 1, 1, 0, 2)]:
+        assert f[o, kd * 32 + (kh * 3 + kw) * 3 + c] == w[o, c, kd, kh, kw]
+    assert not f.view(6, 3, 32)[:, :, 27:].any()
+    with pytest.raises(ValueError):
+        fc.fold_conv_weight_f16(torch.zeros(6, 4, 3, 3, 3, dtype=torch.float16))
+    x = torch.empty((1, 3, 5, 16, 16), dtype=torch.float16, device="meta")
+    y = fc.tap_fold_pack(x, 2)
+    assert y.shape == (1, 32, 7, 16, 16) and y.is_contiguous(memory_format=torch.channels_last_3d)
+    with pytest.raises(ValueError, match="C in 1..3"):
+        fc.tap_fold_pack(torch.empty((1, 4, 5, 16, 16), dtype=torch.float16, device="meta"), 2)
