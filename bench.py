@@ -414,8 +414,8 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
             do, ho, wo = (dp - k) // stride[0] + 1, (hp - k) // stride[1] + 1, (wp - k) // stride[2] + 1
             ys = torch.empty((b, cout, do, ho, wo), device=dev, dtype=f16).contiguous(
                 memory_format=torch.channels_last_3d)
-            t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), p(ys), b, cin, dp, hp, wp, cout, k, k, k,
-                                     *stride, int(causal), stream))
+            t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), None, p(ys), b, cin, dp, hp, wp, cout, k, k,
+                                     k, *stride, int(causal), stream))
             t_t = timed(lambda: F.conv3d(xs, ws, bs, stride=stride))
             xn = xs.contiguous()
             t_n = timed(lambda: F.conv3d(xn, ws, bs, stride=stride))

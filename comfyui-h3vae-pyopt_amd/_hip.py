@@ -35,6 +35,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_gemm_i8_dequant": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "h3v_gemm_i8_swiglu": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P],
     "h3v_gemm_i8_i32": [_P, _P, _P, _I64, _I64, _I64, _P],
+    "h3v_conv3d_i8_residual": [_P] * 7 + [_I] * 13 + [_P],
     "h3v_conv3d_i8": [_P, _P, _P, _P, _P, _P] + [_I] * 13 + [_P],
     "h3v_conv3d_i8_i32": [_P, _P, _P] + [_I] * 13 + [_P],
     "h3v_tensor_quant_i8": [_P, _I64, _P, _P, _P, _P],
@@ -50,7 +51,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_finalize_pixels": [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P],
     "h3v_causal_reflect_pack": [_P, _P] + [_I] * 10 + [_P],
     "h3v_tap_fold_pack": [_P, _P] + [_I] * 7 + [_P],
-    "h3v_conv3d_f16": [_P, _P, _P, _P] + [_I] * 13 + [_P],
+    "h3v_conv3d_f16": [_P, _P, _P, _P, _P] + [_I] * 13 + [_P],
     "h3v_gn_norm_pack_f16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "h3v_attention_d64": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
 }

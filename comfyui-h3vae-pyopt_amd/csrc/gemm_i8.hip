@@ -53,6 +53,7 @@ struct GemmParams {
     int sx_stride;
     const float* sw;   // per weight row
     const uint16_t* bias;  // fp16 per weight row, nullable
+    const uint16_t* res;   // fp16 residual in the output's layout, nullable: out = fp16(fp32(y) + fp32(res))
     void* out;
     int64_t ldo;
     int tiles_m, tiles_n;
@@ -391,22 +392,61 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
         };
         if (has_bias) convert(std::true_type{});
         else convert(std::false_type{});
-        lds_barrier();   // the output tile is complete in LDS
         const int gcol0 = (EP == Epi::SwiGLU) ? tn * (BN / 2) : n0;
         uint16_t* out = static_cast<uint16_t*>(p.out);
+        if (p.res == nullptr) {
+            lds_barrier();   // the output tile is complete in LDS
 #pragma unroll 4
-        for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
-            const int r = idx / RCH, ch = idx - r * RCH;
-            const int grow = m0 + r, gcol = gcol0 + ch * 8;
-            if (grow >= p.M || gcol >= p.N) continue;
-            const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
-            uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
-            if (p.vec_out && gcol + 8 <= p.N) {
-                *reinterpret_cast<u16x8*>(dst) = v;
-            } else {
+            for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
+                const int r = idx / RCH, ch = idx - r * RCH;
+                const int grow = m0 + r, gcol = gcol0 + ch * 8;
+                if (grow >= p.M || gcol >= p.N) continue;
+                const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
+                uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+                if (p.vec_out && gcol + 8 <= p.N) {
+                    *reinterpret_cast<u16x8*>(dst) = v;
+                } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    if (gcol + e < p.N) dst[e] = v[e];
+                    for (int e = 0; e < 8; ++e)
+                        if (gcol + e < p.N) dst[e] = v[e];
+                }
+            }
+        } else {
+            // The residual block's closing add, fused: out = fp16(fp32(res) + fp32(y)) with y the rounded
+            // output.  Every residual piece this thread stores is loaded before the barrier (the
+            // accumulators are dead by now), so the loads overlap the barrier and each other.
+            constexpr int NT = NW * 64;
+            constexpr int PER = (BM * RCH + NT - 1) / NT;
+            u16x8 rv[PER] = {};
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int idx = tid + i * NT;
+                const int r = idx / RCH, ch = idx - r * RCH;
+                const int grow = m0 + r, gcol = gcol0 + ch * 8;
+                if (idx < BM * RCH && grow < p.M && p.vec_out && gcol + 8 <= p.N)
+                    rv[i] = *reinterpret_cast<const u16x8*>(p.res + (int64_t)grow * p.ldo + gcol);
+            }
+            lds_barrier();   // the output tile is complete in LDS
+#pragma unroll
+            for (int i = 0; i < PER; ++i) {
+                const int idx = tid + i * NT;
+                const int r = idx / RCH, ch = idx - r * RCH;
+                const int grow = m0 + r, gcol = gcol0 + ch * 8;
+                if (idx >= BM * RCH || grow >= p.M || gcol >= p.N) continue;
+                u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
+                uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+                if (p.vec_out && gcol + 8 <= p.N) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] = f2h(h2f(rv[i][e]) + h2f(v[e]));
+                    *reinterpret_cast<u16x8*>(dst) = v;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e)
+                        if (gcol + e < p.N) {
+                            const int64_t o = (int64_t)grow * p.ldo + gcol + e;
+                            dst[e] = f2h(h2f(p.res[o]) + h2f(v[e]));
+                        }
+                }
             }
         }
     }
@@ -903,7 +943,9 @@ __global__ __launch_bounds__(256) void gemm_i8_generic(GemmParams p) {
     } else if constexpr (EP == Epi::Int32) {
         static_cast<int32_t*>(p.out)[(int64_t)row * p.ldo + col] = dot(col);
     } else {
-        static_cast<uint16_t*>(p.out)[(int64_t)row * p.ldo + col] = f2h(g1_value(dot(col), sx, p.sw[col], p.bias, col));
+        const int64_t o = (int64_t)row * p.ldo + col;
+        const uint16_t y = f2h(g1_value(dot(col), sx, p.sw[col], p.bias, col));
+        static_cast<uint16_t*>(p.out)[o] = p.res ? f2h(h2f(p.res[o]) + h2f(y)) : y;
     }
 }
 
@@ -913,7 +955,7 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     p.tiles_m = (p.M + BM - 1) / BM;
     p.tiles_n = (ncols + BN - 1) / BN;
     p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) && p.N % 4 == 0;
-    p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
+    p.vec_out = aligned(p.out, 16) && (p.res == nullptr || aligned(p.res, 16)) && p.ldo % 8 == 0;
     p.conv_tpf = 0;
     if (AM == AMode::Conv && ((int64_t)p.Ho * p.Wo) % BM == 0) p.conv_tpf = (int)((int64_t)p.Ho * p.Wo / BM);
     int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
@@ -954,7 +996,7 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.tiles_m = p.M / 512;
     p.tiles_n = p.N / 128;
     p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) && p.N % 4 == 0;
-    p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
+    p.vec_out = aligned(p.out, 16) && (p.res == nullptr || aligned(p.res, 16)) && p.ldo % 8 == 0;
     p.conv_tpf = 0;
     const int64_t grid = (int64_t)p.tiles_m * p.tiles_n;
     const int64_t a_bytes = (int64_t)(p.M / ((int64_t)p.Do * p.Ho * p.Wo)) * p.Dp * p.Hp * p.Wp * p.C * ES;
@@ -1110,17 +1152,35 @@ int h3v_conv3d_i8(const int8_t* qx, const float* x_scale, const int8_t* qw, cons
     return run_conv<Epi::Dequant>(p, stream, what);
 }
 
-int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int batch, int cin,
-                   int d, int h, int wd, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
-                   hipStream_t stream) {
+int h3v_conv3d_i8_residual(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                           const uint16_t* bias, const uint16_t* residual, uint16_t* out, int batch, int cin, int d,
+                           int h, int w, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                           hipStream_t stream) {
+    const char* what = "h3v_conv3d_i8_residual";
+    H3V_REQUIRE(qx && x_scale && qw && w_scale && residual && out, "%s: null pointer argument", what);
+    H3V_REQUIRE(residual != out, "%s: the residual must not alias the output", what);
+    GemmParams p{};
+    int rc = fill_conv(p, what, batch, cin, d, h, w, cout, kd, kh, kw, sd, sh, sw);
+    if (rc) return rc;
+    p.a = qx; p.b = qw; p.sx = x_scale; p.sx_stride = 0; p.sw = w_scale; p.bias = bias; p.out = out;
+    p.res = residual;
+    p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
+    return run_conv<Epi::Dequant>(p, stream, what);
+}
+
+int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
+                   uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw, int sd,
+                   int sh, int sw, int causal_skip, hipStream_t stream) {
     const char* what = "h3v_conv3d_f16";
     H3V_REQUIRE(x && w && out, "%s: null pointer argument", what);
+    H3V_REQUIRE(residual != out, "%s: the residual must not alias the output", what);
     GemmParams p{};
     int rc = fill_conv(p, what, batch, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw);
     if (rc) return rc;
     p.a = reinterpret_cast<const int8_t*>(x);
     p.b = reinterpret_cast<const int8_t*>(w);
     p.bias = bias;
+    p.res = residual;
     p.out = out;
     p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
     H3V_REQUIRE(cin % 32 == 0 && aligned(x, 16) && aligned(w, 16),

@@ -60,7 +60,7 @@ def conv3d_f16_fits(x, weight, stride):
     return x.numel() * 2 < 2 ** 32 and weight.numel() * 2 < 2 ** 31 and m < 2 ** 31
 
 
-def _check_conv(x, w_packed, bias, kernel_size, stride):
+def _check_conv(x, w_packed, bias, kernel_size, stride, residual=None):
     if x.ndim != 5 or x.dtype != torch.float16 or w_packed.dtype != torch.float16 or w_packed.ndim != 2:
         raise ValueError("conv3d_f16 requires an fp16 [B, C, D, H, W] input and an fp16 [Cout, K] packed weight")
     if len(kernel_size) != 3 or len(stride) != 3 or min(kernel_size) < 1 or min(stride) < 1:
@@ -76,6 +76,9 @@ def _check_conv(x, w_packed, bias, kernel_size, stride):
         raise ValueError("conv3d_f16 requires a contiguous fp16 [Cout] bias")
     if b > 1 and not x.is_contiguous(memory_format=torch.channels_last_3d):
         raise ValueError("conv3d_f16 requires a channels-last-3d input")
+    if residual is not None and (residual.dtype != torch.float16
+                                 or tuple(residual.shape) != _out_shape(x, w_packed, kernel_size, stride)):
+        raise ValueError("conv3d_f16 requires an fp16 residual of the output's shape")
 
 
 def _out_shape(x, w_packed, kernel_size, stride):
@@ -86,25 +89,28 @@ def _out_shape(x, w_packed, kernel_size, stride):
 
 @torch.library.custom_op("h3vae_encoder::conv3d_f16", mutates_args=(), device_types="cuda")
 def conv3d_f16(x: torch.Tensor, w_packed: torch.Tensor, bias: Optional[torch.Tensor], kernel_size: List[int],
-               stride: List[int], causal_skip: bool) -> torch.Tensor:
+               stride: List[int], causal_skip: bool, residual: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Valid conv of a padded fp16 [B, C, D, H, W] (channels-last-3d) -> fp16 [B, Cout, Do, Ho, Wo] channels-last-3d.
 
-    causal_skip (3-deep kernels at depth stride 1) assumes two zero leading frames per item."""
-    _check_conv(x, w_packed, bias, kernel_size, stride)
+    causal_skip (3-deep kernels at depth stride 1) assumes two zero leading frames per item; residual (the
+    output's shape) is added as a separate fp16 add would: fp16(residual + fp16 output)."""
+    _check_conv(x, w_packed, bias, kernel_size, stride, residual)
     _hip.require_gfx950(x.device, "conv3d_f16")
     if not x.is_contiguous(memory_format=torch.channels_last_3d):
         x = x.contiguous(memory_format=torch.channels_last_3d)
+    if residual is not None and not residual.is_contiguous(memory_format=torch.channels_last_3d):
+        residual = residual.contiguous(memory_format=torch.channels_last_3d)
     b, c, d, h, w = x.shape
     out = torch.empty(_out_shape(x, w_packed, kernel_size, stride), device=x.device, dtype=x.dtype,
                       memory_format=torch.channels_last_3d)
-    _hip.call("h3v_conv3d_f16", _hip.ptr(x), _hip.ptr(w_packed), _hip.ptr(bias), _hip.ptr(out), b, c, d, h, w,
-              w_packed.shape[0], *kernel_size, *stride, int(bool(causal_skip)), _hip.stream(x.device))
+    _hip.call("h3v_conv3d_f16", _hip.ptr(x), _hip.ptr(w_packed), _hip.ptr(bias), _hip.ptr(residual), _hip.ptr(out),
+              b, c, d, h, w, w_packed.shape[0], *kernel_size, *stride, int(bool(causal_skip)), _hip.stream(x.device))
     return out
 
 
 @conv3d_f16.register_fake
-def _fake_conv(x, w_packed, bias, kernel_size, stride, causal_skip):
-    _check_conv(x, w_packed, bias, kernel_size, stride)
+def _fake_conv(x, w_packed, bias, kernel_size, stride, causal_skip, residual=None):
+    _check_conv(x, w_packed, bias, kernel_size, stride, residual)
     return torch.empty(_out_shape(x, w_packed, kernel_size, stride), device=x.device, dtype=x.dtype,
                        memory_format=torch.channels_last_3d)
 
@@ -199,21 +205,23 @@ def native_device(x):
     return x.is_cuda and _hip.is_gfx950(x.device)
 
 
-def valid_conv3d(x, weight, bias, stride, causal_skip=False):
+def valid_conv3d(x, weight, bias, stride, causal_skip=False, residual=None):
     """Valid convolution of an already padded input: h3v_conv3d_f16 when the shape fits, else F.conv3d.
 
-    causal_skip: x holds two zero leading frames per item (the producers' causal padding)."""
+    causal_skip: x holds two zero leading frames per item (the producers' causal padding).
+    residual: the residual block's closing ``residual + conv`` fused into the epilogue."""
     stride = tuple(stride)
     if native_device(x) and conv3d_f16_fits(x, weight, stride):
         kernel = list(weight.shape[2:])
         skip = bool(causal_skip) and kernel[0] == 3 and stride[0] == 1
-        return conv3d_f16(x, _PACKED.get(weight), bias, kernel, list(stride), skip)
-    return F.conv3d(x, weight, bias, stride=stride)
+        return conv3d_f16(x, _PACKED.get(weight), bias, kernel, list(stride), skip, residual)
+    y = F.conv3d(x, weight, bias, stride=stride)
+    return y if residual is None else residual + y
 
 
-def producer_conv3d(y, weight, bias, stride):
+def producer_conv3d(y, weight, bias, stride, residual=None):
     """The FP16 conv after a GroupNorm/SiLU/pad producer (two zero leading frames per item)."""
-    return valid_conv3d(y, weight, bias, stride, causal_skip=True)
+    return valid_conv3d(y, weight, bias, stride, causal_skip=True, residual=residual)
 
 
 def pointwise_conv3d(x, conv):

@@ -76,11 +76,12 @@ class BatchedResidualBlock(torch.nn.Module):
     def forward(self, x, zq=None):
         if zq is not None:
             raise ValueError("Unconditional inference only")
+        residual = pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x
         h = producer_conv3d(self.first(x), self.first.weight, None, self.first.stride)
         h = batched_temporal_norm_pack(h, self.first.bias, self.second.norm_weight, self.second.norm_bias,
                                        self.second.eps)
-        h = producer_conv3d(h, self.second.weight, self.second.bias, self.second.stride)
-        return (pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x) + h
+        # the closing residual add runs in the second conv's epilogue (fp16(residual + fp16 conv))
+        return producer_conv3d(h, self.second.weight, self.second.bias, self.second.stride, residual=residual)
 
 
 class BatchedSuffix(EncoderSuffix):

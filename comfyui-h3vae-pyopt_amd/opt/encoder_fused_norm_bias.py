@@ -151,7 +151,20 @@ class BiasFusedResidualBlock(torch.nn.Module):
                 else producer_conv3d(second_input, self.second.weight, second_bias, self.second.stride))
 
     def forward(self, x, zq=None):
+        """(shortcut(x) or x) + body(x), the add fused into the second conv's epilogue where that conv is a
+        kernel of this package (bit-identical to the separate fp16 add of the reference, :141)."""
         if zq is not None:
             raise ValueError("Unconditional inference only")
-        h = self._residual_body(x, self.second.bias)
-        return (pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x) + h
+        residual = pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x
+        if self.int8_first is not None and self.int8_first.fuse_norm:
+            h = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
+            return self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias, self.second.eps,
+                                                 pre_bias=self.first.bias, residual=residual)
+        if self.int8_first is None:
+            first_input = self.first(x)
+            h = producer_conv3d(first_input, self.first.weight, None, self.first.stride)
+            second_input = bias_temporal_norm_pack(h, self.first.bias, self.second.norm_weight,
+                                                   self.second.norm_bias, self.second.eps)
+            return producer_conv3d(second_input, self.second.weight, self.second.bias, self.second.stride,
+                                   residual=residual)
+        return residual + self._residual_body(x, self.second.bias)

@@ -178,12 +178,13 @@ def int8_valid_conv3d(x, qweight, weight_scale, *, config: Int8Conv3DConfig, bia
 
 
 def _conv3d_from_quantized(qx, activation_scale, qweight, weight_scale, *, config: Int8Conv3DConfig, bias,
-                           tile_variant: str, causal_prefix_zero: bool = False):
+                           tile_variant: str, causal_prefix_zero: bool = False, residual=None):
     """Launch the implicit-GEMM conv on an int8 NDHWC input.
 
     Only a producer that guarantees two leading zero temporal planes may set
     causal_prefix_zero; the skipped taps multiply those zeros, so the result is
-    identical to the full reduction.
+    identical to the full reduction.  ``residual`` (fp16, the output's shape)
+    is added in the epilogue exactly as a following fp16 ``residual + out``.
     """
     if tile_variant not in _TILE_VARIANTS:
         raise ValueError(f"unknown tile variant {tile_variant!r}")
@@ -194,9 +195,17 @@ def _conv3d_from_quantized(qx, activation_scale, qweight, weight_scale, *, confi
     b, c, d, h, w = qx.shape
     kd, kh, kw = config.kernel_size
     sd, sh, sw = config.stride
-    _hip.call("h3v_conv3d_i8", _hip.ptr(qx), _hip.ptr(activation_scale), _hip.ptr(qweight), _hip.ptr(weight_scale),
-              _hip.ptr(bias), _hip.ptr(output), b, c, d, h, w, config.out_channels, kd, kh, kw, sd, sh, sw,
-              int(bool(causal_prefix_zero)), _hip.stream(qx.device))
+    if residual is None:
+        _hip.call("h3v_conv3d_i8", _hip.ptr(qx), _hip.ptr(activation_scale), _hip.ptr(qweight),
+                  _hip.ptr(weight_scale), _hip.ptr(bias), _hip.ptr(output), b, c, d, h, w, config.out_channels, kd, kh,
+                  kw, sd, sh, sw, int(bool(causal_prefix_zero)), _hip.stream(qx.device))
+        return output
+    if residual.shape != output.shape or residual.dtype != torch.float16 or residual.device != output.device:
+        raise ValueError("residual must be an fp16 tensor of the convolution output's shape on its device")
+    residual = residual.contiguous(memory_format=torch.channels_last_3d)
+    _hip.call("h3v_conv3d_i8_residual", _hip.ptr(qx), _hip.ptr(activation_scale), _hip.ptr(qweight),
+              _hip.ptr(weight_scale), _hip.ptr(bias), _hip.ptr(residual), _hip.ptr(output), b, c, d, h, w,
+              config.out_channels, kd, kh, kw, sd, sh, sw, int(bool(causal_prefix_zero)), _hip.stream(qx.device))
     return output
 
 

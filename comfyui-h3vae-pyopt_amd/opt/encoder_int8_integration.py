@@ -96,6 +96,28 @@ def _int8_norm_conv3d_fake(x, norm_weight, norm_bias, pre_bias, eps, qweight, we
                        memory_format=torch.channels_last_3d)
 
 
+@torch.library.custom_op("h3vae_encoder::int8_norm_conv3d_residual", mutates_args=(), device_types="cuda")
+def int8_norm_conv3d_residual(x: torch.Tensor, norm_weight: torch.Tensor, norm_bias: torch.Tensor,
+                              pre_bias: torch.Tensor | None, eps: float, qweight: torch.Tensor,
+                              weight_scale: torch.Tensor, bias: torch.Tensor | None,
+                              residual: torch.Tensor) -> torch.Tensor:
+    """``residual + int8_norm_conv3d(...)`` in one conv launch: the residual block's closing add
+    (opt/encoder_fused_norm_bias.py:141) fused into the conv epilogue, bit-identical to the add."""
+    from .encoder_int8_norm import quantized_temporal_norm_pad
+
+    qx, scale = quantized_temporal_norm_pad(x, norm_weight, norm_bias, eps, pre_bias=pre_bias)
+    return _conv3d_from_quantized(qx, scale, qweight, weight_scale,
+                                  config=Int8Conv3DConfig(x.shape[1], qweight.shape[0], (3, 3, 3), (1, 1, 1)),
+                                  bias=bias, tile_variant="128x128x64_pipeline4", causal_prefix_zero=True,
+                                  residual=residual)
+
+
+@int8_norm_conv3d_residual.register_fake
+def _int8_norm_conv3d_residual_fake(x, norm_weight, norm_bias, pre_bias, eps, qweight, weight_scale, bias, residual):
+    return torch.empty((x.shape[0], qweight.shape[0], *x.shape[2:]), device=x.device, dtype=x.dtype,
+                       memory_format=torch.channels_last_3d)
+
+
 class Int8FusedValidConv3d(nn.Module):
     """Static-weight INT8 wrapper for an already-padded fused Conv3d call."""
 
@@ -142,15 +164,19 @@ class Int8FusedValidConv3d(nn.Module):
         self.bias.data = original_bias.to(device=self.bias.device, dtype=torch.float16)
         return result
 
-    def forward_norm(self, x, norm_weight, norm_bias, eps, pre_bias=None):
+    def forward_norm(self, x, norm_weight, norm_bias, eps, pre_bias=None, residual=None):
+        """Fused producer + conv; ``residual`` adds the block's closing residual in the conv epilogue."""
         if not self.fuse_norm:
             raise RuntimeError("INT8 norm fusion is not enabled for this convolution")
         if x.dtype != torch.float16:
             raise RuntimeError("INT8 encoder convolution requires FP16 activations")
         if x.device != self.qweight.device:
             raise RuntimeError("INT8 encoder activation and qweight must be on the same device")
-        return int8_norm_conv3d(x, norm_weight, norm_bias, pre_bias, eps, self.qweight, self.weight_scale,
-                                self.bias if self.apply_bias else None)
+        bias = self.bias if self.apply_bias else None
+        if residual is not None:
+            return int8_norm_conv3d_residual(x, norm_weight, norm_bias, pre_bias, eps, self.qweight,
+                                             self.weight_scale, bias, residual)
+        return int8_norm_conv3d(x, norm_weight, norm_bias, pre_bias, eps, self.qweight, self.weight_scale, bias)
 
     def forward(self, x):
         if x.dtype != torch.float16:

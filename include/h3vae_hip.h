@@ -86,16 +86,18 @@ int h3v_gn_norm_pack_f16(const uint16_t* x, const uint16_t* pre_bias, const uint
  * [batch, d, h, wd, cin] (already padded); w: fp16 [cout, kd*kh*kw*cin] packed
  * (kd, kh, kw, c) with c fastest; bias: fp16 [cout] (nullable); out: fp16
  * NDHWC [batch, do, ho, wo, cout] with do = (d - kd) / sd + 1 (likewise ho,
- * wo) = fp16(sum fp32 + bias), fp32 accumulation on v_mfma_f32_32x32x16_f16.
+ * wo) = fp16(sum fp32 + bias), fp32 accumulation on v_mfma_f32_32x32x16_f16;
+ * residual (nullable, same layout as out, not aliasing it) adds the residual
+ * block's closing `shortcut(x) + h` as fp16(fp32(residual) + fp32(out)).
  * causal_skip (kd == 3, sd == 1 only): output frames 0 and 1 of each batch
  * item skip the depth taps that read the two leading zero frames.  Requires
  * cin % 32 == 0 and 16-byte aligned x and w.  Stride-1 3x3x3 convs with
  * cout % 128 == 0, an output width of 32, 64, 128 or 256 and an output height
  * that is a multiple of 512 / width run with the input window in LDS; others
  * as an implicit GEMM. */
-int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int batch, int cin,
-                   int d, int h, int wd, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
-                   hipStream_t stream);
+int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
+                   uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw, int sd,
+                   int sh, int sw, int causal_skip, hipStream_t stream);
 
 /* ---- decoder attention (head_dim 64) --------------------------------------
  * Replaces the model's `perform_attention` (flash attention) called from
@@ -172,6 +174,17 @@ int h3v_gemm_i8_i32(const int8_t* a, const int8_t* w, int32_t* acc, int64_t m, i
 int h3v_conv3d_i8(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
                   const uint16_t* bias, uint16_t* out, int batch, int cin, int d, int h, int w, int cout,
                   int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip, hipStream_t stream);
+
+/* The same conv with the residual block's closing add fused into the epilogue:
+ * out = fp16(fp32(residual) + fp32(y)) with y the fp16 output above, i.e. the
+ * `shortcut(x) + h` (or `x + h`) of opt/encoder_fused_norm_bias.py:141
+ * (BiasFusedResidualBlock.forward) in one pass instead of a separate add kernel;
+ * bit-identical to the conv followed by torch's fp16 add.  residual: fp16 NDHWC
+ * [batch, do, ho, wo, cout], not aliasing out. */
+int h3v_conv3d_i8_residual(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                           const uint16_t* bias, const uint16_t* residual, uint16_t* out, int batch, int cin, int d,
+                           int h, int w, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                           hipStream_t stream);
 
 /* Raw int32 accumulators of the same convolution (exactness checks). */
 int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,

@@ -109,6 +109,33 @@ def test_conv_dequant_epilogue(ops, oracle, with_bias, d, h, w, c):
     assert_bitwise(np_(out), want, "conv out")
 
 
+# the residual block's closing add fused into the epilogue: window kernel, implicit GEMM, scalar fallback
+@pytest.mark.parametrize("d,h,w,c,n", [(4, 6, 130, 128, 128), (5, 12, 20, 256, 256), (4, 7, 9, 7, 19)])
+def test_conv_residual_epilogue(ops, oracle, d, h, w, c, n):
+    print(f"conv residual epilogue D={d} {h}x{w} C={c} N={n}", flush=True)
+    gen = _gen(9 + c)
+    qx = torch.randint(-127, 128, (1, d, h, w, c), generator=gen, dtype=torch.int8)
+    qx[:, :2] = 0                                    # the producer's causal zero planes (causal_skip below)
+    qw = torch.randint(-127, 128, (n, 27 * c), generator=gen, dtype=torch.int8)
+    xs = torch.tensor([0.013], dtype=torch.float32)
+    ws = (torch.rand(n, generator=gen) * 0.001 + 1e-4).float()
+    bias = torch.randn(n, generator=gen).half()
+    res = (torch.randn(1, d - 2, h - 2, w - 2, n, generator=gen) * 3).half()
+    out = torch.empty((1, d - 2, h - 2, w - 2, n), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) for t in (qx, xs, qw, ws, bias)]
+    rd = res.to(DEV)
+    ops.hip.call("h3v_conv3d_i8_residual", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(rd), ops.hip.ptr(out), 1, c, d,
+                 h, w, n, 3, 3, 3, 1, 1, 1, 1, ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    acc = oracle.conv3d_acc(qx.numpy(), qw.numpy(), (3, 3, 3), (1, 1, 1))
+    conv = oracle.gemm_dequant(acc.reshape(-1, n), xs.numpy(), ws.numpy(), bias.numpy()).reshape(acc.shape)
+    want = (res.numpy().astype(np.float32) + conv.astype(np.float32)).astype(np.float16)   # torch's fp16 add
+    assert_bitwise(np_(out), want, "conv + residual")
+    with pytest.raises(ValueError, match="alias"):
+        ops.hip.call("h3v_conv3d_i8_residual", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(out), ops.hip.ptr(out), 1,
+                     c, d, h, w, n, 3, 3, 3, 1, 1, 1, 1, ops.hip.stream(DEV))
+
+
 # reference tests/test_encoder_int8_norm.py:38 (seed, c, d, h, w) plus a full-resolution frame set
 NORM_CASES = [(41, 128, 1, 2, 3), (42, 256, 3, 13, 19), (43, 128, 3, 256, 256), (44, 256, 17, 32, 48)]
 

@@ -144,6 +144,29 @@ def test_conv3d_f16_implicit_gemm_matches_float64(fc, b, c, d, h, w, cout, kerne
     _assert_close(y, ref, mag)
 
 
+@pytest.mark.parametrize("b,c,d,h,w,cout,kernel", [(2, 64, 5, 10, 66, 128, (3, 3, 3)), (1, 64, 4, 10, 50, 96, (3, 3, 3)),
+                                                   (3, 256, 4, 8, 8, 256, (1, 1, 1))])
+def test_conv3d_f16_residual_equals_separate_add(fc, b, c, d, h, w, cout, kernel):
+    """The fused residual (window kernel, implicit GEMM, 1x1x1) == the conv followed by torch's fp16 add."""
+    gen = torch.Generator().manual_seed(c + cout + d)
+    x = torch.randn(b, c, d, h, w, generator=gen).half()
+    x[:, :, :2] = 0
+    wt = (torch.randn(cout, c, *kernel, generator=gen) * (c * kernel[0] ** 3) ** -0.5).half()
+    bias = (0.5 * torch.randn(cout, generator=gen)).half()
+    do, ho, wo = d - kernel[0] + 1, h - kernel[1] + 1, w - kernel[2] + 1
+    res = (torch.randn(b, cout, do, ho, wo, generator=gen) * 2).half().to(DEV).contiguous(
+        memory_format=torch.channels_last_3d)
+    xd = x.to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    wp = fc.pack_conv_weight_f16(wt.to(DEV))
+    with torch.inference_mode():
+        plain = fc.conv3d_f16(xd, wp, bias.to(DEV), list(kernel), [1, 1, 1], kernel[0] == 3)
+        fused = fc.conv3d_f16(xd, wp, bias.to(DEV), list(kernel), [1, 1, 1], kernel[0] == 3, res)
+        strided = fc.conv3d_f16(xd, wp, bias.to(DEV), list(kernel), [1, 1, 1], kernel[0] == 3, res.contiguous())
+        torch.cuda.synchronize()
+    assert torch.equal(fused, res + plain)
+    assert torch.equal(strided, fused)                           # an NCDHW residual is made channels-last first
+
+
 def test_conv3d_f16_implicit_gemm_causal_skip(fc):
     """Stride-1 convs outside the window kernel skip the zero depth taps per tile with the same values."""
     x, wt, bias = _operands(2, 64, 6, 10, 50, 64, True, seed=9)
