@@ -53,6 +53,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-configs", action="store_true", help="skip the per-config (BASELINE configs 1-4) kernel timings")
+    p.add_argument("--vs-torch", action="store_true",
+                   help="also time the model's F.conv3d (MIOpen) on the FP16 conv configs; its first call per shape "
+                        "runs MIOpen's solver search, which takes minutes")
+    p.add_argument("--configs-only", action="store_true",
+                   help="run only the per-config kernel timings and print them as JSON (for rocprofv3 kernel traces)")
     p.add_argument("--traffic-sample", action="store_true",
                    help="run only a 1 GiB elementwise copy and three stage-0 fused layers (for rocprofv3 --pmc)")
     p.add_argument("--enc-calls", type=int, default=ENC_CALLS, help=argparse.SUPPRESS)
@@ -252,7 +257,7 @@ def mfma_ceiling(torch, hip, wl, stream):
     }
 
 
-def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
+def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=False):
     """BASELINE.json configs 1-4 on their own shapes: mean kernel time and roofline fraction each.
 
     Every entry is timed with HIP events on the launch stream over `reps` launches after 3 warm-up
@@ -400,10 +405,10 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
         out["attention_h3_4x1797x32x64"] = attention_case(4, 1797, 32)
         out["attention_cfg4_1x16384x16x64"] = attention_case(1, 16384, 16)
 
-        # FP16 encoder convs outside the INT8 path (h3v_conv3d_f16) and the model's F.conv3d on the same padded
-        # channels-last operands (and on an NCDHW copy): suffix 3x3x3 convs of a staged batch of 4 clips after
-        # the producer (two causal zero frames per clip: the kernel skips those taps; flops count the dense
-        # reduction), the two prefix downsample convs and a nin_shortcut projection
+        # FP16 encoder convs outside the INT8 path (h3v_conv3d_f16; with --vs-torch also the model's F.conv3d on
+        # the same padded channels-last operands and on an NCDHW copy): suffix 3x3x3 convs of a staged batch of 4
+        # clips after the producer (two causal zero frames per clip: the kernel skips those taps; flops count the
+        # dense reduction), the two prefix downsample convs and a nin_shortcut projection
         def fp16_conv_case(b, cin, cout, dp, hp, wp, k, stride, causal):
             xs = randn(b, cin, dp, hp, wp).contiguous(memory_format=torch.channels_last_3d)
             if causal:
@@ -416,12 +421,13 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
                 memory_format=torch.channels_last_3d)
             t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), None, p(ys), b, cin, dp, hp, wp, cout, k, k,
                                      k, *stride, int(causal), stream))
-            t_t = timed(lambda: F.conv3d(xs, ws, bs, stride=stride))
-            xn = xs.contiguous()
-            t_n = timed(lambda: F.conv3d(xn, ws, bs, stride=stride))
             flops = 2 * b * do * ho * wo * cout * k ** 3 * cin
-            return {"h3v_conv3d_f16": fp16_mfma(t_c, flops), "torch_conv3d": fp16_mfma(t_t, flops),
-                    "torch_conv3d_ncdhw": fp16_mfma(t_n, flops)}
+            res = {"h3v_conv3d_f16": fp16_mfma(t_c, flops)}
+            if vs_torch:
+                res["torch_conv3d"] = fp16_mfma(timed(lambda: F.conv3d(xs, ws, bs, stride=stride)), flops)
+                xn = xs.contiguous()
+                res["torch_conv3d_ncdhw"] = fp16_mfma(timed(lambda: F.conv3d(xn, ws, bs, stride=stride)), flops)
+            return res
 
         out["suffix_conv_f16_4x256x9x64x64"] = fp16_conv_case(4, 256, 256, 11, 66, 66, 3, (1, 1, 1), True)
         out["suffix_conv_f16_4x512x5x32x32"] = fp16_conv_case(4, 512, 512, 7, 34, 34, 3, (1, 1, 1), True)
@@ -429,6 +435,23 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20):
         out["downsample0_f16_128x17x256x256_s122"] = fp16_conv_case(1, 128, 128, 19, 258, 258, 3, (1, 2, 2), False)
         out["downsample1_f16_256x17x128x128_s222"] = fp16_conv_case(1, 256, 256, 19, 129, 129, 3, (2, 2, 2), False)
         out["nin_shortcut_f16_128to256x17x128x128"] = fp16_conv_case(1, 128, 256, 17, 128, 128, 1, (1, 1, 1), False)
+
+        # conv_in 3 -> 128 of one clip: tap-folded pack (3x3 taps x 3 channels -> 32, reflect border, two causal
+        # zero frames) + the 3x1x1 conv over 32 channels; flops count the 81 real taps x channels
+        xin = randn(1, 3, 17, 256, 256).contiguous(memory_format=torch.channels_last_3d)
+        xf = torch.empty((1, 32, 19, 256, 256), device=dev, dtype=f16).contiguous(memory_format=torch.channels_last_3d)
+        wf = randn(128, 96, scale=81 ** -0.5)
+        bf = randn(128, scale=0.1)
+        yf = torch.empty((1, 128, 17, 256, 256), device=dev, dtype=f16).contiguous(memory_format=torch.channels_last_3d)
+
+        def conv_in():
+            call("h3v_tap_fold_pack", p(xin), p(xf), 1, 3, 17, 256, 256, 2, 32, stream)
+            call("h3v_conv3d_f16", p(xf), p(wf), p(bf), None, p(yf), 1, 32, 19, 256, 256, 128, 3, 1, 1, 1, 1, 1, 1,
+                 stream)
+
+        t_in = timed(conv_in)
+        out["conv_in_f16_3to128x17x256x256"] = {"tap_fold_pack_and_conv3d_f16":
+                                                fp16_mfma(t_in, 2 * 17 * 256 * 256 * 128 * 81)}
     torch.cuda.synchronize()
     return out
 
@@ -545,6 +568,10 @@ def main():
     stream = hip.stream(wl.dev)
     enc_calls, dec_calls = args.enc_calls, args.dec_calls
 
+    if args.configs_only:
+        print(json.dumps(config_measurements(torch, hip, kitchen, enc, stream, vs_torch=args.vs_torch)), flush=True)
+        return
+
     if args.traffic_sample:
         # Counter calibration + the dominant kernel in pipeline context.  FETCH_SIZE/WRITE_SIZE of the
         # copy (1 GiB read + 1 GiB written) give the counter's scale; the stage-0 conv launches follow
@@ -650,7 +677,7 @@ def main():
     result["mfma_ceiling"] = ceiling
     if not args.no_configs:
         log("timing BASELINE configs 1-4 on their own shapes")
-        result["configs"] = config_measurements(torch, hip, kitchen, enc, stream)
+        result["configs"] = config_measurements(torch, hip, kitchen, enc, stream, vs_torch=args.vs_torch)
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline sample")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
