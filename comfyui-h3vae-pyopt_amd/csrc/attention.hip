@@ -88,18 +88,51 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
         for (int kc = 0; kc < 4; ++kc) qf[kc] = *reinterpret_cast<const half8*>(src + 16 * kc);
     }
 
-    // cooperative K / V block loads: 64 keys x 8 chunks of 8 dims = 512 chunks, two per thread
-    u32x4 kreg[2], vreg[2];
+    // cooperative K / V block loads.  K: 64 keys x 8 chunks of 8 dims = 512 chunks, two per thread,
+    // consecutive threads walking a key row.  V: each thread reads a 4-key x 4-dim block (four
+    // 8-byte loads; 16 consecutive threads cover one 128-byte key row) and transposes it in
+    // registers, so the V^T rows go to LDS as four 8-byte stores of 4 consecutive keys each.
+    u32x4 kreg[2];
+    uint32_t vreg[4][2];                                  // [key of the 4][dims 0-1, 2-3]
+    const int vdg = tid & 15, vkg = tid >> 4;             // dims 4 vdg .. +3, keys 4 vkg .. +3
+    // Per-thread source rows of block 0; a full block adds the uniform kb0 * stride (scalar),
+    // only the last, partial block clamps rows past the end to the last token.
+    const uint16_t* kbase[2];
+    const uint16_t* vbase[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = tid + kThreads * i;
+        kbase[i] = p.k + (row0 + (c >> 3)) * p.k_ts + h * p.k_hs + 8 * (c & 7);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vbase[i] = p.v + (row0 + 4 * vkg + i) * p.v_ts + h * p.v_hs + 4 * vdg;
     auto load_block = [&](int kb0) {
+        if (kb0 + kBK <= n) {
+            const int64_t ko = (int64_t)kb0 * p.k_ts, vo = (int64_t)kb0 * p.v_ts;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) kreg[i] = *reinterpret_cast<const u32x4*>(kbase[i] + ko);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint2 w = *reinterpret_cast<const uint2*>(vbase[i] + vo);
+                vreg[i][0] = w.x;
+                vreg[i][1] = w.y;
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = tid + kThreads * i;
-            const int key = c >> 3, dch = c & 7;             // K: consecutive threads walk a key row
+            const int key = c >> 3, dch = c & 7;
             const int kr = kb0 + key < n ? kb0 + key : n - 1;
             kreg[i] = *reinterpret_cast<const u32x4*>(p.k + (row0 + kr) * p.k_ts + h * p.k_hs + 8 * dch);
-            const int vkey = c & 63, vdch = c >> 6;         // V: consecutive threads walk keys (transposed store)
-            const int vr = kb0 + vkey < n ? kb0 + vkey : n - 1;
-            vreg[i] = *reinterpret_cast<const u32x4*>(p.v + (row0 + vr) * p.v_ts + h * p.v_hs + 8 * vdch);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = 4 * vkg + i;
+            const int vr = kb0 + key < n ? kb0 + key : n - 1;
+            const uint2 w = *reinterpret_cast<const uint2*>(p.v + (row0 + vr) * p.v_ts + h * p.v_hs + 4 * vdg);
+            vreg[i][0] = w.x;
+            vreg[i][1] = w.y;
         }
     };
     auto store_block = [&]() {
@@ -108,13 +141,16 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
             const int c = tid + kThreads * i;
             const int key = c >> 3, dch = c & 7;
             *reinterpret_cast<u32x4*>(ks + key * kD + 8 * swz(key, dch)) = kreg[i];
-            const int vkey = c & 63, vdch = c >> 6;
+        }
+        // dim j of the 4: keys 0-1 from the low (j even) or high (j odd) halves of vreg[0..1][j >> 1],
+        // keys 2-3 likewise from vreg[2..3]; v_perm_b32 picks the two halves into one dword
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int d = 8 * vdch + e;
-                const uint32_t w = vreg[i][e >> 1];
-                vt[d * kBK + 8 * swz(d, vkey >> 3) + (vkey & 7)] = (uint16_t)(e & 1 ? w >> 16 : w & 0xffff);
-            }
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+            const uint32_t lo = __builtin_amdgcn_perm(vreg[1][j >> 1], vreg[0][j >> 1], sel);
+            const uint32_t hi = __builtin_amdgcn_perm(vreg[3][j >> 1], vreg[2][j >> 1], sel);
+            const int d = 4 * vdg + j;
+            *reinterpret_cast<uint2*>(vt + d * kBK + 8 * swz(d, vkg >> 1) + 4 * (vkg & 1)) = make_uint2(lo, hi);
         }
     };
 
