@@ -110,21 +110,28 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
             }
         }
     }
+    // From here on only fp16-rounded values are used (h_out = fp16(raw), then n = fp16(...)): the row
+    // is held as packed fp16, half the registers of fp32, so all rows of an H3 call are resident at once.
+    u16x8 hv[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) hv[c][e] = f2h(raw[c][e]);
     const float ss = row_tree<NCH>(part);
     const float inv = rsqrt_rn(ss / (float)K + eps);
     float amax = 0.0f;
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 512 + lane * 8;
-        float wv[8], hr[8];
+        float wv[8];
         load8f(w + col, wv);
+        *reinterpret_cast<u16x8*>(h_out + row * K + col) = hv[c];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            hr[e] = rt16(raw[c][e]);
-            raw[c][e] = rt16((hr[e] * inv) * wv[e]);
-            amax = __builtin_fmaxf(amax, __builtin_fabsf(raw[c][e]));
+            const float n = rt16((h2f(hv[c][e]) * inv) * wv[e]);
+            amax = __builtin_fmaxf(amax, __builtin_fabsf(n));
+            hv[c][e] = f2h(n);
         }
-        store8h(h_out + row * K + col, hr);
     }
     amax = wave_max(amax);
     const float sc = q1_scale(amax);
@@ -132,7 +139,9 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 512 + lane * 8;
-        const float* v = raw[c];
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = h2f(hv[c][e]);
         uint32_t lo = pack4(q1_quant(v[0], qd), q1_quant(v[1], qd), q1_quant(v[2], qd), q1_quant(v[3], qd));
         uint32_t hi = pack4(q1_quant(v[4], qd), q1_quant(v[5], qd), q1_quant(v[6], qd), q1_quant(v[7], qd));
         *reinterpret_cast<uint2*>(q + row * K + col) = make_uint2(lo, hi);
