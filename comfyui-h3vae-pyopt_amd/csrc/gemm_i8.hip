@@ -1194,11 +1194,17 @@ int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, c
     // implicit GEMM with channels and reduction counted in bytes
     p.C = cin * 2;
     p.K = p.K * 2;
+    // Cout > 128 with so few 256 x 256 tiles that even twice as many fit one round on the 256 CUs
+    // (the 16^2 suffix stage: 80 tiles): 256 x 128 tiles of eight 64 x 64 wave blocks.  At 144 tiles
+    // (the stride-2 downsample) the 288 smaller tiles need a second round and ran 35% slower.
+    const bool few = p.N > 128 && 2 * (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256) <= 256;
     if (p.C % 128 == 0) {
         if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        if (few) return launch_tiled<256, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
         return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
     }
     if (p.N <= 128) return launch_tiled<512, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
+    if (few) return launch_tiled<256, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
     return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
 }
 
