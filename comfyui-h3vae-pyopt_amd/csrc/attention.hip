@@ -78,6 +78,7 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
     const int64_t row0 = (int64_t)b * n;                 // first token row of this batch item
     const int qi = blockIdx.x * kBQ + wave * 32 + (lane & 31);
     const int hi = lane >> 5;                           // which 8 of a 16-wide k chunk this lane holds
+    const bool wave_active = blockIdx.x * kBQ + wave * 32 < n;   // wave-uniform
 
     // the wave's Q fragments: query qi, dims 16 kc + 8 hi .. + 7
     half8 qf[4];
@@ -168,6 +169,9 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
         store_block();
         __syncthreads();
         if (j + 1 < nblk) load_block(kb0 + kBK);          // next block in flight during this one
+        // a wave whose 32 queries all lie past the end (the last workgroup of a head) only helps
+        // with the shared K / V loads and barriers
+        if (!wave_active) continue;
 
         // S = K . Q^T for the 64 keys of the block (two 32-key halves)
         f32x16 s[2];
