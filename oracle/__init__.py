@@ -10,10 +10,10 @@ fused multiply-add).  This module loads the compiled library with ctypes and
 exposes numpy-facing wrappers.  FP16 arrays are passed as ``np.float16`` and
 reinterpreted as raw ``uint16`` bit patterns.
 
-Parity status per function (what pins it) is listed in DESIGN.md; every
-function here is checked by ``tests/test_oracle_*.py`` against the
+Every function here is pinned by ``tests/test_oracle_pins.py``: the
 reference's own known-answer vectors, closed forms, invariants or an
-independent float64 / integer computation.
+independent float64 / integer computation, chosen so that a dropped term, a
+wrong sign or index, or a transposed operand fails one of them.
 """
 from __future__ import annotations
 
