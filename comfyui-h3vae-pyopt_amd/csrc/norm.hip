@@ -90,6 +90,10 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
     if (row >= m) return;
     float raw[NCH][8];
     float part[NCH][2];
+    // the norm weight goes out with the row loads: no second round trip after the reduction
+    u16x8 wq[NCH];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) wq[c] = *reinterpret_cast<const u16x8*>(w + c * 512 + lane * 8);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 512 + lane * 8;
@@ -123,12 +127,10 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 512 + lane * 8;
-        float wv[8];
-        load8f(w + col, wv);
         *reinterpret_cast<u16x8*>(h_out + row * K + col) = hv[c];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float n = rt16((h2f(hv[c][e]) * inv) * wv[e]);
+            const float n = rt16((h2f(hv[c][e]) * inv) * h2f(wq[c][e]));
             amax = __builtin_fmaxf(amax, __builtin_fabsf(n));
             hv[c][e] = f2h(n);
         }
