@@ -127,6 +127,8 @@ GEMM_CASES = [
     (1, 32, 4, 9, 21, 96, (3, 3, 3), (1, 1, 1)),
     (3, 256, 4, 8, 8, 512, (1, 1, 1), (1, 1, 1)),          # nin_shortcut
     (1, 128, 3, 20, 20, 200, (3, 3, 3), (1, 1, 1)),
+    (1, 96, 4, 12, 12, 256, (3, 3, 3), (1, 1, 1)),          # 64-byte steps on 256 x 128 tiles (few tiles)
+    (1, 256, 3, 18, 18, 1024, (3, 3, 3), (1, 1, 1)),        # 16^2 width, Cout 1024 on 256 x 128 tiles
 ]
 
 
