@@ -10,8 +10,8 @@
 // strides (in elements; the 64 dims contiguous), so v can be the strided
 // slice of the QKV projection and q, k the QK-RoPE outputs, with no copies.
 //
-// One workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
-// 32 queries.  Keys and values stream in blocks of 64 through LDS:
+// One workgroup = 4 waves = 256 queries of one (batch, head); each wave owns
+// two sets of 32 queries.  Keys and values stream in blocks of 64 through LDS:
 //
 //   S = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = the wave's
 //                 Q fragments (registers, loaded once).  In the 32 x 32 result
@@ -40,8 +40,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 64;        // head dim
-constexpr int kBQ = 128;      // queries per workgroup
 constexpr int kBK = 64;       // keys per block
+// 32-query sets per wave: two share every K / V^T fragment read (246 VGPRs, 2 waves per SIMD);
+// one set (152 VGPRs, 3 waves per SIMD) measured 5% slower on the H3 shape, 11% on [1, 16384, 16, 64]
+constexpr int kQuerySets = 2;
 constexpr int kThreads = 256;
 
 struct AttnParams {
@@ -66,7 +68,11 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
 }
 
+// QS sets of 32 queries per wave (4 waves: 128 * QS queries per workgroup); every K and V^T
+// fragment read from LDS feeds the MFMAs of all QS sets.
+template <int QS>
 __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
+    constexpr int BQ = 128 * QS;
     __shared__ __attribute__((aligned(16))) uint16_t ks[kBK * kD];   // [key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kBK];   // [dim][key]
 
@@ -76,17 +82,19 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int n = p.tokens;
     const int64_t row0 = (int64_t)b * n;                 // first token row of this batch item
-    const int qi = blockIdx.x * kBQ + wave * 32 + (lane & 31);
+    const int q0 = blockIdx.x * BQ + wave * 32 * QS;   // the wave's first query
     const int hi = lane >> 5;                           // which 8 of a 16-wide k chunk this lane holds
-    const bool wave_active = blockIdx.x * kBQ + wave * 32 < n;   // wave-uniform
+    const bool wave_active = q0 < n;                    // wave-uniform
 
-    // the wave's Q fragments: query qi, dims 16 kc + 8 hi .. + 7
-    half8 qf[4];
-    {
+    // the wave's Q fragments: query q0 + 32 qs + lane % 32, dims 16 kc + 8 hi .. + 7
+    half8 qf[QS][4];
+#pragma unroll
+    for (int qs = 0; qs < QS; ++qs) {
+        const int qi = q0 + 32 * qs + (lane & 31);
         const int qr = qi < n ? qi : n - 1;
         const uint16_t* src = p.q + (row0 + qr) * p.q_ts + h * p.q_hs + 8 * hi;
 #pragma unroll
-        for (int kc = 0; kc < 4; ++kc) qf[kc] = *reinterpret_cast<const half8*>(src + 16 * kc);
+        for (int kc = 0; kc < 4; ++kc) qf[qs][kc] = *reinterpret_cast<const half8*>(src + 16 * kc);
     }
 
     // cooperative K / V block loads.  K: 64 keys x 8 chunks of 8 dims = 512 chunks, two per thread,
@@ -155,11 +163,15 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
         }
     };
 
-    f32x16 oacc[2];
+    f32x16 oacc[QS][2];
+    float m_run[QS], l_run[QS];
 #pragma unroll
-    for (int db = 0; db < 2; ++db) oacc[db] = f32x16{};
-    float m_run = -__builtin_inff();
-    float l_run = 0.0f;
+    for (int qs = 0; qs < QS; ++qs) {
+        oacc[qs][0] = f32x16{};
+        oacc[qs][1] = f32x16{};
+        m_run[qs] = -__builtin_inff();
+        l_run[qs] = 0.0f;
+    }
 
     const int nblk = (n + kBK - 1) / kBK;
     load_block(0);
@@ -173,97 +185,117 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
         // with the shared K / V loads and barriers
         if (!wave_active) continue;
 
-        // S = K . Q^T for the 64 keys of the block (two 32-key halves)
-        f32x16 s[2];
+        // S = K . Q^T for the 64 keys of the block (two 32-key halves), each K fragment used by every set
+        f32x16 s[QS][2];
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-            s[kh] = f32x16{};
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) s[qs][kh] = f32x16{};
             const int row = 32 * kh + (lane & 31);
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
                 const half8 a = *reinterpret_cast<const half8*>(ks + row * kD + 8 * swz(row, 2 * kc + hi));
-                s[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[kc], s[kh], 0, 0, 0);
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs)
+                    s[qs][kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qs][kc], s[qs][kh], 0, 0, 0);
             }
         }
         // keys past the end (last block only): -inf
         if (kb0 + kBK > n) {
 #pragma unroll
+            for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int key = kb0 + 32 * kh + 8 * (r >> 2) + 4 * hi + (r & 3);
+                        if (key >= n) s[qs][kh][r] = -__builtin_inff();
+                    }
+        }
+        // online softmax per set (raw-score units; the exponent folds in scale * log2 e); P in fp16
+        uint32_t pk[QS][2][8];                            // [set][half][g * 2 + dword]
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+            float mloc = s[qs][0][0];
+#pragma unroll
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = kb0 + 32 * kh + 8 * (r >> 2) + 4 * hi + (r & 3);
-                    if (key >= n) s[kh][r] = -__builtin_inff();
+                for (int r = 0; r < 16; ++r) mloc = __builtin_fmaxf(mloc, s[qs][kh][r]);
+            const float m_new = __builtin_fmaxf(m_run[qs], wave_pair_max(mloc));
+            const float alpha = __builtin_amdgcn_exp2f((m_run[qs] - m_new) * p.c);
+            const float mc = m_new * p.c;
+            m_run[qs] = m_new;
+            float lsum = 0.0f;
+#pragma unroll
+            for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float e4[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qs][kh][4 * g + e], p.c, -mc));
+                    pk[qs][kh][2 * g] = pack_f16x2(e4[0], e4[1]);
+                    pk[qs][kh][2 * g + 1] = pack_f16x2(e4[2], e4[3]);
+                    // the row sum adds the fp16 weights the P.V product uses, two per v_dot2_f32_f16
+                    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+                    lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[qs][kh][2 * g]), one, lsum, false);
+                    lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[qs][kh][2 * g + 1]), one, lsum, false);
                 }
-        }
-        // online softmax (raw-score units; the exponent folds in scale * log2 e)
-        float mloc = s[0][0];
+            l_run[qs] = l_run[qs] * alpha + lsum;
+            // alpha is exactly 1 where the running maximum did not move; skip the rescale
+            // when that holds for every lane (most blocks once the maximum has settled)
+            if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
+                for (int db = 0; db < 2; ++db)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) mloc = __builtin_fmaxf(mloc, s[kh][r]);
-        const float m_new = __builtin_fmaxf(m_run, wave_pair_max(mloc));
-        const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * p.c);
-        const float mc = m_new * p.c;
-        m_run = m_new;
-        float lsum = 0.0f;
-        uint32_t pk[2][8];                                // P in fp16: [half][g * 2 + dword]
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float e4[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kh][4 * g + e], p.c, -mc));
-                pk[kh][2 * g] = pack_f16x2(e4[0], e4[1]);
-                pk[kh][2 * g + 1] = pack_f16x2(e4[2], e4[3]);
-                // the row sum adds the fp16 weights the P.V product uses, two per v_dot2_f32_f16
-                const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
-                lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[kh][2 * g]), one, lsum, false);
-                lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[kh][2 * g + 1]), one, lsum, false);
+                    for (int r = 0; r < 16; ++r) oacc[qs][db][r] *= alpha;
             }
-        l_run = l_run * alpha + lsum;
-        // alpha is exactly 1 where the running maximum did not move; skip the rescale
-        // when that holds for every lane (most blocks once the maximum has settled)
-        if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-            for (int db = 0; db < 2; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
         }
 
-        // O^T += V^T . P^T over four 16-key chunks
+        // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int kh = c >> 1, g0 = 2 * (c & 1);
             // lane < 32 needs keys 16c + 0..7 (its own group g0 + the partner's), lane >= 32
             // keys 16c + 8..15 (the partner's group g0 + 1 + its own)
-            const auto x0 = __builtin_amdgcn_permlane32_swap(pk[kh][2 * g0], pk[kh][2 * g0 + 2], false, false);
-            const auto x1 = __builtin_amdgcn_permlane32_swap(pk[kh][2 * g0 + 1], pk[kh][2 * g0 + 3], false, false);
-            const u32x4 bw = {x0[0], x1[0], x0[1], x1[1]};
-            const half8 bop = __builtin_bit_cast(half8, bw);
+            half8 bop[QS];
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+                const auto x0 = __builtin_amdgcn_permlane32_swap(pk[qs][kh][2 * g0], pk[qs][kh][2 * g0 + 2], false, false);
+                const auto x1 = __builtin_amdgcn_permlane32_swap(pk[qs][kh][2 * g0 + 1], pk[qs][kh][2 * g0 + 3], false,
+                                                                 false);
+                const u32x4 bw = {x0[0], x1[0], x0[1], x1[1]};
+                bop[qs] = __builtin_bit_cast(half8, bw);
+            }
 #pragma unroll
             for (int db = 0; db < 2; ++db) {
                 const int row = 32 * db + (lane & 31);
                 const half8 a = *reinterpret_cast<const half8*>(vt + row * kBK + 8 * swz(row, 2 * c + hi));
-                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop, oacc[db], 0, 0, 0);
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs)
+                    oacc[qs][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop[qs], oacc[qs][db], 0, 0, 0);
             }
         }
     }
 
-    // normalise and store: lane l holds query qi, dims 32 db + 8 g + 4 hi + e
-    const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
-    const float inv = 1.0f / l_tot;
-    if (qi < n) {
-        uint16_t* dst = p.o + (row0 + qi) * p.o_ts + h * p.o_hs + 4 * hi;
+    // normalise and store: lane l holds query q0 + 32 qs + l % 32, dims 32 db + 8 g + 4 hi + e
 #pragma unroll
-        for (int db = 0; db < 2; ++db)
+    for (int qs = 0; qs < QS; ++qs) {
+        const int qi = q0 + 32 * qs + (lane & 31);
+        const float l_tot = l_run[qs] + __shfl_xor(l_run[qs], 32, 64);
+        const float inv = 1.0f / l_tot;
+        if (qi < n) {
+            uint16_t* dst = p.o + (row0 + qi) * p.o_ts + h * p.o_hs + 4 * hi;
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                u16x4 v;
+            for (int db = 0; db < 2; ++db)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = f2h(oacc[db][4 * g + e] * inv);
-                *reinterpret_cast<u16x4*>(dst + 32 * db + 8 * g) = v;
-            }
+                for (int g = 0; g < 4; ++g) {
+                    u16x4 v;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] = f2h(oacc[qs][db][4 * g + e] * inv);
+                    *reinterpret_cast<u16x4*>(dst + 32 * db + 8 * g) = v;
+                }
+        }
     }
 }
 
@@ -297,7 +329,8 @@ extern "C" int h3v_attention_d64(const uint16_t* q, int64_t q_token_stride, int6
     p.o_ts = o_token_stride; p.o_hs = o_head_stride;
     p.tokens = (int)tokens;
     p.c = scale * 1.4426950408889634f;
-    dim3 grid((unsigned)((tokens + kBQ - 1) / kBQ), (unsigned)heads, (unsigned)batch);
-    hipLaunchKernelGGL(fmha_d64, grid, dim3(kThreads), 0, stream, p);
+    constexpr int QS = kQuerySets;
+    dim3 grid((unsigned)((tokens + 128 * QS - 1) / (128 * QS)), (unsigned)heads, (unsigned)batch);
+    hipLaunchKernelGGL(fmha_d64<QS>, grid, dim3(kThreads), 0, stream, p);
     return launch_status(what);
 }
