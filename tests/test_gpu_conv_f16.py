@@ -147,7 +147,8 @@ def test_conv3d_f16_implicit_gemm_matches_float64(fc, b, c, d, h, w, cout, kerne
 
 
 @pytest.mark.parametrize("b,c,d,h,w,cout,kernel", [(2, 64, 5, 10, 66, 128, (3, 3, 3)), (1, 64, 4, 10, 50, 96, (3, 3, 3)),
-                                                   (3, 256, 4, 8, 8, 256, (1, 1, 1))])
+                                                   (3, 256, 4, 8, 8, 256, (1, 1, 1)),
+                                                   (1, 64, 4, 10, 50, 100, (3, 3, 3))])   # scalar output rows
 def test_conv3d_f16_residual_equals_separate_add(fc, b, c, d, h, w, cout, kernel):
     """The fused residual (window kernel, implicit GEMM, 1x1x1) == the conv followed by torch's fp16 add."""
     gen = torch.Generator().manual_seed(c + cout + d)
