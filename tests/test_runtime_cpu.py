@@ -363,3 +363,34 @@ def test_build_comfy_vae_configuration(rt, monkeypatch):
     assert fp.working_dtypes == [torch.float16, torch.float32]
     assert math.isclose(vae.memory_used_decode((1, 24, 1, 1, 1), torch.float16),
                         int(1000 + (3 * 1 * 16 * 16 * 2 * 2.5 + 1_100_000_000) * 1.1))
+
+
+def test_encoder_wiring_on_a_reconstructed_core(rt, pkg):
+    """The runtime's encoder wiring (reference h3vae_runtime.py:389-395, plus conv_in): conv_in and
+    down.0.downsample.conv through the internal-padding wrapper, the bias-fused prefix with the residual
+    pack downsample, and the clip-batched fused suffix over every suffix stage."""
+    import h3_arch
+    import torch.nn as nn
+
+    class _Core(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.encoder = h3_arch.H3Encoder()
+            self.quant_conv = nn.Conv3d(48, 48, 1)
+            self.decoder = h3_arch.H3Decoder(dim=128, hidden=256, depth=1)
+            self.clip_length, self.token_drop, self.vae_ratio, self.tile_overlap_min = 17, 3, 16, 64
+            self.tile_size, self.decoder_tile_size, self.stack_tiling = 672, 256, False
+
+        def _run_tile_tasks(self, *args, **kwargs):
+            raise AssertionError("not called")
+
+    config = {"latents_mean": [0.0] * 24, "latents_std": [1.0] * 24}
+    runtime = rt.H3VAEPyOptRuntime(device="cpu", dtype=torch.float32, log_calls=False, core=_Core().eval(),
+                                   config=config)
+    assert type(runtime.prefix.conv_in).__name__ == "ImplicitTemporalPadConv3d"
+    assert type(runtime.prefix.stages[0].downsample.conv).__name__ == "ImplicitTemporalPadConv3d"
+    assert [type(b).__name__ for b in runtime.prefix.stages[0].block] == ["BiasFusedResidualBlock"] * 2
+    assert type(runtime.prefix.stages[1].block[-1]).__name__ == "ResidualDownsampleBlock"
+    assert type(runtime.suffix).__name__ == "BatchedSuffix"
+    assert type(runtime.suffix.stages[0].block[0]).__name__ == "BatchedResidualBlock"
+    assert runtime.suffix.final is not None
