@@ -10,7 +10,7 @@
 // strides (in elements; the 64 dims contiguous), so v can be the strided
 // slice of the QKV projection and q, k the QK-RoPE outputs, with no copies.
 //
-// One workgroup = 4 waves = 256 queries of one (batch, head); each wave owns
+// One workgroup = 8 waves = 512 queries of one (batch, head); each wave owns
 // two sets of 32 queries.  Keys and values stream in blocks of 64 through LDS:
 //
 //   S = K . Q^T   v_mfma_f32_32x32x16_f16, A = K rows from LDS, B = the wave's
@@ -44,7 +44,7 @@ constexpr int kBK = 64;       // keys per block
 // 32-query sets per wave: two share every K / V^T fragment read (246 VGPRs, 2 waves per SIMD);
 // one set (152 VGPRs, 3 waves per SIMD) measured 5% slower on the H3 shape, 11% on [1, 16384, 16, 64]
 constexpr int kQuerySets = 2;
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;   // the K / V loading threads (waves 0-3); a workgroup has 8 waves
 
 struct AttnParams {
     const uint16_t* q;
@@ -68,11 +68,12 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
 }
 
-// QS sets of 32 queries per wave (4 waves: 128 * QS queries per workgroup); every K and V^T
-// fragment read from LDS feeds the MFMAs of all QS sets.
+// QS sets of 32 queries per wave, 8 waves (256 * QS queries per workgroup); every K and V^T
+// fragment read from LDS feeds the MFMAs of all QS sets.  Waves 0-3 move each K / V block
+// into LDS for all 8 (half the per-query load and transpose work of 4-wave workgroups).
 template <int QS>
-__global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
-    constexpr int BQ = 128 * QS;
+__global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
+    constexpr int BQ = 256 * QS;
     __shared__ __attribute__((aligned(16))) uint16_t ks[kBK * kD];   // [key][dim]
     __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kBK];   // [dim][key]
 
@@ -174,13 +175,14 @@ __global__ __launch_bounds__(kThreads) void fmha_d64(AttnParams p) {
     }
 
     const int nblk = (n + kBK - 1) / kBK;
-    load_block(0);
+    const bool loader = tid < kThreads;                   // waves 0-3 (wave-uniform)
+    if (loader) load_block(0);
     for (int j = 0; j < nblk; ++j) {
         const int kb0 = j * kBK;
         __syncthreads();                                  // every wave is done with the previous block
-        store_block();
+        if (loader) store_block();
         __syncthreads();
-        if (j + 1 < nblk) load_block(kb0 + kBK);          // next block in flight during this one
+        if (loader && j + 1 < nblk) load_block(kb0 + kBK);   // next block in flight during this one
         // a wave whose 32 queries all lie past the end (the last workgroup of a head) only helps
         // with the shared K / V loads and barriers
         if (!wave_active) continue;
@@ -330,7 +332,7 @@ extern "C" int h3v_attention_d64(const uint16_t* q, int64_t q_token_stride, int6
     p.tokens = (int)tokens;
     p.c = scale * 1.4426950408889634f;
     constexpr int QS = kQuerySets;
-    dim3 grid((unsigned)((tokens + 128 * QS - 1) / (128 * QS)), (unsigned)heads, (unsigned)batch);
-    hipLaunchKernelGGL(fmha_d64<QS>, grid, dim3(kThreads), 0, stream, p);
+    dim3 grid((unsigned)((tokens + 256 * QS - 1) / (256 * QS)), (unsigned)heads, (unsigned)batch);
+    hipLaunchKernelGGL(fmha_d64<QS>, grid, dim3(2 * kThreads), 0, stream, p);
     return launch_status(what);
 }
