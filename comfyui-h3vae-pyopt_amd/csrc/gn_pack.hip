@@ -39,6 +39,22 @@
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
+#include <mutex>
+
+// ---------------------------------------------------------------------------
+// Static scratch of h3v_gn_norm_pack_i8_noalloc, for callers that cannot
+// allocate device memory.  Each GPU holds its own copy of this array for the
+// life of the process (4 MiB + 256 bytes): 64 head floats (word 0 is the absmax
+// key) then the workspace, which covers every [D, H, W] whose
+// workspace_floats() fits (at 256 x 256 frames up to D = 61).  Every call on a
+// GPU reuses that GPU's copy; gn_init clears the keys each call, so nothing
+// carries over, but calls that overlap on one GPU (two streams, two threads)
+// race on it.  The name `scratch` is a host-side stand-in: host code uses only
+// the device address hipGetSymbolAddress returns, looked up once per device.
+constexpr int64_t kScratchHeadFloats = 64;
+constexpr int64_t kScratchWorkspaceFloats = (int64_t)1 << 20;
+static __device__ __align__(256) float scratch[kScratchHeadFloats + kScratchWorkspaceFloats];
+
 namespace h3v {
 namespace {
 
@@ -683,6 +699,53 @@ void launch_f16(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
                        beta, stats, d, h, w, y);
 }
 
+
+// ---------------------------------------------------------------------------
+// Checks and launch shared by h3v_gn_norm_pack_i8 and its no-allocation variant.
+int run_norm_pack_i8(const char* what, const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
+                     const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
+                     float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
+    H3V_REQUIRE(x && gamma && beta && q && scale && stats, "%s: null pointer argument", what);
+    H3V_REQUIRE(c == 128 || c == 256, "%s: C must be 128 or 256 (got %d)", what, c);
+    H3V_REQUIRE(d >= 1 && h >= 2 && w >= 2, "%s: requires D >= 1 and H, W >= 2", what);
+    H3V_REQUIRE((int64_t)c * (d + 2) * (h + 2) * (w + 2) < ((int64_t)1 << 31), "%s: padded output exceeds int32 index range",
+                what);
+    H3V_REQUIRE(eps > 0.0f, "%s: eps must be positive", what);
+    H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(beta, 16) && (!pre_bias || aligned(pre_bias, 16)) &&
+                    aligned(q, 8),
+                "%s: x, gamma, beta, pre_bias need 16-byte and q 8-byte alignment", what);
+    if (c == 128) {
+        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+    } else {
+        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+    }
+    return launch_status(what);
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(const char* what, float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(H3V_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+    H3V_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device index %d out of range", what, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p)
+            return fail(H3V_ELAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                        hipGetErrorString(e));
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return H3V_OK;
+}
+
 }  // namespace
 }  // namespace h3v
 
@@ -699,24 +762,28 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
                         float eps, int c, int d, int h, int w, int8_t* q, float* scale, float* stats,
                         float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
     const char* what = "h3v_gn_norm_pack_i8";
-    H3V_REQUIRE(x && gamma && beta && q && scale && stats && workspace && amax_scratch, "%s: null pointer argument",
-                what);
-    H3V_REQUIRE(c == 128 || c == 256, "%s: C must be 128 or 256 (got %d)", what, c);
+    H3V_REQUIRE(workspace && amax_scratch, "%s: null pointer argument", what);
+    H3V_REQUIRE(aligned(workspace, 16), "%s: workspace needs 16-byte alignment", what);
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, q, scale, stats, workspace, amax_scratch,
+                            stream);
+}
+
+int h3v_gn_norm_pack_i8_noalloc(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
+                                const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
+                                float* stats, hipStream_t stream) {
+    const char* what = "h3v_gn_norm_pack_i8_noalloc";
     H3V_REQUIRE(d >= 1 && h >= 2 && w >= 2, "%s: requires D >= 1 and H, W >= 2", what);
-    H3V_REQUIRE((int64_t)c * (d + 2) * (h + 2) * (w + 2) < ((int64_t)1 << 31), "%s: padded output exceeds int32 index range",
-                what);
-    H3V_REQUIRE(eps > 0.0f, "%s: eps must be positive", what);
-    H3V_REQUIRE(aligned(x, 16) && aligned(gamma, 16) && aligned(beta, 16) && (!pre_bias || aligned(pre_bias, 16)) &&
-                    aligned(q, 8) && aligned(workspace, 16),
-                "%s: x, gamma, beta, pre_bias, workspace need 16-byte and q 8-byte alignment", what);
-    if (c == 128) {
-        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
-        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
-    } else {
-        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
-        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
-    }
-    return launch_status(what);
+    const int64_t need = workspace_floats(d, h, w);
+    H3V_REQUIRE(need <= kScratchWorkspaceFloats,
+                "%s: [D=%d, H=%d, W=%d] needs %lld workspace floats; the static scratch holds %lld "
+                "(use h3v_gn_norm_pack_i8 with a caller workspace)",
+                what, d, h, w, (long long)need, (long long)kScratchWorkspaceFloats);
+    float* base = nullptr;
+    const int rc = scratch_for_current_device(what, &base);
+    if (rc != H3V_OK) return rc;
+    // word 0: the absmax key; the workspace starts 256 bytes in (16-byte alignment kept)
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, q, scale, stats,
+                            base + kScratchHeadFloats, reinterpret_cast<uint32_t*>(base), stream);
 }
 
 int64_t h3v_gn_norm_pack_f16_workspace_floats(int batch, int c, int d, int h, int w) {

@@ -213,6 +213,21 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
                         float eps, int c, int d, int h, int w, int8_t* q, float* scale, float* stats,
                         float* workspace, uint32_t* amax_scratch, hipStream_t stream);
 
+/* h3v_gn_norm_pack_i8 without a workspace argument and without allocating:
+ * no counterpart in the reference.  It is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The workspace and the absmax word live in a static
+ * device array of the library, one per GPU, 4 MiB + 256 bytes, held until the
+ * process ends; a call whose h3v_gn_norm_pack_workspace_floats(d, h, w)
+ * exceeds 1048576 floats is rejected with H3V_EINVAL (256 x 256 frames: up to
+ * d = 61).  The array of the current device is used, so `stream` must belong
+ * to it.  Every call on one GPU shares that array; calls that overlap on one
+ * GPU (two streams or threads) race.  Same inputs, outputs and results as
+ * h3v_gn_norm_pack_i8. */
+int h3v_gn_norm_pack_i8_noalloc(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
+                                const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
+                                float* stats, hipStream_t stream);
+
 /* ---- decoder row producers (row width k in {1024, 2048, 4096}) ---------
  * norm1: raw = fma(o, g, h); h_out = fp16(raw) (h_out may equal h: in place);
  * ss = published W16 tree of raw^2; inv = 1/sqrt(ss/k + eps);
