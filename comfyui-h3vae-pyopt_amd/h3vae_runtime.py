@@ -179,6 +179,105 @@ def _load_weights(core, weights_path: str):
         logger.info("[H3VAE-PyOpt] ignored non-model buffer keys: %s", sorted(unexpected))
 
 
+# ---- planning and stitching of spatial tiles ------------------------------------------------------------
+
+def axis_tiles(length, tile, overlap_min, step):
+    """Starts, lengths and overlaps of the tiles that cover one axis of ``length`` pixels.
+
+    The fewest tiles of ``tile`` pixels whose overlaps are all at least ``overlap_min`` (n tiles
+    cover n * tile - (n - 1) * overlap_min pixels); the surplus coverage is handed out in ``step``
+    pixel units, one unit per overlap in turn from the first.  One tile if it already covers the axis.
+    """
+    if tile <= overlap_min:
+        raise ValueError("encoder tile must exceed its minimum overlap")
+    if tile >= length:
+        return [0], [length], []
+    count = -(-(length - overlap_min) // (tile - overlap_min))
+    units = (count * tile - (count - 1) * overlap_min - length) // step
+    each, extra = divmod(units, count - 1)
+    overlaps = [overlap_min + step * (each + (k < extra)) for k in range(count - 1)]
+    starts = [0]
+    for overlap in overlaps:
+        starts.append(starts[-1] + tile - overlap)
+    return starts, [tile] * count, overlaps
+
+
+def stitch_tiles(grid, y_overlaps, x_overlaps, blend):
+    """Row-major grid of equally shaped tiles [..., h, w] -> one tensor.
+
+    Each tile is cross-faded with the untouched tile above it over their vertical overlap, then
+    with the untouched tile to its left over their horizontal overlap (``blend``); the part it
+    shares with the tile below / to the right is cut, and the rest is placed on the canvas."""
+    rows, cols = len(grid), len(grid[0])
+    keep_h = [grid[i][0].shape[-2] - (y_overlaps[i] if i < rows - 1 else 0) for i in range(rows)]
+    keep_w = [grid[0][j].shape[-1] - (x_overlaps[j] if j < cols - 1 else 0) for j in range(cols)]
+    canvas = grid[0][0].new_empty((*grid[0][0].shape[:-2], sum(keep_h), sum(keep_w)))
+    top = 0
+    for i in range(rows):
+        left = 0
+        for j in range(cols):
+            tile = grid[i][j]
+            if i:
+                tile = blend(grid[i - 1][j], tile, y_overlaps[i - 1], dim=-2)
+            if j:
+                tile = blend(grid[i][j - 1], tile, x_overlaps[j - 1], dim=-1)
+            canvas[..., top:top + keep_h[i], left:left + keep_w[j]] = tile[..., :keep_h[i], :keep_w[j]]
+            left += keep_w[j]
+        top += keep_h[i]
+    return canvas
+
+
+class _TileBatcher:
+    """Replacement for the core's ``_run_tile_tasks``: decoder tiles go through ``forward_fn`` in
+    groups of ``batch`` (0: 1 or 2 by free GPU memory).  Anything it does not batch (class-token
+    aggregation, batch > 1 or non-24-channel tiles, autograd) goes to the core's own routine."""
+
+    RESERVE = 12 * 1024 ** 3      # kept free for the decoded video and other GPU users
+    PER_TILE = 4 * 1024 ** 3
+
+    def __init__(self, core, own, batch):
+        self.core, self.own, self.batch = core, own, int(batch)
+
+    def _group_size(self, device):
+        if self.batch:
+            return self.batch
+        free, _ = torch.cuda.mem_get_info(device)
+        return max(1, min(2, (free - self.RESERVE) // self.PER_TILE))
+
+    def __call__(self, tiles, indices, forward_fn, stack_tiling, cls_agg=None):
+        plain = bool(tiles) and tiles[0].shape[0] == 1 and tiles[0].shape[1] == 24
+        if cls_agg is not None or not plain or torch.is_grad_enabled():
+            return self.own(tiles, indices, forward_fn, stack_tiling, cls_agg)
+        size = self._group_size(tiles[0].device)
+        self.core._last_tile_batch = size
+        if size == 1:
+            return self.own(tiles, indices, forward_fn, stack_tiling, cls_agg)
+        results = []
+        for first in range(0, len(indices), size):
+            group = [tiles[i] for i in indices[first:first + size]]
+            results += list(forward_fn(torch.cat(group, dim=0)).split(1, dim=0))
+        return results
+
+
+class _CallTimer:
+    """Wall time of encode / decode calls with a running mean (logged when ``log_calls`` is on)."""
+
+    def __init__(self):
+        self.count, self.total_ms = {"encode": 0, "decode": 0}, {"encode": 0.0, "decode": 0.0}
+
+    def reset(self):
+        self.__init__()
+
+    def record(self, kind, started, device):
+        if device.type == "cuda":
+            torch.cuda.synchronize(device)
+        ms = (time.monotonic() - started) * 1e3
+        self.count[kind] += 1
+        self.total_ms[kind] += ms
+        logger.info("[H3VAE-PyOpt] %s #%d: %.1f ms (running mean %.1f ms)", kind, self.count[kind], ms,
+                    self.total_ms[kind] / self.count[kind])
+
+
 class H3VAEPyOptRuntime(torch.nn.Module):
     """ComfyUI first_stage_model over the gfx950 hot path."""
 
@@ -202,13 +301,6 @@ class H3VAEPyOptRuntime(torch.nn.Module):
             raise ValueError("encoder_tile_size must be 0 (auto) or a positive multiple of 16")
         if int(tile_batch) < 0:
             raise ValueError("tile_batch must be non-negative")
-        from .opt.decoder_fused_qk_rope import clone_with_qk_fusion
-        from .opt.encoder_fused_norm_next import next_fused_prefix
-        from .opt.encoder_internal_padding import replace_selected
-        from .opt.encoder_fused_batched_norm import fused_suffix
-        from .opt.encoder_staged_batch import encode_staged
-        self._encode_staged = encode_staged
-
         if core is None:
             core, config = _load_klvae_core(model_code_dir)
             if encoder_tile_size and encoder_tile_size <= core.tile_overlap_min:
@@ -217,258 +309,204 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         elif config is None:
             raise ValueError("a prebuilt core needs its config (latents_mean / latents_std)")
         core.to(device=device, dtype=dtype)
-        self.core = core
-        self.config = config
+        self.core, self.config = core, config
         self.encoder_tile_size = int(encoder_tile_size)
         core.tile_size = self.encoder_tile_size or 672
-
-        # ---- decoder -------------------------------------------------------------------------------
-        new_dec = clone_with_qk_fusion(core.decoder, qk_rows)
-        if int8_decode:
-            from .opt.kitchen_int8 import install_kitchen_int8_ffn
-            try:
-                count = install_kitchen_int8_ffn(new_dec, mode="INT8both", require_cuda=True)
-            except Exception as exc:  # noqa: BLE001 - an explicit option has no fallback
-                raise RuntimeError("int8_decode installation failed; no fallback was applied") from exc
-            logger.info("[H3VAE-PyOpt] INT8 FFNs: %d", count)
-            if decode_fusions:
-                from .opt.int8_attention_out import from_raw_decoder
-                from .opt.int8_norm1_quant import clone_norm1_quant_decoder, supports_norm1_quant
-                new_dec = from_raw_decoder(new_dec, warps=8)
-                if supports_norm1_quant(device) and not getattr(new_dec, "spatial_parallel", False):
-                    new_dec = clone_norm1_quant_decoder(new_dec, enabled=True)
-        core.decoder = new_dec
-        core.decoder_tile_size = int(decoder_tile_size)
-        core.stack_tiling = False
-        if int(tile_batch) == 0 or int(tile_batch) > 1:
-            self._install_batched_tiles(core, int(tile_batch))
-
-        # ---- encoder -------------------------------------------------------------------------------
-        enc = core.encoder.to(memory_format=torch.channels_last_3d)
-        quant = core.quant_conv.to(memory_format=torch.channels_last_3d)
-        replace_selected(enc, ["down.0.downsample.conv"])
-        try:
-            # conv_in (3 channels) through the tap-folded native conv; a conv_in that is not a causal
-            # reflect-padded CausalConv3d stays the model's
-            replace_selected(enc, ["conv_in"])
-        except ValueError:
-            pass
-        prefix = next_fused_prefix(enc, "extend_bias_pack")
-        suffix = fused_suffix(enc, quant, all_stages=True)
-        metadata = None
-        if int8_encode:
-            from .opt.encoder_int8_integration import install_int8_encoder_prefix
-            try:
-                metadata = install_int8_encoder_prefix(prefix, require_cuda=True, tile_variant="auto")
-            except Exception as exc:  # noqa: BLE001 - an explicit option has no fallback
-                raise RuntimeError("int8_encode installation failed; no fallback was applied") from exc
-            logger.info("[H3VAE-PyOpt] INT8 encoder convolutions: %d", metadata["count"])
-        self.prefix, self.suffix = prefix, suffix
         self.encoder_staged_batch = int(encoder_staged_batch)
-        self.fast_linear = bool(fast_linear)
+        self.fast_linear = False
         self.int8_decode, self.int8_encode = int8_decode, int8_encode
         self.decode_fusions = bool(decode_fusions)
         self.compile_decoder, self.compile_encoder = bool(compile_decoder), bool(compile_encoder)
-        self.int8_encoder_metadata = metadata
-
-        # ---- normalisation constants ---------------------------------------------------------------
-        self.latents_mean = torch.tensor(config["latents_mean"], dtype=dtype, device=device).view(1, -1, 1, 1, 1)
-        self.latents_std = torch.tensor(config["latents_std"], dtype=dtype, device=device).view(1, -1, 1, 1, 1)
+        if self.compile_decoder or self.compile_encoder:
+            logger.debug("[H3VAE-PyOpt] compile_decoder / compile_encoder are accepted but not used: the hot "
+                         "operators are hand-written kernels, nothing is traced")
+        self._wire_decoder(core, qk_rows, int(decoder_tile_size), int(tile_batch), device)
+        self._wire_encoder(core)
+        stats = {name: torch.tensor(config[name], dtype=dtype, device=device).view(1, -1, 1, 1, 1)
+                 for name in ("latents_mean", "latents_std")}
+        self.latents_mean, self.latents_std = stats["latents_mean"], stats["latents_std"]
         self._img_mean = torch.tensor(_IMG_MEAN, dtype=torch.float32, device=device).view(1, 3, 1, 1, 1)
         self._img_std = torch.tensor(_IMG_STD, dtype=torch.float32, device=device).view(1, 3, 1, 1, 1)
-
         self.log_calls = bool(log_calls)
-        self._dec_calls, self._dec_total_ms = 0, 0.0
-        self._enc_calls, self._enc_total_ms = 0, 0.0
+        self._timer = _CallTimer()
         logger.info("[H3VAE-PyOpt] runtime ready: decoder_tile=%d encoder_tile=%s tile_batch=%d staged_batch=%d "
                     "int8_decode=%s int8_encode=%s decode_fusions=%s", core.decoder_tile_size,
                     self.encoder_tile_size or "auto", tile_batch, self.encoder_staged_batch, self.int8_decode,
                     self.int8_encode, self.decode_fusions)
 
-    # ---- helpers ------------------------------------------------------------------------------------
+    # ---- wiring ---------------------------------------------------------------------------------------
+
+    def _wire_decoder(self, core, qk_rows, tile_size, tile_batch, device):
+        """Fused QK-RMSNorm/RoPE always; INT8 FFNs with int8_decode; with decode_fusions also INT8 QKV and
+        attention-out linears and the residual carry chain (reference h3vae_runtime.py:346-377)."""
+        from .opt.decoder_fused_qk_rope import clone_with_qk_fusion
+        decoder = clone_with_qk_fusion(core.decoder, qk_rows)
+        if self.int8_decode:
+            from .opt.kitchen_int8 import install_kitchen_int8_ffn
+            try:
+                count = install_kitchen_int8_ffn(decoder, mode="INT8both", require_cuda=True)
+            except Exception as exc:  # noqa: BLE001 - an explicit option has no fallback
+                raise RuntimeError("int8_decode installation failed; no fallback was applied") from exc
+            logger.info("[H3VAE-PyOpt] INT8 FFNs: %d", count)
+            if self.decode_fusions:
+                from .opt.int8_attention_out import from_raw_decoder
+                from .opt.int8_norm1_quant import clone_norm1_quant_decoder, supports_norm1_quant
+                decoder = from_raw_decoder(decoder, warps=8)
+                if supports_norm1_quant(device) and not getattr(decoder, "spatial_parallel", False):
+                    decoder = clone_norm1_quant_decoder(decoder, enabled=True)
+        core.decoder = decoder
+        core.decoder_tile_size = tile_size
+        core.stack_tiling = False
+        if tile_batch != 1:
+            self._install_batched_tiles(core, tile_batch)
+
+    def _wire_encoder(self, core):
+        """conv_in and every downsample conv with packed padding; the bias-fused prefix (residual-pack
+        downsample) with INT8 convolutions under int8_encode; the clip-batched native suffix."""
+        from .opt.encoder_fused_batched_norm import fused_suffix
+        from .opt.encoder_fused_norm_next import next_fused_prefix
+        from .opt.encoder_internal_padding import replace_selected
+        from .opt.encoder_staged_batch import encode_staged
+        self._encode_staged = encode_staged
+        encoder = core.encoder.to(memory_format=torch.channels_last_3d)
+        quant = core.quant_conv.to(memory_format=torch.channels_last_3d)
+        replace_selected(encoder, ["down.0.downsample.conv", "conv_in"])
+        prefix = next_fused_prefix(encoder, "extend_bias_pack")
+        suffix = fused_suffix(encoder, quant, all_stages=True)
+        self.int8_encoder_metadata = None
+        if self.int8_encode:
+            from .opt.encoder_int8_integration import install_int8_encoder_prefix
+            try:
+                self.int8_encoder_metadata = install_int8_encoder_prefix(prefix, require_cuda=True,
+                                                                         tile_variant="auto")
+            except Exception as exc:  # noqa: BLE001 - an explicit option has no fallback
+                raise RuntimeError("int8_encode installation failed; no fallback was applied") from exc
+            logger.info("[H3VAE-PyOpt] INT8 encoder convolutions: %d", self.int8_encoder_metadata["count"])
+        self.prefix, self.suffix = prefix, suffix
 
     @staticmethod
     def _install_batched_tiles(core, batch: int):
-        """Batch decoder tiles per forward; zero picks 1 or 2 from free memory (reference :452-483)."""
-        original = core._run_tile_tasks
+        """Batch decoder tiles per forward call (0 picks 1 or 2 from free memory; reference :452-483)."""
+        core._run_tile_tasks = _TileBatcher(core, core._run_tile_tasks, batch)
 
-        def batched(tiles, indices, forward_fn, stack_tiling, cls_agg=None):
-            if (cls_agg is not None or not tiles or tiles[0].shape[1] != 24 or tiles[0].shape[0] != 1
-                    or torch.is_grad_enabled()):
-                return original(tiles, indices, forward_fn, stack_tiling, cls_agg)
-            current = batch
-            if batch == 0:
-                free, _ = torch.cuda.mem_get_info(tiles[0].device)
-                # keep room for the decoded video and other users of the GPU before pairing tiles
-                current = max(1, min(2, (free - 12 * 1024**3) // (4 * 1024**3)))
-            core._last_tile_batch = current
-            if current == 1:
-                return original(tiles, indices, forward_fn, stack_tiling, cls_agg)
-            outputs = []
-            for start in range(0, len(indices), current):
-                selected = indices[start:start + current]
-                pixels = forward_fn(torch.cat([tiles[i] for i in selected], dim=0))
-                outputs.extend(pixels.split(1, dim=0))
-            return outputs
-
-        core._run_tile_tasks = batched
+    # ---- small helpers --------------------------------------------------------------------------------
 
     def _device(self):
         return self.latents_mean.device
 
     @staticmethod
     def _frames_from_tokens(t: int) -> int:
-        """Latent frames -> pixel frames: 5k+2 -> 17k+5 (reference :485-488)."""
-        return 1 if t <= 1 else max(1, (t - 2) // 5 * 17 + 5)
+        """Latent frames -> pixel frames, 5k+2 -> 17k+5 (reference :485-488)."""
+        return 1 if t <= 1 else max(1, 17 * ((t - 2) // 5) + 5)
 
     @staticmethod
     def _tokens_from_frames(frames: int) -> int:
-        """Pixel frames -> latent frames: 17k+5 -> 5k+2 (reference :490-493)."""
-        return 1 if frames <= 1 else max(1, (frames - 5) // 17 * 5 + 2)
-
-    def _log_call(self, kind: str, t0: float):
-        if not self.log_calls:
-            return
-        if self._device().type == "cuda":
-            torch.cuda.synchronize()
-        dt = (time.monotonic() - t0) * 1000.0
-        if kind == "decode":
-            self._dec_calls += 1
-            self._dec_total_ms += dt
-            calls, total = self._dec_calls, self._dec_total_ms
-        else:
-            self._enc_calls += 1
-            self._enc_total_ms += dt
-            calls, total = self._enc_calls, self._enc_total_ms
-        logger.info("[H3VAE-PyOpt] %s #%d: %.1f ms (running mean %.1f ms)", kind, calls, dt, total / calls)
-
-    # ---- comfy first_stage_model interface -----------------------------------------------------------
-
-    def decode_output_shape(self, input_shape):
-        b, _, t, h, w = input_shape
-        channels = getattr(self.core.decoder, "out_channels", 3)
-        return (b, channels, self._frames_from_tokens(t), h * 16, w * 16)
-
-    def decode(self, z, output_buffer=None, **kwargs):
-        """Normalised latents -> fp32 pixels in [0, 1] (reference :514-564)."""
-        t0 = time.monotonic()
-        if self.int8_decode and z.dtype != torch.float16:
-            raise RuntimeError("int8_decode requires FP16 latent input; use the FP16 VAE dtype")
-        z = z.to(device=self._device())
-        zn = z * self.latents_std + self.latents_mean
-        t = zn.shape[2]
-        if t == 1:
-            dec = self.core.decode(zn)[:, :, -1:, :, :]
-        else:
-            if t < 7:
-                # fewer latent frames than one temporal chunk: repeat the last one
-                zn = torch.cat([zn, zn[:, :, -1:, :, :].repeat(1, 1, 7 - t, 1, 1)], dim=2)
-            dec = self.core.decode_base(zn, frame_num=self._frames_from_tokens(t))
-        # raw decoder output -> fp32 pixels in [0, 1] (reference :543-563)
-        if self.decode_fusions:
-            from .opt.fp16_finalize import finalize_pixels
-            direct = (output_buffer is not None and output_buffer.shape == dec.shape
-                      and output_buffer.dtype == torch.float32 and output_buffer.device == dec.device
-                      and output_buffer.is_contiguous())
-            pixels = finalize_pixels(dec, self._img_std, self._img_mean, output_buffer if direct else None)
-        else:
-            pixels = dec.float() * self._img_std + self._img_mean
-            pixels = pixels.clamp_(0.0, 1.0)
-        if output_buffer is not None:
-            if pixels is not output_buffer:
-                output_buffer.copy_(pixels)
-            out = output_buffer
-        else:
-            out = pixels
-        self._log_call("decode", t0)
-        return out
-
-    def _normalize_pixels(self, x):
-        # [-1, 1] ComfyUI pixels -> ImageNet-normalised [0, 1] pixels in the model dtype
-        x01 = (x.float() + 1.0) * 0.5
-        normed = (x01 - self._img_mean.to(x01.dtype)) / self._img_std.to(x01.dtype)
-        return normed.to(self.latents_mean.dtype)
-
-    def _encode_moments(self, normed):
-        if normed.shape[2] == 1:
-            moments = self.suffix(self.prefix(normed.contiguous(memory_format=torch.channels_last_3d)))
-            return moments[:, :, -1:, :, :]
-        return self._encode_staged(normed, self.prefix, self.suffix, clip_length=self.core.clip_length,
-                                   token_drop=self.core.token_drop, batch_size=self.encoder_staged_batch, cut=2)
+        """Pixel frames -> latent frames, 17k+5 -> 5k+2 (reference :490-493)."""
+        return 1 if frames <= 1 else max(1, 5 * ((frames - 5) // 17) + 2)
 
     @staticmethod
     def _split_encoder_tiles(length, tile_size, overlap_min, ratio):
-        """Tile starts/lengths/overlaps along one axis (reference :584-603).
-
-        The smallest tile count whose minimum overlaps cover ``length``; the
-        slack is spread round-robin over the overlaps in steps of ``ratio``.
-        """
-        if tile_size <= overlap_min:
-            raise ValueError("encoder tile must exceed its minimum overlap")
-        if tile_size >= length:
-            return [0], [length], []
-        count = math.ceil(length / tile_size)
-        while True:
-            overlaps = [overlap_min] * (count - 1)
-            remaining = tile_size * count - sum(overlaps) - length
-            if remaining >= 0:
-                break
-            count += 1
-        for i in range(remaining // ratio):
-            overlaps[i % (count - 1)] += ratio
-        starts = [0]
-        for overlap in overlaps:
-            starts.append(starts[-1] + tile_size - overlap)
-        return starts, [tile_size] * count, overlaps
+        return axis_tiles(length, tile_size, overlap_min, ratio)
 
     @staticmethod
     def _select_encoder_tile(configured, height, width):
-        return configured or (672 if max(height, width) <= 672 else 256)
+        """The configured encoder tile, or 672 when the frame fits one, else 256."""
+        if configured:
+            return configured
+        return 672 if max(height, width) <= 672 else 256
+
+    def _record(self, kind, started):
+        if self.log_calls:
+            self._timer.record(kind, started, self._device())
+
+    # ---- decode ---------------------------------------------------------------------------------------
+
+    def decode_output_shape(self, input_shape):
+        b, _, t, h, w = input_shape
+        return (b, getattr(self.core.decoder, "out_channels", 3), self._frames_from_tokens(t), 16 * h, 16 * w)
+
+    def _decode_raw(self, latents):
+        """Denormalised latents -> the model's raw decoder output (reference :533-541): one latent
+        frame is decoded alone and its last frame kept; fewer than 7 latent frames repeat the last one
+        up to a whole temporal chunk."""
+        t = latents.shape[2]
+        if t == 1:
+            return self.core.decode(latents)[:, :, -1:]
+        if t < 7:
+            latents = torch.cat([latents, latents[:, :, -1:].expand(-1, -1, 7 - t, -1, -1)], dim=2)
+        return self.core.decode_base(latents, frame_num=self._frames_from_tokens(t))
+
+    def _finalize(self, raw, output_buffer):
+        """Raw pixels -> fp32 in [0, 1]: x * std + mean, then clamp.  A contiguous fp32 output_buffer of
+        the output's shape on its device is written in place; any other buffer receives a copy."""
+        direct = (output_buffer is not None and tuple(output_buffer.shape) == tuple(raw.shape)
+                  and output_buffer.dtype == torch.float32 and output_buffer.device == raw.device
+                  and output_buffer.is_contiguous())
+        if self.decode_fusions:
+            from .opt.fp16_finalize import finalize_pixels
+            pixels = finalize_pixels(raw, self._img_std, self._img_mean, output_buffer if direct else None)
+        else:
+            pixels = (raw.float() * self._img_std + self._img_mean).clamp_(0.0, 1.0)
+        if output_buffer is None:
+            return pixels
+        if pixels is not output_buffer:
+            output_buffer.copy_(pixels)
+        return output_buffer
+
+    def decode(self, z, output_buffer=None, **kwargs):
+        """Normalised latents [B, 24, t, h, w] -> fp32 pixels [B, 3, F, 16h, 16w] in [0, 1] (reference :514-564)."""
+        started = time.monotonic()
+        if self.int8_decode and z.dtype != torch.float16:
+            raise RuntimeError("int8_decode requires FP16 latent input; use the FP16 VAE dtype")
+        latents = z.to(device=self._device()) * self.latents_std + self.latents_mean
+        out = self._finalize(self._decode_raw(latents), output_buffer)
+        self._record("decode", started)
+        return out
+
+    # ---- encode ---------------------------------------------------------------------------------------
+
+    def _normalize_pixels(self, x):
+        """[-1, 1] pixels -> ImageNet-normalised [0, 1] pixels in the model dtype (fp32 arithmetic)."""
+        unit = (x.float() + 1.0) * 0.5
+        return ((unit - self._img_mean) / self._img_std).to(self.latents_mean.dtype)
+
+    def _encode_moments(self, normed):
+        """Moments of one spatial tile: clip-staged (reference :566-579); a single frame runs prefix and
+        suffix directly and keeps the last latent frame."""
+        if normed.shape[2] == 1:
+            single = self.suffix(self.prefix(normed.contiguous(memory_format=torch.channels_last_3d)))
+            return single[:, :, -1:]
+        return self._encode_staged(normed, self.prefix, self.suffix, clip_length=self.core.clip_length,
+                                   token_drop=self.core.token_drop, batch_size=self.encoder_staged_batch, cut=2)
 
     def _encode_spatial_tiled(self, x, tile_size):
+        """Tiles of ``tile_size`` pixels encoded one by one and stitched with the core's blend
+        (reference :609-639); x is normalised once for the whole video."""
         core = self.core
-
-        def split(length):
-            return self._split_encoder_tiles(length, tile_size, core.tile_overlap_min, core.vae_ratio)
-
-        y_idx, y_len, y_overlap = split(x.shape[-2])
-        x_idx, x_len, x_overlap = split(x.shape[-1])
-        rows = [[self._encode_moments(self._normalize_pixels(x[..., yp:yp + hh, xp:xp + ww]))
-                 for xp, ww in zip(x_idx, x_len)] for yp, hh in zip(y_idx, y_len)]
-        y_overlap = [o // core.vae_ratio for o in y_overlap]
-        x_overlap = [o // core.vae_ratio for o in x_overlap]
-        result_rows = []
-        for i, row in enumerate(rows):
-            result_row = []
-            for j, tile in enumerate(row):
-                if i:
-                    tile = core.blend(rows[i - 1][j], tile, y_overlap[i - 1], dim=-2)
-                if j:
-                    tile = core.blend(row[j - 1], tile, x_overlap[j - 1], dim=-1)
-                if i < len(rows) - 1:
-                    tile = tile[..., :-y_overlap[i], :]
-                if j < len(row) - 1:
-                    tile = tile[..., :, :-x_overlap[j]]
-                result_row.append(tile)
-            result_rows.append(torch.cat(result_row, dim=-1))
-        return torch.cat(result_rows, dim=-2)
+        ys, hs, y_over = axis_tiles(x.shape[-2], tile_size, core.tile_overlap_min, core.vae_ratio)
+        xs, ws, x_over = axis_tiles(x.shape[-1], tile_size, core.tile_overlap_min, core.vae_ratio)
+        normed = self._normalize_pixels(x)
+        grid = [[self._encode_moments(normed[..., y:y + h, x0:x0 + w]) for x0, w in zip(xs, ws)]
+                for y, h in zip(ys, hs)]
+        r = core.vae_ratio
+        return stitch_tiles(grid, [o // r for o in y_over], [o // r for o in x_over], core.blend)
 
     def encode(self, x, device=None):
-        """[-1, 1] pixels -> normalised latent means (reference :641-661)."""
-        t0 = time.monotonic()
+        """[-1, 1] pixels [B, 3, T, H, W] -> normalised latent means [B, 24, t, H/16, W/16] (reference :641-661)."""
+        started = time.monotonic()
         if self.int8_encode and x.dtype != torch.float16:
             raise RuntimeError("int8_encode requires FP16 pixel input; use the FP16 VAE dtype")
         x = x.to(device=self._device())
         if x.ndim == 4:
             x = x.unsqueeze(2)
-        tile_size = self._select_encoder_tile(self.encoder_tile_size, x.shape[-2], x.shape[-1])
-        if x.shape[-2] > tile_size or x.shape[-1] > tile_size:
-            moments = self._encode_spatial_tiled(x, tile_size)
+        tile = self._select_encoder_tile(self.encoder_tile_size, x.shape[-2], x.shape[-1])
+        if max(x.shape[-2], x.shape[-1]) > tile:
+            moments = self._encode_spatial_tiled(x, tile)
         else:
             moments = self._encode_moments(self._normalize_pixels(x))
         mean = moments.float()[:, :moments.shape[1] // 2]
         latents = (mean - self.latents_mean.float()) / self.latents_std.float()
-        self._log_call("encode", t0)
+        self._record("encode", started)
         return latents
 
     def decode_tiled(self, z, **kwargs):
@@ -479,35 +517,65 @@ class H3VAEPyOptRuntime(torch.nn.Module):
 
     @torch.no_grad()
     def warmup(self, frames: int, width: int, height: int, mode: str = "both"):
-        """Run one dummy decode and/or encode of the given shape (first-call costs leave the first request)."""
+        """One dummy decode and/or encode of the given shape, so first-call costs leave the first request."""
         dev = self._device()
-        is_gpu = dev.type == "cuda"
         results = {}
+        runs = []
         if mode in ("decode", "both"):
             z = torch.randn((1, 24, self._tokens_from_frames(frames), height // 16, width // 16), device=dev,
                             dtype=self.latents_mean.dtype)
-            if is_gpu:
-                torch.cuda.synchronize()
-            t0 = time.monotonic()
-            self.decode(z)
-            if is_gpu:
-                torch.cuda.synchronize()
-            results["decode_first_s"] = round(time.monotonic() - t0, 3)
+            runs.append(("decode_first_s", self.decode, z))
         if mode in ("encode", "both"):
             x = torch.rand((1, 3, frames, height, width), device=dev, dtype=self.latents_mean.dtype) * 2.0 - 1.0
-            if is_gpu:
-                torch.cuda.synchronize()
-            t0 = time.monotonic()
-            self.encode(x)
-            if is_gpu:
-                torch.cuda.synchronize()
-            results["encode_first_s"] = round(time.monotonic() - t0, 3)
-        if is_gpu:
+            runs.append(("encode_first_s", self.encode, x))
+        for key, fn, arg in runs:
+            if dev.type == "cuda":
+                torch.cuda.synchronize(dev)
+            started = time.monotonic()
+            fn(arg)
+            if dev.type == "cuda":
+                torch.cuda.synchronize(dev)
+            results[key] = round(time.monotonic() - started, 3)
+        del runs
+        if dev.type == "cuda":
             torch.cuda.empty_cache()
-        self._dec_calls, self._dec_total_ms = 0, 0.0
-        self._enc_calls, self._enc_total_ms = 0, 0.0
+        self._timer.reset()
         logger.info("[H3VAE-PyOpt] warmup %s (%d frames, %dx%d): %s", mode, frames, width, height, results)
         return results
+
+
+# ---- ComfyUI VAE wrapper ------------------------------------------------------------------------------
+
+def _encode_memory(vae, shape, dtype):
+    """Bytes ComfyUI reserves for an encode: the staged prefix holds about 1 kB per pixel of one clip."""
+    import comfy.model_management as mm
+    _, _, t, h, w = shape
+    return int(vae.size + (1000 * min(t, 17) * h * w + 1_100_000_000) * mm.dtype_size(dtype) / 2 * 1.15)
+
+
+def _decode_memory(vae, shape, dtype):
+    """Bytes ComfyUI reserves for a decode: the whole fp16 video canvas, tile outputs and blend temporaries."""
+    import comfy.model_management as mm
+    _, _, t, h, w = shape
+    canvas = 3 * vae.upscale_ratio[0](t) * (16 * h) * (16 * w) * 2 * 2.5
+    return int(vae.size + (canvas + 1_100_000_000) * mm.dtype_size(dtype) / 2 * 1.1)
+
+
+def _comfy_fields(int8):
+    """The attributes ComfyUI's VAE reads, as its H3 branch sets them (reference :731-806)."""
+    return {
+        "latent_channels": 24, "latent_dim": 3, "output_channels": 3,
+        "upscale_ratio": (H3VAEPyOptRuntime._frames_from_tokens, 16, 16), "upscale_index_formula": (4, 16, 16),
+        "downscale_ratio": (H3VAEPyOptRuntime._tokens_from_frames, 16, 16), "downscale_index_formula": (4, 16, 16),
+        "working_dtypes": [torch.float16] if int8 else [torch.float16, torch.float32],
+        # the runtime tiles internally and returns finalised [0, 1] pixels; it wants [-1, 1] input
+        "handles_tiling": True,
+        "process_output": lambda image: image,
+        "process_input": lambda image: image * 2.0 - 1.0,
+        # defaults of the base class, whose constructor is not run
+        "pad_channel_value": None, "disable_offload": False, "not_video": False, "size": None,
+        "extra_1d_channel": None, "crop_input": True, "format_encoded": None,
+    }
 
 
 def build_comfy_vae(runtime: H3VAEPyOptRuntime, dtype=None):
@@ -522,51 +590,19 @@ def build_comfy_vae(runtime: H3VAEPyOptRuntime, dtype=None):
         def __init__(self, first_stage_model, device=None, dtype=None):
             # configured directly: the parent constructor would sniff a state dict
             self.first_stage_model = first_stage_model
-            self.latent_channels = 24
-            self.latent_dim = 3
-            self.output_channels = 3
-            self.upscale_ratio = (H3VAEPyOptRuntime._frames_from_tokens, 16, 16)
-            self.upscale_index_formula = (4, 16, 16)
-            self.downscale_ratio = (H3VAEPyOptRuntime._tokens_from_frames, 16, 16)
-            self.downscale_index_formula = (4, 16, 16)
-            self.working_dtypes = [torch.float16] if int8 else [torch.float16, torch.float32]
-            self.handles_tiling = True
-            self.process_output = lambda image: image
-            self.process_input = lambda image: image * 2.0 - 1.0
-            self.pad_channel_value = None
-            self.disable_offload = False
-            self.not_video = False
-            self.size = None
-            self.extra_1d_channel = None
-            self.crop_input = True
-            self.format_encoded = None
-            if device is None:
-                device = model_management.vae_device()
-            self.device = device
-            offload_device = model_management.vae_offload_device()
+            for name, value in _comfy_fields(int8).items():
+                setattr(self, name, value)
+            self.device = model_management.vae_device() if device is None else device
             if dtype is None:
                 dtype = model_management.vae_dtype(self.device, self.working_dtypes)
             if int8 and dtype != torch.float16:
                 raise RuntimeError("INT8 VAE mode requires ComfyUI to select an FP16 VAE dtype")
             self.vae_dtype = dtype
             self.output_device = model_management.intermediate_device()
-
-            def estimate_encode_memory(shape, dtype_):
-                _, _, t, h, w = shape
-                dsize = model_management.dtype_size(dtype_)
-                act = 1000 * min(t, 17) * h * w          # staged prefix activations, about 1 kB per clip pixel
-                return int(self.size + (act + 1_100_000_000) * dsize / 2 * 1.15)
-
-            def estimate_decode_memory(shape, dtype_):
-                _, _, t, h, w = shape
-                dsize = model_management.dtype_size(dtype_)
-                out = 3 * self.upscale_ratio[0](t) * (h * 16) * (w * 16) * 2 * 2.5   # canvas + tiles + blend
-                return int(self.size + (out + 1_100_000_000) * dsize / 2 * 1.1)
-
-            self.memory_used_encode = estimate_encode_memory
-            self.memory_used_decode = estimate_decode_memory
-            self.patcher = comfy.model_patcher.CoreModelPatcher(first_stage_model, load_device=self.device,
-                                                                offload_device=offload_device)
+            self.memory_used_encode = lambda shape, dtype_: _encode_memory(self, shape, dtype_)
+            self.memory_used_decode = lambda shape, dtype_: _decode_memory(self, shape, dtype_)
+            self.patcher = comfy.model_patcher.CoreModelPatcher(
+                first_stage_model, load_device=self.device, offload_device=model_management.vae_offload_device())
             self.model_size()
 
     return H3VAEPyOptVAE(runtime, dtype=dtype)

@@ -25,7 +25,7 @@ from typing import List, Optional
 
 import torch
 import torch.nn.functional as F
-from torch.utils.weak import WeakIdKeyDictionary
+from torch import nn
 
 from .. import _hip
 
@@ -174,30 +174,35 @@ def _fake_fold(x, front):
     return torch.empty((b, 32, d + front, h, w), device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
 
 
-class _PackedWeights:
-    """Packed fp16 copies of conv weights, one per live weight tensor.
-
-    Keyed by the tensor object (weakly: a copy lives as long as its weight), stamped with
-    the storage address, device, dtype, shape and in-place version, so a module move or an
-    in-place load repacks.  Inference tensors carry no version counter: their in-place
-    updates (inside inference mode) are not seen."""
-
-    def __init__(self, pack=pack_conv_weight_f16):
-        self._cache = WeakIdKeyDictionary()
-        self._pack = pack
-
-    def get(self, weight):
-        stamp = (weight.data_ptr(), weight.device, weight.dtype, tuple(weight.shape),
-                 -1 if weight.is_inference() else weight._version)
-        hit = self._cache.get(weight)
-        if hit is None or hit[0] != stamp:
-            hit = (stamp, self._pack(weight.detach()))
-            self._cache[weight] = hit
-        return hit[1]
+def _weight_stamp(weight):
+    """What identifies the contents of a weight: storage, device, dtype, shape and in-place version
+    (inference tensors carry no version counter; their in-place updates are not seen)."""
+    return (weight.data_ptr(), weight.device, weight.dtype, tuple(weight.shape),
+            -1 if weight.is_inference() else weight._version)
 
 
-_PACKED = _PackedWeights()
-_FOLDED = _PackedWeights(fold_conv_weight_f16)
+class PackedConvWeight(nn.Module):
+    """The packed fp16 copy of one conv weight, owned by the module that runs the conv.
+
+    The copy is made on first use and kept as a non-persistent buffer, so it moves and is freed
+    with its owner (``.to()``, an offload of the runtime): no packed copy outlives the module or
+    stays behind on a GPU, and a conv that never runs never holds one.  Each use compares the
+    source weight with the stamp taken at packing and repacks when it changed (an in-place
+    state-dict load, a move of the model's weights)."""
+
+    def __init__(self, weight, fold=False):
+        super().__init__()
+        self.fold = bool(fold)
+        self.register_buffer("packed", None, persistent=False)
+        self._stamp = None
+
+    def forward(self, weight):
+        stamp = _weight_stamp(weight)
+        if self.packed is None or stamp != self._stamp:
+            source = weight.detach()
+            self.packed = fold_conv_weight_f16(source) if self.fold else pack_conv_weight_f16(source)
+            self._stamp = stamp
+        return self.packed
 
 
 def native_device(x):
@@ -205,50 +210,88 @@ def native_device(x):
     return x.is_cuda and _hip.is_gfx950(x.device)
 
 
-def valid_conv3d(x, weight, bias, stride, causal_skip=False, residual=None):
-    """Valid convolution of an already padded input: h3v_conv3d_f16 when the shape fits, else F.conv3d.
-
-    causal_skip: x holds two zero leading frames per item (the producers' causal padding).
-    residual: the residual block's closing ``residual + conv`` fused into the epilogue."""
-    stride = tuple(stride)
-    if native_device(x) and conv3d_f16_fits(x, weight, stride):
-        kernel = list(weight.shape[2:])
-        skip = bool(causal_skip) and kernel[0] == 3 and stride[0] == 1
-        return conv3d_f16(x, _PACKED.get(weight), bias, kernel, list(stride), skip, residual)
-    y = F.conv3d(x, weight, bias, stride=stride)
-    return y if residual is None else residual + y
+def _require_native(x, what):
+    if not native_device(x):
+        raise RuntimeError(f"{what} runs on an AMD MI355X (gfx950) GPU only; got a tensor on {x.device}")
 
 
-def producer_conv3d(y, weight, bias, stride, residual=None):
-    """The FP16 conv after a GroupNorm/SiLU/pad producer (two zero leading frames per item)."""
-    return valid_conv3d(y, weight, bias, stride, causal_skip=True, residual=residual)
+class NativeConv(nn.Module):
+    """One FP16 convolution of the model run as ``h3v_conv3d_f16`` on an already padded input.
+
+    Shares the model's weight and bias; owns their packed copy.  Shapes outside the kernel's gate
+    (``conv3d_f16_fits``) raise: there is no second implementation to fall back to."""
+
+    def __init__(self, weight, bias, stride):
+        super().__init__()
+        if weight.ndim != 5:
+            raise ValueError("NativeConv expects a [Cout, Cin, kd, kh, kw] weight")
+        self.weight, self.bias = weight, bias
+        self.stride = tuple(int(s) for s in stride)
+        self.packed_weight = PackedConvWeight(weight)
+
+    def forward(self, x, *, with_bias=True, causal_skip=False, residual=None):
+        _require_native(x, "FP16 encoder convolution")
+        if not conv3d_f16_fits(x, self.weight, self.stride):
+            raise ValueError(f"FP16 encoder convolution: input {tuple(x.shape)} / weight {tuple(self.weight.shape)} "
+                             f"at stride {self.stride} is outside h3v_conv3d_f16's gate (Cin % 32 == 0, fp16)")
+        kernel = list(self.weight.shape[2:])
+        skip = bool(causal_skip) and kernel[0] == 3 and self.stride[0] == 1
+        return conv3d_f16(x, self.packed_weight(self.weight), self.bias if with_bias else None, kernel,
+                          list(self.stride), skip, residual)
 
 
-def pointwise_conv3d(x, conv):
-    """A 1x1x1 nn.Conv3d (``nin_shortcut``) on a channels-last-3d input."""
-    if (native_device(x) and tuple(conv.kernel_size) == (1, 1, 1) and tuple(conv.padding) == (0, 0, 0)
-            and tuple(conv.dilation) == (1, 1, 1) and conv.groups == 1
-            and x.is_contiguous(memory_format=torch.channels_last_3d)):
-        return valid_conv3d(x, conv.weight, conv.bias, conv.stride)
-    return conv(x)
+class PointwiseConv(nn.Module):
+    """A 1x1x1 ``nn.Conv3d`` over channels-last-3d activations.
+
+    Cin % 32 == 0 (``nin_shortcut``) runs as ``h3v_conv3d_f16``; other widths (the 48-channel
+    ``quant_conv``) are a plain [rows, Cin] x [Cin, Cout] GEMM through torch's BLAS (hipBLASLt) over
+    the channels-last rows, with the bias added in the same call."""
+
+    def __init__(self, conv):
+        super().__init__()
+        if (tuple(conv.kernel_size) != (1, 1, 1) or tuple(conv.padding) != (0, 0, 0) or tuple(conv.stride) != (1, 1, 1)
+                or tuple(conv.dilation) != (1, 1, 1) or conv.groups != 1):
+            raise ValueError("PointwiseConv expects a 1x1x1, stride-1, unpadded, ungrouped Conv3d")
+        self.weight, self.bias = conv.weight, conv.bias
+        self.conv = NativeConv(conv.weight, conv.bias, (1, 1, 1)) if conv.weight.shape[1] % 32 == 0 else None
+
+    def forward(self, x):
+        _require_native(x, "pointwise convolution")
+        if self.conv is not None:
+            return self.conv(x.contiguous(memory_format=torch.channels_last_3d))
+        b, c, d, h, w = x.shape
+        rows = x.permute(0, 2, 3, 4, 1).reshape(-1, c)
+        y = F.linear(rows, self.weight.view(self.weight.shape[0], c), self.bias)
+        return y.view(b, d, h, w, -1).permute(0, 4, 1, 2, 3)
 
 
-def padded_causal_conv3d(x, weight, bias, stride, front, top, bottom, left, right):
-    """Zero frames in front + reflect border + valid conv, the padding packed by one HIP kernel.
+class PaddedCausalConv(nn.Module):
+    """Zero frames in front + reflect border + valid conv (conv_in, the downsample convs).
 
-    The output has exactly (D + front - kd) // sd + 1 frames."""
-    if (native_device(x) and x.dtype == torch.float16 and weight.dtype == torch.float16 and 1 <= x.shape[1] <= 3
-            and tuple(weight.shape[1:]) == (x.shape[1], 3, 3, 3) and tuple(stride) == (1, 1, 1)
-            and (top, bottom, left, right) == (1, 1, 1, 1) and min(x.shape[3:]) >= 2):
-        xf = tap_fold_pack(x, front)
-        return conv3d_f16(xf, _FOLDED.get(weight), bias, [3, 1, 1], [1, 1, 1], front == 2)
-    if native_device(x) and x.shape[1] % 8 == 0 and max(top, bottom) < x.shape[3] and max(left, right) < x.shape[4]:
-        xp = causal_reflect_pack(x, front, top, bottom, left, right)
-        if conv3d_f16_fits(xp, weight, stride):
-            return valid_conv3d(xp, weight, bias, stride, causal_skip=front == 2)
-        return F.conv3d(xp, weight, bias, stride=stride)
-    if top or bottom or left or right:
-        x = F.pad(x, (left, right, top, bottom, 0, 0), mode="reflect")
-    if front:
-        x = F.pad(x, (0, 0, 0, 0, front, 0))
-    return F.conv3d(x, weight, bias, stride=stride)
+    The padding is written by one pack kernel and the conv runs over exactly the kept outputs.
+    A 3-channel stride-1 3x3x3 conv with a border of 1 (conv_in) folds its 3x3 spatial taps into 32
+    channels in the pack (``h3v_tap_fold_pack``) and becomes a 3x1x1 conv with K = 96."""
+
+    def __init__(self, weight, bias, stride, border):
+        super().__init__()
+        self.weight, self.bias = weight, bias
+        self.stride, self.border = tuple(int(s) for s in stride), tuple(int(b) for b in border)
+        self.folded = (weight.shape[1] <= 3 and tuple(weight.shape[2:]) == (3, 3, 3) and self.stride == (1, 1, 1)
+                       and self.border == (1, 1, 1, 1))
+        if self.folded:
+            self.packed_weight = PackedConvWeight(weight, fold=True)
+        else:
+            self.conv = NativeConv(weight, bias, stride)
+
+    def forward(self, x, front):
+        _require_native(x, "padded causal convolution")
+        if self.folded:
+            if min(x.shape[3:]) < 2:
+                raise ValueError("conv_in requires H, W >= 2")
+            return conv3d_f16(tap_fold_pack(x, front), self.packed_weight(self.weight), self.bias, [3, 1, 1],
+                              [1, 1, 1], front == 2)
+        top, bottom, left, right = self.border
+        if x.shape[1] % 8 or max(top, bottom) >= x.shape[3] or max(left, right) >= x.shape[4]:
+            raise ValueError(f"padded causal convolution: input {tuple(x.shape)} needs C % 8 == 0 and a reflect "
+                             f"border {self.border} smaller than H, W")
+        return self.conv(causal_reflect_pack(x, front, top, bottom, left, right), causal_skip=front == 2)

@@ -7,20 +7,21 @@ Mirror of opt/encoder_fused_batched_norm.py in fishelegs/ComfyUI-H3VAE-PyOpt
 for the suffix stages; each clip keeps its own per-frame statistics and its
 own causal zero frames.  The producer is one ``h3v_gn_norm_pack_f16`` launch
 sequence over batch x depth frames (statistics, merge, fp16 pack).  The
-3x3x3 convolutions that follow it and the ``nin_shortcut`` projections run
-as ``h3v_conv3d_f16`` (FP16 operands, fp32 accumulation on the matrix cores,
-causal-zero depth taps skipped) when their shape fits it (Cin % 32 == 0);
-other shapes keep the model's ``F.conv3d``, as in the reference.
+3x3x3 convolutions that follow it, the ``nin_shortcut`` projections and the
+stages' downsample convs run as ``h3v_conv3d_f16`` (FP16 operands, fp32
+accumulation on the matrix cores, causal-zero depth taps skipped); the
+48-channel ``quant_conv`` is one channels-last GEMM.  With ``all_stages`` every
+suffix layer is native; a shape outside the kernels' gates raises.
 """
 from __future__ import annotations
 
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
-from .encoder_fp16_conv import pointwise_conv3d, producer_conv3d
+from .encoder_fp16_conv import PointwiseConv
 from .encoder_fused_norm_bias import FusedNormPadConv, norm_pack_f16
+from .encoder_internal_padding import ImplicitTemporalPadConv3d
 from .encoder_staged_batch import EncoderSuffix
 
 
@@ -59,7 +60,7 @@ def _fake(x, pre_bias, weight, bias, eps):
 class BatchedNormPadConv(FusedNormPadConv):
     def forward(self, x):
         y = batched_temporal_norm_pack(x, None, self.norm_weight, self.norm_bias, self.eps)
-        return producer_conv3d(y, self.weight, self.bias, self.stride) if self.with_conv else y
+        return self.conv(y, causal_skip=True) if self.with_conv else y
 
 
 class BatchedResidualBlock(torch.nn.Module):
@@ -72,16 +73,28 @@ class BatchedResidualBlock(torch.nn.Module):
         self.first = BatchedNormPadConv(block.norm1, block.conv1, with_conv=False)
         self.second = BatchedNormPadConv(block.norm2, block.conv2, with_conv=False)
         self.shortcut = getattr(block, "nin_shortcut", None)
+        self.shortcut_conv = PointwiseConv(self.shortcut) if self.shortcut is not None else None
 
     def forward(self, x, zq=None):
         if zq is not None:
             raise ValueError("Unconditional inference only")
-        residual = pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x
-        h = producer_conv3d(self.first(x), self.first.weight, None, self.first.stride)
+        residual = self.shortcut_conv(x) if self.shortcut_conv is not None else x
+        h = self.first.conv(self.first(x), with_bias=False, causal_skip=True)
         h = batched_temporal_norm_pack(h, self.first.bias, self.second.norm_weight, self.second.norm_bias,
                                        self.second.eps)
         # the closing residual add runs in the second conv's epilogue (fp16(residual + fp16 conv))
-        return producer_conv3d(h, self.second.weight, self.second.bias, self.second.stride, residual=residual)
+        return self.second.conv(h, causal_skip=True, residual=residual)
+
+
+class SuffixDownsample(torch.nn.Module):
+    """A suffix stage's downsample conv, its causal / reflect padding written by the pack kernel."""
+
+    def __init__(self, downsample):
+        super().__init__()
+        self.conv = ImplicitTemporalPadConv3d(downsample.conv)
+
+    def forward(self, x):
+        return self.conv(x)
 
 
 class BatchedSuffix(EncoderSuffix):
@@ -92,18 +105,15 @@ class BatchedSuffix(EncoderSuffix):
             stage = torch.nn.Module()
             stage.block = torch.nn.ModuleList([BatchedResidualBlock(block) for block in original.block])
             if hasattr(original, "downsample"):
-                stage.downsample = original.downsample
+                stage.downsample = SuffixDownsample(original.downsample)
             self.stages[i] = stage
         self.final = BatchedNormPadConv(encoder.norm_out, encoder.conv_out) if all_stages else None
+        self.quant = PointwiseConv(quant_conv) if all_stages else None
 
-    def forward(self, h):
-        for stage in self.stages:
-            for block in stage.block:
-                h = block(h)
-            if hasattr(stage, "downsample"):
-                h = stage.downsample(h)
-        h = self.final(h) if self.final is not None else self.conv_out(F.silu(self.norm_out(h)))
-        return self.quant_conv(h)
+    def head(self, h):
+        if self.final is None:
+            return super().head(h)
+        return self.quant(self.final(h))
 
 
 def fused_suffix(encoder, quant_conv, all_stages=False):

@@ -14,7 +14,7 @@ not applied in its epilogue; it is folded into the second producer as
 Without INT8 wrappers (the FP16 encoder mode) the same producers emit fp16
 through ``h3v_gn_norm_pack_f16`` (one fused statistics + pack launch
 sequence) and the convolutions run in FP16 through ``h3v_conv3d_f16``
-(``producer_conv3d``; the ``nin_shortcut`` through ``pointwise_conv3d``);
+(``NativeConv``; the ``nin_shortcut`` through ``PointwiseConv``);
 nothing in this file ever falls back from the INT8 path to them.
 """
 from __future__ import annotations
@@ -23,7 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _hip
-from .encoder_fp16_conv import pointwise_conv3d, producer_conv3d
+from .encoder_fp16_conv import NativeConv, PointwiseConv
 
 
 def _check_channel_vectors(x, *vectors):
@@ -112,10 +112,12 @@ class FusedNormPadConv(torch.nn.Module):
         self.stride = conv.stride
         self.config = config
         self.with_conv = with_conv
+        # the FP16 conv after the producer (FP16 encoder mode); packs its weight on first use only
+        self.conv = NativeConv(conv.weight, conv.bias, conv.stride)
 
     def forward(self, x):
         y = temporal_norm_pack(x, self.norm_weight, self.norm_bias, self.eps)
-        return producer_conv3d(y, self.weight, self.bias, self.stride) if self.with_conv else y
+        return self.conv(y, causal_skip=True) if self.with_conv else y
 
 
 # The reference's opaque-op subclass has the same behaviour here (every producer is an opaque op).
@@ -132,6 +134,7 @@ class BiasFusedResidualBlock(torch.nn.Module):
         self.first = OpaqueFusedNormPadConv(block.norm1, block.conv1, with_conv=False)
         self.second = OpaqueFusedNormPadConv(block.norm2, block.conv2, with_conv=False)
         self.shortcut = getattr(block, "nin_shortcut", None)
+        self.shortcut_conv = PointwiseConv(self.shortcut) if self.shortcut is not None else None
         # INT8 wrappers are installed by encoder_int8_integration.install_int8_encoder_prefix;
         # None keeps the FP16 encoder mode.
         self.int8_first = None
@@ -144,27 +147,25 @@ class BiasFusedResidualBlock(torch.nn.Module):
                                                  self.second.eps, pre_bias=self.first.bias)
         first_input = self.first(x)
         h = (self.int8_first(first_input) if self.int8_first is not None
-             else producer_conv3d(first_input, self.first.weight, None, self.first.stride))
+             else self.first.conv(first_input, with_bias=False, causal_skip=True))
         second_input = bias_temporal_norm_pack(h, self.first.bias, self.second.norm_weight,
                                                self.second.norm_bias, self.second.eps)
         return (self.int8_second(second_input) if self.int8_second is not None
-                else producer_conv3d(second_input, self.second.weight, second_bias, self.second.stride))
+                else self.second.conv(second_input, with_bias=second_bias is not None, causal_skip=True))
 
     def forward(self, x, zq=None):
         """(shortcut(x) or x) + body(x), the add fused into the second conv's epilogue where that conv is a
         kernel of this package (bit-identical to the separate fp16 add of the reference, :141)."""
         if zq is not None:
             raise ValueError("Unconditional inference only")
-        residual = pointwise_conv3d(x, self.shortcut) if self.shortcut is not None else x
+        residual = self.shortcut_conv(x) if self.shortcut_conv is not None else x
         if self.int8_first is not None and self.int8_first.fuse_norm:
             h = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
             return self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias, self.second.eps,
                                                  pre_bias=self.first.bias, residual=residual)
         if self.int8_first is None:
-            first_input = self.first(x)
-            h = producer_conv3d(first_input, self.first.weight, None, self.first.stride)
+            h = self.first.conv(self.first(x), with_bias=False, causal_skip=True)
             second_input = bias_temporal_norm_pack(h, self.first.bias, self.second.norm_weight,
                                                    self.second.norm_bias, self.second.eps)
-            return producer_conv3d(second_input, self.second.weight, self.second.bias, self.second.stride,
-                                   residual=residual)
+            return self.second.conv(second_input, causal_skip=True, residual=residual)
         return residual + self._residual_body(x, self.second.bias)

@@ -13,7 +13,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _hip
-from .encoder_fp16_conv import valid_conv3d
+from .encoder_fp16_conv import NativeConv
 from .encoder_fused_norm_bias import BiasFusedResidualBlock
 
 
@@ -65,6 +65,7 @@ class ResidualDownsampleBlock(BiasFusedResidualBlock):
             raise ValueError("Expected stage1 final identity-shortcut block and causal reflect downsample")
         self.down_weight = conv.weight
         self.down_bias = conv.bias
+        self.down = NativeConv(conv.weight, conv.bias, (2, 2, 2))
 
     def forward(self, x, zq=None):
         if zq is not None:
@@ -72,4 +73,4 @@ class ResidualDownsampleBlock(BiasFusedResidualBlock):
         # second.bias is added by the pack, not by the second convolution
         h = self._residual_body(x, None)
         h = residual_downsample_pack(h, x, self.second.bias)
-        return valid_conv3d(h, self.down_weight, self.down_bias, (2, 2, 2))
+        return self.down(h)

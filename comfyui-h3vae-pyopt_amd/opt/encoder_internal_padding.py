@@ -1,61 +1,81 @@
-"""Causal temporal zero padding folded into the convolution call (FP16 encoder layers).
+"""The model's causal padded convolutions, with their padding written by a pack kernel.
 
-Mirror of opt/encoder_internal_padding.py in fishelegs/ComfyUI-H3VAE-PyOpt.
-The spatial reflect pad stays explicit; the left-only causal zero frames are
-requested from the convolution as symmetric temporal padding and the extra
-tail outputs are dropped.  Used for ``down.0.downsample.conv`` (and, in this
-build's runtime, ``conv_in``), FP16 layers outside the INT8 path.  On gfx950
-the zero frames and the reflect border are written by one pack kernel
-(``h3v_causal_reflect_pack``; for conv_in's 3 channels ``h3v_tap_fold_pack``,
-which also folds the 3x3 spatial taps into 32 channels) and the convolution
-runs as ``h3v_conv3d_f16`` over exactly the kept outputs.
+Counterpart of opt/encoder_internal_padding.py in fishelegs/ComfyUI-H3VAE-PyOpt
+(``ImplicitTemporalPadConv3d`` :14-35, ``replace_selected`` / ``restore_selected``
+:38-56), which moves the causal zero frames of ``down.0.downsample.conv`` into
+the cuDNN call.  Here a wrapped conv never materialises ``F.pad`` output: one
+HIP pack (``h3v_causal_reflect_pack``) writes the zero frames and the reflect
+border into a channels-last-3d buffer and ``h3v_conv3d_f16`` convolves it over
+exactly the output frames the model keeps (3-channel ``conv_in`` folds its
+spatial taps in the pack instead, see ``encoder_fp16_conv.PaddedCausalConv``).
+
+The model pads a causal conv with ``2 * pt`` zero frames in front (``kd - 1``
+for a one-frame input) and a reflect border of ``ph`` / ``pw`` on every side,
+or of one row and one column at the far edges when ``right_bottom_only`` is
+set (the stride-2 downsample convs).  This build wraps ``conv_in``, every
+downsample conv of the prefix and of the suffix stages the same way.
 """
 from __future__ import annotations
 
-import torch
-import torch.nn.functional as F
+from dataclasses import dataclass
 
-from .encoder_fp16_conv import native_device, padded_causal_conv3d
+import torch
+
+from .encoder_fp16_conv import PaddedCausalConv
+
+
+def _reflect_border(conv):
+    """(top, bottom, left, right) reflect rows / columns the model pads around a frame."""
+    _, ph, pw = conv.padding
+    if getattr(conv, "right_bottom_only", False):
+        return (0, 1, 0, 1)
+    return (ph, ph, pw, pw)
 
 
 class ImplicitTemporalPadConv3d(torch.nn.Module):
+    """A causal zero-time / reflect-space padded conv of the model, run as pack + native conv."""
+
     def __init__(self, original):
         super().__init__()
-        if not (getattr(original, "causal", False) and getattr(original, "pad_mode_t", None) == "constant"
-                and not getattr(original, "spatial_parallel", False) and original.groups == 1
-                and original.dilation == (1, 1, 1) and original.padding[0] > 0):
+        supported = (getattr(original, "causal", False) and getattr(original, "pad_mode_t", None) == "constant"
+                     and getattr(original, "pad_mode", None) == "reflect"
+                     and not getattr(original, "spatial_parallel", False) and original.groups == 1
+                     and tuple(original.dilation) == (1, 1, 1) and original.padding[0] > 0)
+        if not supported:
             raise ValueError("Only single-GPU causal zero-temporal-padding convolutions are supported")
-        self.weight = original.weight
-        self.bias = original.bias
-        self.padding = original.padding
-        self.stride = original.stride
-        self.kernel_size = original.kernel_size
+        self.weight, self.bias = original.weight, original.bias
+        self.kernel_size, self.stride, self.padding = tuple(original.kernel_size), tuple(original.stride), \
+            tuple(original.padding)
         self.pad_mode = original.pad_mode
+        # zero frames in front of a clip / of a single image
+        self.front_video, self.front_image = 2 * self.padding[0], self.kernel_size[0] - 1
+        self.native = PaddedCausalConv(self.weight, self.bias, self.stride, _reflect_border(original))
 
     def forward(self, x):
-        depth = x.shape[2]
-        left = 2 * self.padding[0] if depth > 1 else self.kernel_size[0] - 1
-        output_depth = (depth + left - self.kernel_size[0]) // self.stride[0] + 1
-        ph, pw = self.padding[1:]
-        if self.pad_mode == "reflect" and native_device(x):
-            return padded_causal_conv3d(x, self.weight, self.bias, self.stride, left, ph, ph, pw, pw)
-        if ph or pw:
-            x = F.pad(x, (pw, pw, ph, ph, 0, 0), mode=self.pad_mode)
-        y = F.conv3d(x, self.weight, self.bias, stride=self.stride, padding=(left, 0, 0))
-        return y[:, :, :output_depth]
+        return self.native(x, self.front_video if x.shape[2] > 1 else self.front_image)
+
+
+@dataclass
+class _Swap:
+    owner: torch.nn.Module
+    name: str
+    original: torch.nn.Module
+
+    def undo(self):
+        self.owner._modules[self.name] = self.original
 
 
 def replace_selected(encoder, names):
-    replacements = []
-    for name in names:
-        parent_path, _, leaf = name.rpartition(".")
-        parent = encoder.get_submodule(parent_path) if parent_path else encoder
-        original = getattr(parent, leaf)
-        setattr(parent, leaf, ImplicitTemporalPadConv3d(original))
-        replacements.append((parent, leaf, original))
-    return replacements
+    """Wrap the named convs of ``encoder`` in place; -> handles for ``restore_selected``."""
+    swaps = []
+    for path in names:
+        *owner_path, leaf = path.split(".")
+        owner = encoder.get_submodule(".".join(owner_path))
+        swaps.append(_Swap(owner, leaf, owner._modules[leaf]))
+        owner._modules[leaf] = ImplicitTemporalPadConv3d(swaps[-1].original)
+    return swaps
 
 
 def restore_selected(replacements):
-    for parent, leaf, original in replacements:
-        setattr(parent, leaf, original)
+    for swap in reversed(replacements):
+        swap.undo()

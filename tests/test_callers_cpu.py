@@ -18,7 +18,8 @@ import h3_arch
 
 @pytest.fixture(scope="module")
 def mods(pkg):
-    names = ["int8_qkv", "int8_attention_out", "int8_norm1_quant", "decoder_fused_qk_rope", "encoder_fused_norm_bias",
+    names = ["int8_qkv", "int8_attention_out", "int8_norm1_quant", "decoder_int8", "_modules", "decoder_fused_qk_rope",
+             "encoder_fused_norm_bias",
              "encoder_fused_residual_pack", "encoder_fused_norm_next", "encoder_staged_batch",
              "encoder_internal_padding", "encoder_int8_integration"]
     return {n: importlib.import_module(f"{pkg.__name__}.opt.{n}") for n in names}
@@ -36,10 +37,10 @@ def _block(width=2048):
 
 # -- N6 / O1 install helpers (reference tests/test_int8_qkv.py, tests/test_int8_attention_out.py) ----------
 
-def test_selected_indices(mods):
-    sel = mods["int8_qkv"].selected_indices
-    assert sel(36) == tuple(range(36))
-    assert sel(36, [3, 7]) == (3, 7)
+def test_chosen_blocks(mods):
+    sel = mods["decoder_int8"].chosen_blocks
+    assert sel(36) == list(range(36))
+    assert sel(36, [3, 7]) == [3, 7]
     for bad in ([], [1, 1], [-1], [36], [True], [1.0]):
         with pytest.raises(ValueError):
             sel(36, bad)
@@ -64,8 +65,9 @@ def test_qkv_and_out_linear_validation(mods):
         out_linear(block)
 
 
-def test_clone_containers_alias_and_sharing(mods):
-    clone_containers = mods["int8_attention_out"].clone_containers
+def test_share_containers_alias_and_sharing(mods):
+    clone_containers = mods["_modules"].share_containers
+    assert mods["int8_attention_out"].clone_containers is clone_containers
     raw = _block()
     raw.alias = raw.attn
     raw.register_buffer("probe", torch.ones(2))
@@ -86,7 +88,7 @@ def test_qkv_replacement_scope_original_untouched(mods):
     clone = copy.deepcopy(raw)
     replacement = torch.nn.Identity()
     with patch.object(m, "clone_norm_quant_decoder", return_value=clone), \
-            patch.object(m, "KitchenInt8Linear", return_value=replacement) as factory:
+            patch.object(mods["decoder_int8"], "KitchenInt8Linear", return_value=replacement) as factory:
         result = m.clone_qkv_int8_decoder(raw, indices=[1])
     assert isinstance(raw.transformer_blocks[1].attn.original.to_qkv, torch.nn.Linear)
     assert isinstance(result.transformer_blocks[0].attn.original.to_qkv, torch.nn.Linear)
@@ -100,7 +102,7 @@ def test_out_replacement_scope_original_untouched(mods):
     raw.transformer_blocks = torch.nn.ModuleList([_block(), _block()])
     raw.eval()
     replacement = torch.nn.Identity()
-    with patch.object(m, "KitchenInt8Linear", return_value=replacement) as factory:
+    with patch.object(mods["decoder_int8"], "KitchenInt8Linear", return_value=replacement) as factory:
         result = m.clone_attention_out_decoder(raw, indices=[1])
     for i in range(2):
         assert isinstance(raw.transformer_blocks[i].attn.original.to_out, torch.nn.Linear)
@@ -114,9 +116,8 @@ def test_out_replacement_scope_original_untouched(mods):
 # -- N5 carry protocol (reference tests/test_int8_norm1_quant.py) -------------------------------------------
 
 def test_final_adapter_shares_parameters_and_keeps_tensor_path(mods):
-    n1 = mods["int8_norm1_quant"]
     source = torch.nn.LayerNorm(2048, eps=1e-5, dtype=torch.float16).eval()
-    adapter = n1._FinalNormAdapter(source).eval()
+    adapter = mods["decoder_int8"].CarryLayerNorm(source).eval()
     assert set(adapter.state_dict()) == set(source.state_dict())
     assert adapter.weight is source.weight and adapter.bias is source.bias
     with torch.inference_mode():
@@ -128,9 +129,9 @@ def test_final_adapter_shares_parameters_and_keeps_tensor_path(mods):
 
 
 def test_carry_unpad_rules(mods):
-    n1 = mods["int8_norm1_quant"]
+    carry_unpad = mods["decoder_int8"].carry_unpad
     original = Mock(side_effect=lambda states, pad: states)
-    unpad = n1._carry_safe_unpad(original)
+    unpad = carry_unpad(original)
     carry = (object(), object(), object())
     assert unpad(carry, 0) is carry
     original.reset_mock()
@@ -141,7 +142,7 @@ def test_carry_unpad_rules(mods):
     assert unpad(tensor, 1) is tensor
     original.assert_called_once_with(tensor, 1)
     with pytest.raises(RuntimeError, match="preserve final residual carry"):
-        n1._carry_safe_unpad(lambda s, p: tuple(list(s)))((object(), object(), object()), 0)
+        carry_unpad(lambda s, p: tuple(list(s)))((object(), object(), object()), 0)
 
 
 def test_norm1_platform_gate_and_disabled_clone(mods):
@@ -164,9 +165,10 @@ def test_qk_fusion_clone_wraps_every_attention(mods):
     assert all(type(b.attn) is qk.FusedQKAttention for b in fused.transformer_blocks)
     assert all(type(b.attn) is h3_arch.H3Attention for b in dec.transformer_blocks)
     assert fused.transformer_blocks[1].attn.original is dec.transformer_blocks[1].attn
-    assert mods["int8_norm1_quant"]._qk_rope_for(fused.transformer_blocks[0].attn) is qk.qk_rope
-    with pytest.raises(ValueError):
-        mods["int8_norm1_quant"]._qk_rope_for(dec.transformer_blocks[0].attn)
+    int8_block = mods["decoder_int8"].Int8Block
+    assert int8_block(fused.transformer_blocks[0], carry=True)._rope is qk.qk_rope
+    with pytest.raises(ValueError, match="FusedQKAttention"):
+        int8_block(dec.transformer_blocks[0], carry=True)
 
 
 # -- E9 / C1 encoder wiring ---------------------------------------------------------------------------------
@@ -195,20 +197,30 @@ def test_prefix_structure_and_int8_policy(mods):
         mods["encoder_fused_norm_next"].next_fused_prefix(enc, "extend")
 
 
-def test_implicit_temporal_pad_matches_causal_conv(mods):
+def test_implicit_temporal_pad_geometry_and_no_cpu_fallback(mods):
+    """The wrapper reads the model's padding (2*pt zero frames in front, kd-1 for one frame; a reflect
+    border of ph/pw, or right/bottom only) and runs only on the GPU: a CPU input raises."""
+    ip = mods["encoder_internal_padding"]
     torch.manual_seed(3)
     conv = h3_arch.CausalConv3d(8, 8, 3, stride=(1, 2, 2), padding=(1, 1, 1)).double()
-    x = torch.randn(1, 8, 5, 10, 12, dtype=torch.float64)
-    implicit = mods["encoder_internal_padding"].ImplicitTemporalPadConv3d(conv)
-    assert torch.allclose(implicit(x), conv(x), rtol=0, atol=1e-12)
-    x1 = x[:, :, :1]
-    assert torch.allclose(implicit(x1), conv(x1), rtol=0, atol=1e-12)
+    implicit = ip.ImplicitTemporalPadConv3d(conv)
+    assert (implicit.front_video, implicit.front_image) == (2, 2)
+    assert implicit.native.border == (1, 1, 1, 1) and implicit.native.stride == (1, 2, 2)
+    down = h3_arch.Downsample(8, (2, 2, 2), (1, 0, 0), right_bottom=True)
+    assert ip.ImplicitTemporalPadConv3d(down.conv).native.border == (0, 1, 0, 1)
+    conv_in = h3_arch.CausalConv3d(3, 16)
+    assert ip.ImplicitTemporalPadConv3d(conv_in).native.folded
+    with pytest.raises(RuntimeError, match="gfx950"):
+        implicit(torch.randn(1, 8, 5, 10, 12, dtype=torch.float64))
+    flat = h3_arch.CausalConv3d(8, 8, 3, padding=(0, 1, 1))
+    with pytest.raises(ValueError, match="causal zero-temporal-padding"):
+        ip.ImplicitTemporalPadConv3d(flat)
     parent = torch.nn.Module()
     parent.child = torch.nn.Module()
     parent.child.conv = conv
-    rep = mods["encoder_internal_padding"].replace_selected(parent, ["child.conv"])
+    rep = ip.replace_selected(parent, ["child.conv"])
     assert type(parent.child.conv).__name__ == "ImplicitTemporalPadConv3d"
-    mods["encoder_internal_padding"].restore_selected(rep)
+    ip.restore_selected(rep)
     assert parent.child.conv is conv
 
 

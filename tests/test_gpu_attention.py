@@ -39,9 +39,11 @@ def _check(ops, oracle, q, k, v, out, queries=None):
 
 
 @pytest.mark.parametrize("b,n,h", [(1, 1, 1), (1, 2, 2), (2, 63, 1), (1, 64, 2), (3, 65, 1), (1, 129, 2),
-                                   (2, 200, 3)])
+                                   (2, 200, 3), (1, 513, 1), (2, 1025, 1), (1, 1100, 2), (1, 1537, 1)])
 def test_attention_small_shapes_match_oracle(ops, oracle, b, n, h):
-    """Key-block (64) and query-block (128) edges, one token, odd batches and heads."""
+    """Key-block (64) and wave (64 queries) edges, and the workgroup edges: a workgroup holds 8 waves of 64
+    queries (512), so 513, 1025, 1100 and 1537 tokens put ragged workgroups after full ones; one token, odd
+    batches and heads.  Every query is checked."""
     q, k, v, qd, kd, vd = _qkv(b, n, h, seed=b * 1000 + n * 10 + h)
     with torch.inference_mode():
         out = ops.decoder_fused_qk_rope.attention_d64(qd, kd, vd, 0.125)
@@ -59,7 +61,9 @@ def test_attention_h3_shape_sampled(ops, oracle):
         out = ops.decoder_fused_qk_rope.attention_d64(qd, kd, vd, 0.125)
     torch.cuda.synchronize()
     rng = np.random.default_rng(5)
-    queries = np.unique(np.concatenate([[0, 1, 127, 128, 1791, 1792, 1795, 1796], rng.integers(0, n, 40)]))
+    # workgroup (512-query) and wave (64-query) edges, the ragged tail, random others
+    edges = [0, 1, 63, 64, 127, 128, 511, 512, 1023, 1024, 1535, 1536, 1791, 1792, 1795, 1796]
+    queries = np.unique(np.concatenate([edges, rng.integers(0, n, 40)]))
     _check(ops, oracle, q, k, v, out, queries)
 
 
@@ -84,7 +88,8 @@ def test_attention_cfg4_sampled_and_against_torch_sdpa(ops, oracle):
             qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2).contiguous(), scale=0.125).transpose(1, 2)
     torch.cuda.synchronize()
     rng = np.random.default_rng(6)
-    queries = np.unique(np.concatenate([[0, 16383], rng.integers(0, n, 24)]))
+    edges = [0, 511, 512, 8191, 8192, 16383]
+    queries = np.unique(np.concatenate([edges, rng.integers(0, n, 24)]))
     _check(ops, oracle, q, k, v, out, queries)
     assert float((out.float() - sdpa.float()).abs().max()) < 4e-3
 

@@ -88,8 +88,7 @@ def test_bias_fused_block_matches_oracle(int8_prefix, mods, oracle, where):
     x = _cl(torch.randn(1, cin, 5, hw, hw, generator=gen).half().to(DEV))
     with torch.inference_mode():
         y = block(x)
-        shortcut = (mods["encoder_fp16_conv"].pointwise_conv3d(x, block.shortcut) if block.shortcut is not None
-                    else x)
+        shortcut = block.shortcut_conv(x) if block.shortcut_conv is not None else x
         torch.cuda.synchronize()
     h2 = _oracle_body(oracle, block, ndhwc(x)[0])
     want = (ndhwc(shortcut)[0].astype(np.float32) + h2.astype(np.float32)).astype(np.float16)
@@ -107,7 +106,7 @@ def test_residual_downsample_block_matches_oracle(int8_prefix, mods, oracle):
         body = block._residual_body(x, None)
         pk = mods["encoder_fused_residual_pack"].residual_downsample_pack(body, x, block.second.bias)
         # the FP16 downsample conv on the very same tensor
-        conv = mods["encoder_fp16_conv"].valid_conv3d(pk, block.down_weight, block.down_bias, (2, 2, 2))
+        conv = block.down(pk)
         torch.cuda.synchronize()
     h2 = _oracle_body(oracle, block, ndhwc(x)[0])
     assert_bitwise(ndhwc(body)[0], h2, "residual body")

@@ -271,11 +271,12 @@ def test_batched_residual_block_with_native_convs(bn, fc, cin, cout, hw):
 
 
 def test_batched_suffix_all_stages_matches_model_suffix(pkg, bn):
-    """The runtime's suffix (BatchedSuffix over every suffix stage, norm_out and conv_out) on a staged batch of
-    4 clips == the model's own suffix modules clip by clip, at the tile-256 suffix shape [4, 256, 9, 64, 64]."""
+    """The runtime's suffix (BatchedSuffix over every suffix stage of the H3 encoder: its residual blocks,
+    stride-(2,2,2) and (1,2,2) downsamples, norm_out, conv_out and quant_conv) on a staged batch of 4 clips ==
+    the model's own suffix modules clip by clip, at the tile-256 suffix shape [4, 256, 9, 64, 64]."""
     staged = importlib.import_module(f"{pkg.__name__}.opt.encoder_staged_batch")
     torch.manual_seed(7)
-    enc = h3_arch.H3Encoder().half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
+    enc = h3_arch.H3Encoder(h3_arch.H3_ENCODER_STAGES).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
     quant = torch.nn.Conv3d(48, 48, 1).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
     gen = torch.Generator().manual_seed(8)
     x = torch.randn(4, 256, 9, 64, 64, generator=gen).half().to(DEV).contiguous(memory_format=torch.channels_last_3d)
@@ -285,6 +286,6 @@ def test_batched_suffix_all_stages_matches_model_suffix(pkg, bn):
         ref = torch.cat([model(x[i:i + 1]) for i in range(4)])
         y = fused(x)
         torch.cuda.synchronize()
-    assert y.shape == ref.shape == (4, 48, 9, 64, 64)
+    assert y.shape == ref.shape == (4, 48, 5, 16, 16)
     rel = (y.float() - ref.float()).norm() / ref.float().norm()
     assert rel < 5e-3, float(rel)

@@ -166,6 +166,85 @@ def test_swiglu_gemm_zero_input_bias_contract(ops, oracle, magnitude):
         assert (gq == -128).all() and (gs == np.float32(1e-30)).all()
 
 
+# one fused multiply-add in the G1 / F2 epilogues: acc = 3, sx = 1, sw = 5616981 * 2^-24, b = 2^-23 gives
+# fp16 1 + 4*2^-10 with one rounding and 1 + 5*2^-10 with the product rounded first (closed form in
+# tests/test_oracle_pins.py, test_fma_case_is_what_the_comment_says)
+FMA_SW, FMA_B = 5616981 * 2.0 ** -24, 2.0 ** -23
+FMA_ONE, TWO_ROUNDINGS = 1 + 4 * 2.0 ** -10, 1 + 5 * 2.0 ** -10
+
+
+def _ones_prefix(rows, k, width=3):
+    t = torch.zeros((rows, k), dtype=torch.int8)
+    t[:, :width] = 1
+    return t
+
+
+@pytest.mark.parametrize("m,n,k", [(300, 256, 1024), (7188, 2048, 2048), (64, 6144, 2048)])
+def test_gemm_dequant_epilogue_is_one_fma(ops, m, n, k):
+    print(f"dequant epilogue fma m={m} n={n} k={k}", flush=True)
+    a, w = _ones_prefix(m, k), _ones_prefix(n, k)
+    sx = torch.ones(m, dtype=torch.float32)
+    sw = torch.full((n,), FMA_SW, dtype=torch.float32)
+    b = torch.full((n,), FMA_B, dtype=torch.float16)
+    out = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) for t in (a, sx, w, sw, b)]
+    ops.hip.call("h3v_gemm_i8_dequant", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(out), m, n, k, ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    got = np_(out)
+    assert (got == np.float16(FMA_ONE)).all(), np.unique(got)[:5]
+
+
+def test_swiglu_gemm_epilogue_is_one_fma_per_column(ops):
+    """Gate / up weight rows in reference order: pairs c < 128 have gate = 32 (bias only, SiLU(32) = 32
+    exactly) and up = the fma case, so act = 32 * (1 + 4*2^-10); pairs c >= 128 have gate = the fma case and
+    up = 1, so act = fp16(SiLU(1 + 4*2^-10)) = 0.735 (over a thousand fp32 ulps from an fp16 boundary)."""
+    m, nh, k = 129, 256, 2048
+    q = _ones_prefix(m, k)
+    w = torch.zeros((2 * nh, k), dtype=torch.int8)
+    w[nh:nh + 128, :3] = 1            # up rows of pairs 0..127
+    w[128:nh, :3] = 1                 # gate rows of pairs 128..255
+    sw = torch.ones(2 * nh, dtype=torch.float32)
+    sw[nh:nh + 128] = FMA_SW
+    sw[128:nh] = FMA_SW
+    b = torch.zeros(2 * nh, dtype=torch.float16)
+    b[:128], b[nh:nh + 128] = 32.0, FMA_B
+    b[128:nh], b[nh + 128:] = FMA_B, 1.0
+    scale = torch.ones((m, 1), dtype=torch.float32)
+    act = torch.empty((m, nh), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) for t in (q, scale, w, sw, b)]
+    ops.hip.call("h3v_gemm_i8_swiglu", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(act), m, nh, k, ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    got = np_(act)
+    assert (got[:, :128] == np.float16(32 * FMA_ONE)).all(), np.unique(got[:, :128])[:5]
+    silu_one = np.float16(FMA_ONE / (1 + np.exp(-FMA_ONE)))
+    assert silu_one != np.float16(TWO_ROUNDINGS / (1 + np.exp(-TWO_ROUNDINGS)))
+    assert (got[:, 128:] == silu_one).all(), np.unique(got[:, 128:])[:5]
+
+
+@pytest.mark.parametrize("name,m,n,k", [("cfg2 qkv", 16384, 3072, 1024), ("cfg3 up", 16384, 8192, 1024),
+                                        ("cfg3 down", 16384, 1024, 4096), ("cfg4 out", 16384, 1024, 1024),
+                                        ("H3 ffn-up", 7188, 16384, 2048)])
+def test_gemm_dequant_full_size_sampled_rows(ops, oracle, name, m, n, k):
+    """BASELINE configs 2-4 (and the H3 FFN-up) at full M: the fp16 epilogue of sampled rows (every M tile,
+    the first and last rows) bit for bit against the oracle."""
+    print(f"dequant full size {name}: {m} x {n} x {k}", flush=True)
+    gen = _gen(m + n + k)
+    a = torch.randint(-127, 128, (m, k), generator=gen, dtype=torch.int8)
+    w = torch.randint(-31, 32, (n, k), generator=gen, dtype=torch.int8)
+    sx = (torch.rand(m, generator=gen) * 0.02 + 0.001).float()
+    sw = (torch.rand(n, generator=gen) * 0.002 + 0.0001).float()
+    bias = (0.02 * torch.randn(n, generator=gen)).half()
+    out = torch.empty((m, n), dtype=torch.float16, device=DEV)
+    dev = [t.to(DEV) for t in (a, sx, w, sw, bias)]
+    ops.hip.call("h3v_gemm_i8_dequant", *[ops.hip.ptr(t) for t in dev], ops.hip.ptr(out), m, n, k, ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, m, 257), np.arange(m - 8, m), np.arange(0, 8)]))
+    got = np_(out)[rows]
+    want = oracle.gemm_dequant(oracle.gemm_acc(a.numpy()[rows], w.numpy()), sx.numpy()[rows], sw.numpy(),
+                               bias.numpy())
+    assert_bitwise(got, want, name)
+
+
 def _tensor_quant_gpu(ops, x):
     xd = x.to(DEV).contiguous()
     q = torch.empty(x.shape, dtype=torch.int8, device=DEV)

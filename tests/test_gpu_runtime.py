@@ -1,10 +1,18 @@
-"""GPU: the runtime's encoder wiring end to end on a reconstructed H3 core (tests/h3_arch.py).
+"""GPU: H3VAEPyOptRuntime end to end on a reconstructed H3 core (comfyui-h3vae-pyopt_amd/reconstructed_h3.py).
 
-H3VAEPyOptRuntime is built around the core exactly as for the real model: internal-padding stage-0
-downsample, bias-fused prefix with the residual-pack downsample, INT8 prefix convolutions (int8_encode),
-the clip-batched fused suffix (all stages) and staged clip batching.  Its encode must match the model's own
-modules run through the same staged routine: within FP16 reduction-order differences in FP16 mode, within
-the INT8 quantisation error in INT8 mode.  One, two and three 17-frame clips cover suffix batches 1, 2, 3.
+The runtime is built around the core exactly as around the MiniMax model: packed-padding conv_in and
+downsamples, the bias-fused prefix with the residual-pack downsample, INT8 prefix convolutions
+(int8_encode), the clip-batched native suffix, staged clip batching; on the decoder side fused QK-RoPE,
+INT8 linears (int8_decode), the fused carry chain (decode_fusions), tile batching.  Its results must match
+the core's own FP16 modules run through the same routines:
+
+* encode: within FP16 reduction-order differences (relative L2 1e-2) in FP16 mode, within the INT8
+  quantisation error (0.1) in INT8 mode; one, two and three clips (suffix batches of 1, 2, 3);
+* tiled encode (2 x 2 and 2 x 3 tiles): the model's modules on the same tiles, stitched by a literal
+  restatement of the reference's nested blend loop (h3vae_runtime.py:609-639), within the same bounds;
+* decode: latent t = 1, 2, 7 and 12 (a 2-chunk video) over 2 x 2 tiles, tile batch 1 and 2, with and
+  without decode_fusions: fp32 pixels within relative L2 0.05 of the core's FP16 decode finalised in
+  float32; a matching fp32 output_buffer is written in place and returned.
 """
 from __future__ import annotations
 
@@ -21,26 +29,13 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-class _Core(nn.Module):
-    """The parts of the klvae core the runtime touches on encode (decode is not called here)."""
-
-    def __init__(self):
-        super().__init__()
-        self.encoder = h3_arch.H3Encoder()
-        self.quant_conv = nn.Conv3d(48, 48, 1)
-        self.decoder = h3_arch.H3Decoder(dim=256, hidden=512, depth=1)
-        self.clip_length, self.token_drop, self.vae_ratio, self.tile_overlap_min = 17, 3, 16, 64
-        self.tile_size, self.decoder_tile_size, self.stack_tiling = 672, 256, False
-
-    def _run_tile_tasks(self, tiles, indices, forward_fn, stack_tiling, cls_agg=None):
-        raise AssertionError("decode is not part of this test")
-
-    def blend(self, a, b, extent, dim):
-        raise AssertionError("a single spatial tile needs no blend")
-
-
 def _config():
     return {"latents_mean": [0.05 * i for i in range(24)], "latents_std": [1.0 + 0.02 * i for i in range(24)]}
+
+
+def _core(seed, dim=256, hidden=512, depth=1):
+    torch.manual_seed(seed)
+    return h3_arch.H3Core(h3_arch.H3Encoder(), h3_arch.H3Decoder(dim=dim, hidden=hidden, depth=depth)).eval()
 
 
 @pytest.fixture(scope="module")
@@ -48,14 +43,49 @@ def rt(pkg):
     return importlib.import_module(f"{pkg.__name__}.h3vae_runtime")
 
 
+@pytest.fixture(scope="module")
+def staged(pkg):
+    return importlib.import_module(f"{pkg.__name__}.opt.encoder_staged_batch")
+
+
+def _model_moments(staged, enc, quant, normed):
+    """The model's own modules through the staged routine (reference opt/encoder_staged_batch.py:39-57)."""
+    if normed.shape[2] == 1:
+        return staged.EncoderSuffix(enc, quant, 2)(staged.EncoderPrefix(enc, 2)(normed))[:, :, -1:]
+    return staged.encode_staged(normed, staged.EncoderPrefix(enc, 2), staged.EncoderSuffix(enc, quant, 2),
+                                clip_length=17, token_drop=3, batch_size=4, cut=2)
+
+
+def _reference_stitch(rows, y_over, x_over, blend):
+    """The reference's nested row / column blend and crop loop, restated literally."""
+    result_rows = []
+    for i, row in enumerate(rows):
+        result_row = []
+        for j, tile in enumerate(row):
+            if i:
+                tile = blend(rows[i - 1][j], tile, y_over[i - 1], dim=-2)
+            if j:
+                tile = blend(row[j - 1], tile, x_over[j - 1], dim=-1)
+            if i < len(rows) - 1:
+                tile = tile[..., :-y_over[i], :]
+            if j < len(row) - 1:
+                tile = tile[..., :, :-x_over[j]]
+            result_row.append(tile)
+        result_rows.append(torch.cat(result_row, dim=-1))
+    return torch.cat(result_rows, dim=-2)
+
+
+def _reference_models(core):
+    enc = copy.deepcopy(core.encoder).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
+    quant = copy.deepcopy(core.quant_conv).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
+    return enc, quant
+
+
 @pytest.mark.parametrize("int8_encode,clips", [(False, 1), (False, 2), (True, 3), (True, 2)])
-def test_runtime_encode_matches_model_modules(rt, pkg, int8_encode, clips):
+def test_runtime_encode_matches_model_modules(rt, staged, int8_encode, clips):
     print(f"runtime encode int8_encode={int8_encode} clips={clips}", flush=True)
-    staged = importlib.import_module(f"{pkg.__name__}.opt.encoder_staged_batch")
-    torch.manual_seed(11)
-    core = _Core().eval()
-    ref_enc = copy.deepcopy(core.encoder).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
-    ref_quant = copy.deepcopy(core.quant_conv).half().to(DEV).eval().to(memory_format=torch.channels_last_3d)
+    core = _core(11)
+    enc, quant = _reference_models(core)
     # the INT8 two-clip case builds the runtime under inference mode (its weights become inference tensors)
     with torch.inference_mode(int8_encode and clips == 2):
         runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, int8_encode=int8_encode,
@@ -64,12 +94,92 @@ def test_runtime_encode_matches_model_modules(rt, pkg, int8_encode, clips):
     x = (torch.rand(1, 3, 17 * clips, 64, 64, generator=gen) * 2 - 1).half().to(DEV)
     with torch.inference_mode():
         latents = runtime.encode(x)
-        normed = runtime._normalize_pixels(x)
-        moments = staged.encode_staged(normed, staged.EncoderPrefix(ref_enc, 2), staged.EncoderSuffix(ref_enc, ref_quant, 2),
-                                       clip_length=17, token_drop=3, batch_size=4, cut=2)
+        moments = _model_moments(staged, enc, quant, runtime._normalize_pixels(x))
         want = (moments.float()[:, :24] - runtime.latents_mean.float()) / runtime.latents_std.float()
         torch.cuda.synchronize()
     assert latents.shape == want.shape == (1, 24, 9 * clips - 3, 16, 16)
     assert torch.isfinite(latents).all()
     rel = float((latents - want).norm() / want.norm())
     assert rel < (0.1 if int8_encode else 1e-2), rel
+
+
+@pytest.mark.parametrize("int8_encode,frames,hw", [(True, 1, (192, 192)), (True, 5, (192, 256)),
+                                                    (False, 22, (192, 192)), (True, 22, (192, 192)),
+                                                    (True, 124, (192, 192))])
+def test_runtime_tiled_encode_matches_model_modules(rt, staged, int8_encode, frames, hw):
+    """The full H3 encoder (16x spatial, 4x temporal); tile 128 with the core's 64-pixel minimum overlap:
+    192 px -> 2 tiles (overlap 64), 256 px -> 3 tiles.  Latent t = 1, 2, 7, 7, 37."""
+    print(f"runtime tiled encode int8_encode={int8_encode} frames={frames} hw={hw}", flush=True)
+    torch.manual_seed(13)
+    core = h3_arch.H3Core(h3_arch.H3Encoder(h3_arch.H3_ENCODER_STAGES),
+                          h3_arch.H3Decoder(dim=256, hidden=512, depth=1)).eval()
+    enc, quant = _reference_models(core)
+    runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, int8_encode=int8_encode, encoder_tile_size=128,
+                                   encoder_staged_batch=4, log_calls=False, core=core, config=_config())
+    gen = torch.Generator().manual_seed(frames)
+    x = (torch.rand(1, 3, frames, *hw, generator=gen) * 2 - 1).half().to(DEV)
+    with torch.inference_mode():
+        latents = runtime.encode(x)
+        ys, hs, yo = runtime._split_encoder_tiles(hw[0], 128, 64, 16)
+        xs, ws, xo = runtime._split_encoder_tiles(hw[1], 128, 64, 16)
+        assert len(ys) >= 2 and len(xs) >= 2
+        rows = [[_model_moments(staged, enc, quant, runtime._normalize_pixels(x[..., y:y + h, c:c + w]))
+                 for c, w in zip(xs, ws)] for y, h in zip(ys, hs)]
+        moments = _reference_stitch(rows, [o // 16 for o in yo], [o // 16 for o in xo], core.blend)
+        want = (moments.float()[:, :24] - runtime.latents_mean.float()) / runtime.latents_std.float()
+        torch.cuda.synchronize()
+    t = 1 if frames == 1 else 5 * (-(-frames // 17)) - 3
+    assert latents.shape == want.shape == (1, 24, t, hw[0] // 16, hw[1] // 16)
+    rel = float((latents - want).norm() / want.norm())
+    assert rel < (0.1 if int8_encode else 1e-2), rel
+
+
+def _finalize(raw, runtime):
+    return (raw.float() * runtime._img_std + runtime._img_mean).clamp(0.0, 1.0)
+
+
+@pytest.mark.parametrize("t", [1, 2, 7, 12])
+@pytest.mark.parametrize("tile_batch,fusions", [(1, False), (2, True), (4, True)])
+def test_runtime_decode_matches_fp16_model(rt, t, tile_batch, fusions):
+    print(f"runtime decode t={t} tile_batch={tile_batch} decode_fusions={fusions}", flush=True)
+    core = _core(17, dim=1024, hidden=2048, depth=3)
+    reference = copy.deepcopy(core).half().to(DEV).eval()
+    reference.decoder_tile_size = 256
+    runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, int8_decode=True, decode_fusions=fusions,
+                                   tile_batch=tile_batch, decoder_tile_size=256, log_calls=False, core=core,
+                                   config=_config())
+    gen = torch.Generator().manual_seed(t)
+    z = torch.randn(1, 24, t, 20, 20, generator=gen).half().to(DEV)     # 320 px: 2 x 2 tiles of 256
+    with torch.inference_mode():
+        out_shape = runtime.decode_output_shape(z.shape)
+        buffer = torch.full(out_shape, -1.0, device=DEV)
+        got = runtime.decode(z, output_buffer=buffer)
+        plain = runtime.decode(z)
+        zn = z * runtime.latents_std + runtime.latents_mean
+        if t == 1:
+            raw = reference.decode(zn)[:, :, -1:]
+        else:
+            zp = torch.cat([zn, zn[:, :, -1:].expand(-1, -1, 7 - t, -1, -1)], dim=2) if t < 7 else zn
+            raw = reference.decode_base(zp, frame_num=runtime._frames_from_tokens(t))
+        want = _finalize(raw, runtime)
+        torch.cuda.synchronize()
+    assert got is buffer and tuple(got.shape) == tuple(out_shape) == tuple(want.shape)
+    assert torch.equal(got, plain)
+    assert (got >= 0).all() and (got <= 1).all()
+    if tile_batch > 1 and t > 1:
+        assert core._last_tile_batch == tile_batch
+    rel = float((got - want).norm() / want.norm())
+    assert rel < 0.05, rel
+
+
+def test_runtime_decode_offload_frees_packed_and_int8_copies(rt):
+    """Moving the runtime to the CPU (ComfyUI's offload) leaves none of its tensors on the GPU."""
+    core = _core(19, dim=1024, hidden=2048, depth=1)
+    runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, int8_decode=True, int8_encode=True,
+                                   decode_fusions=True, log_calls=False, core=core, config=_config())
+    x = (torch.rand(1, 3, 17, 64, 64) * 2 - 1).half().to(DEV)
+    with torch.inference_mode():
+        runtime.encode(x)
+    runtime.to("cpu")
+    left = [name for name, t in list(runtime.named_parameters()) + list(runtime.named_buffers()) if t.is_cuda]
+    assert not left, left[:5]

@@ -471,3 +471,65 @@ def test_attention_against_torch_sdpa_float64(oracle):
     assert np.allclose(oracle.attention(q, k, v, 0.125), ref, rtol=1e-12, atol=1e-12)
     sub = oracle.attention(q, k, v, 0.125, queries=[0, 7, 28])
     assert np.array_equal(sub, oracle.attention(q, k, v, 0.125)[:, [0, 7, 28]])
+
+
+# ---------------------------------------------------------------------------
+# one fused multiply-add in the G1 / F2 epilogue: closed-form cases where it differs from two roundings
+# ---------------------------------------------------------------------------
+
+# acc = 3, sx = 1, sw = 5616981 * 2^-24, b = 2^-23: the exact value a*sw + b = 1 + 9*2^-11 + 2^-24 lies
+# half an fp32 ulp above an fp16 midpoint.  One rounding (fma) lands on that midpoint, which ties to the
+# even fp16 1 + 4*2^-10; rounding the product first (1 + 9*2^-11 - 2^-24 ties up to the midpoint) and
+# then adding b lands one fp32 ulp above it, which rounds to 1 + 5*2^-10.  (Found by exact rational
+# search over fp16 midpoints near 1; the same values drive the GPU epilogue tests.)
+FMA_ACC, FMA_SW, FMA_B = 3, np.float32(5616981 * 2.0 ** -24), np.float16(2.0 ** -23)
+FMA_ONE, TWO_ROUNDINGS = np.float16(1 + 4 * 2.0 ** -10), np.float16(1 + 5 * 2.0 ** -10)
+
+
+def _exact(x):
+    from fractions import Fraction
+    return Fraction(float(x))
+
+
+def test_fma_case_is_what_the_comment_says():
+    from fractions import Fraction
+    exact = _exact(FMA_ACC) * _exact(FMA_SW) + _exact(FMA_B)
+    assert exact == 1 + Fraction(9, 2 ** 11) + Fraction(1, 2 ** 24)
+    assert FMA_SW == np.float32(5616981 * 2.0 ** -24) and float(FMA_SW) * 2 ** 24 == 5616981
+    two = np.float16(np.float32(np.float32(FMA_ACC) * FMA_SW) + np.float32(FMA_B))
+    assert two == TWO_ROUNDINGS != FMA_ONE
+
+
+def test_gemm_dequant_rounds_once(oracle):
+    acc = np.full((2, 3), FMA_ACC, np.int32)
+    out = oracle.gemm_dequant(acc, np.ones(2, np.float32), np.full(3, FMA_SW, np.float32), np.full(3, FMA_B))
+    assert (out == FMA_ONE).all()
+    # without a bias the epilogue is (acc * sx) * sw, one rounding per product
+    plain = oracle.gemm_dequant(acc, np.ones(2, np.float32), np.full(3, FMA_SW, np.float32), None)
+    assert (plain == np.float16(np.float32(FMA_ACC) * FMA_SW)).all()
+
+
+def _silu64(g):
+    g = float(g)
+    return g / (1.0 + np.exp(-g))
+
+
+def test_gemm_swiglu_gate_and_up_round_once(oracle):
+    """[gate | up] columns in weight-row order; gate 32 makes SiLU(gate) exactly 32, so act = fp16(32 * up)
+    carries the up column's rounding unchanged; up 1.0 leaves act = fp16(SiLU(gate))."""
+    nh = 2
+    acc = np.zeros((1, 2 * nh), np.int32)
+    sw = np.ones(2 * nh, np.float32)
+    b = np.zeros(2 * nh, np.float16)
+    # pair 0: gate = 32 (bias only), up = the fma case
+    b[0], acc[0, nh], sw[nh], b[nh] = 32.0, FMA_ACC, FMA_SW, FMA_B
+    # pair 1: gate = the fma case, up = 1 (bias only)
+    acc[0, 1], sw[1], b[1], b[nh + 1] = FMA_ACC, FMA_SW, FMA_B, 1.0
+    act = oracle.gemm_swiglu(acc, np.ones(1, np.float32), sw, b)[0]
+    assert act[0] == np.float16(32 * float(FMA_ONE)) != np.float16(32 * float(TWO_ROUNDINGS))
+    # SiLU(1 + 4*2^-10) = 0.73468... lies over a thousand fp32 ulps from an fp16 rounding boundary, so any
+    # SiLU within a few fp32 ulps rounds to the same fp16 value; the two-rounding gate gives another one
+    want, wrong = np.float16(_silu64(FMA_ONE)), np.float16(_silu64(TWO_ROUNDINGS))
+    ulps = _silu64(FMA_ONE) / 2.0 ** -11
+    assert abs(ulps - np.floor(ulps) - 0.5) * 2.0 ** -11 > 64 * 2.0 ** -24
+    assert want != wrong and act[1] == want

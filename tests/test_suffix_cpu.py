@@ -1,5 +1,5 @@
-"""CPU checks of the FP16 encoder conv routing: the packed weight layout the kernel reads, the shape
-gate that picks h3v_conv3d_f16 over the model's F.conv3d, and the ops' host-side guards (meta tensors)."""
+"""CPU checks of the FP16 encoder convs: the packed weight layout the kernel reads, the shape gate of
+h3v_conv3d_f16, the packed copies' ownership, and the ops' host-side guards (meta tensors)."""
 from __future__ import annotations
 
 import importlib
@@ -75,39 +75,43 @@ def test_pack_op_guards_on_meta(fc):
         fc.causal_reflect_pack(x[:, :12], 2, 1, 1, 1, 1)
 
 
-def test_cpu_tensors_keep_the_model_convs(fc):
-    """Off the GPU the routing helpers are the model's own F.conv3d / F.pad calls."""
+def test_cpu_tensors_raise_no_fallback(fc):
+    """Off the GPU the native conv modules refuse to run: there is no second implementation."""
     gen = torch.Generator().manual_seed(1)
-    x = torch.randn(1, 32, 5, 6, 6, generator=gen)
-    w = torch.randn(64, 32, 3, 3, 3, generator=gen)
-    b = torch.randn(64, generator=gen)
-    F = torch.nn.functional
-    assert torch.equal(fc.valid_conv3d(x, w, b, (1, 2, 2)), F.conv3d(x, w, b, stride=(1, 2, 2)))
-    want = F.conv3d(F.pad(F.pad(x, (1, 1, 1, 1, 0, 0), mode="reflect"), (0, 0, 0, 0, 2, 0)), w, b, stride=(1, 2, 2))
-    assert torch.equal(fc.padded_causal_conv3d(x, w, b, (1, 2, 2), 2, 1, 1, 1, 1), want)
+    w = torch.nn.Parameter(torch.randn(64, 32, 3, 3, 3, generator=gen).half(), requires_grad=False)
+    conv = fc.NativeConv(w, None, (1, 2, 2))
+    with pytest.raises(RuntimeError, match="gfx950"):
+        conv(torch.randn(1, 32, 5, 6, 6, generator=gen).half())
+    padded = fc.PaddedCausalConv(w, None, (1, 2, 2), (1, 1, 1, 1))
+    with pytest.raises(RuntimeError, match="gfx950"):
+        padded(torch.randn(1, 32, 5, 6, 6, generator=gen).half(), 2)
+    point = fc.PointwiseConv(torch.nn.Conv3d(48, 48, 1).half())
+    with pytest.raises(RuntimeError, match="gfx950"):
+        point(torch.randn(1, 48, 2, 3, 3, generator=gen).half())
+    with pytest.raises(ValueError, match="1x1x1"):
+        fc.PointwiseConv(torch.nn.Conv3d(48, 48, 3))
 
 
-def test_packed_weight_cache_tracks_tensors(fc):
-    cache = fc._PackedWeights()
+def test_packed_weight_tracks_its_source_and_moves_with_its_owner(fc):
     gen = torch.Generator().manual_seed(3)
     w = torch.nn.Parameter(torch.randn(4, 32, 3, 3, 3, generator=gen).half(), requires_grad=False)
-    p1 = cache.get(w)
-    assert cache.get(w) is p1                                  # reused while unchanged
+    owner = torch.nn.Module()
+    owner.packed = fc.PackedConvWeight(w)
+    assert owner.packed.packed is None                         # nothing is packed before the first use
+    p1 = owner.packed(w)
+    assert owner.packed(w) is p1                               # reused while unchanged
+    assert torch.equal(p1, fc.pack_conv_weight_f16(w.detach()))
     with torch.no_grad():
         w.mul_(2)                                              # in-place update (a state-dict load) repacks
-    p2 = cache.get(w)
+    p2 = owner.packed(w)
     assert p2 is not p1 and torch.equal(p2, fc.pack_conv_weight_f16(w.detach()))
-    other = torch.nn.Parameter(w.detach().clone() + 1, requires_grad=False)
-    assert torch.equal(cache.get(other), fc.pack_conv_weight_f16(other.detach()))
+    assert "packed.packed" not in owner.state_dict()          # derived data: not saved
+    owner.to("meta")                                           # the copy moves (and is freed) with its owner
+    assert owner.packed.packed.device.type == "meta"
     with torch.inference_mode():                               # weights created under inference mode
         wi = torch.randn(4, 32, 3, 3, 3, generator=gen).half()
-        assert torch.equal(cache.get(wi), fc.pack_conv_weight_f16(wi))
-        assert cache.get(wi) is cache.get(wi)
-    n = len(cache._cache)
-    del other
-    import gc
-    gc.collect()
-    assert len(cache._cache) == n - 1                          # a copy lives only as long as its weight
+        folded = fc.PackedConvWeight(wi[:, :3], fold=True)
+        assert torch.equal(folded(wi[:, :3]), fc.fold_conv_weight_f16(wi[:, :3]))
 
 
 def test_folded_conv_in_weight_layout(fc):
