@@ -1,4 +1,4 @@
-"""Benchmark: full-VAE encode + decode of the H3 video VAE on one MI355X (BASELINE config 5).
+"""Benchmark: full-VAE encode + decode of the H3 video VAE on one MI355X (BASELINE.json config 5).
 
 One step = ``runtime.encode`` of a synthetic fp16 1x3x124x768x1344 clip, then
 ``runtime.decode`` of its latents into a preallocated fp32 pixel buffer, through
@@ -15,7 +15,7 @@ block with its attention, the output head and the pixel finalisation run.
   (M = 4 x 1797 = 7188 tokens, width 2048, 36 blocks), blending, finalisation.
 
 The dominant kernel's roofline (stage-0 INT8 conv) and the FFN-up GEMM's are
-timed with HIP events around their launches inside the timed steps.  BASELINE
+timed with HIP events around their launches inside the timed steps.  BASELINE.json
 configs 1-4 are timed on their own shapes afterwards, then a CPU baseline.
 
 Prints one JSON line (rank 0, N=1).  `--gpus N` with N > 1 exits: this build
@@ -55,7 +55,7 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-configs", action="store_true", help="skip the per-config (BASELINE configs 1-4) kernel timings")
+    p.add_argument("--no-configs", action="store_true", help="skip the per-config (BASELINE.json configs 1-4) kernel timings")
     p.add_argument("--vs-torch", action="store_true",
                    help="also time the model's F.conv3d (MIOpen) on the FP16 conv configs; its first call per shape "
                         "runs MIOpen's solver search, which takes minutes")
@@ -158,7 +158,7 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
         bias = randn(128, scale=0.1)
         qx = torch.empty(xn.numel(), device=dev, dtype=i8)
         xs = torch.empty(1, device=dev, dtype=f32)
-        amax = torch.empty(1, device=dev, dtype=torch.int32)
+        amax = torch.empty(int(hip.lib().h3v_tensor_quant_scratch_words()), device=dev, dtype=torch.int32)
         y = torch.empty((9, 64, 64, 128), device=dev, dtype=f16)
         t_q = timed(lambda: call("h3v_tensor_quant_i8", p(xn), xn.numel(), p(qx), p(xs), p(amax), stream))
         t_c = timed(lambda: call("h3v_conv3d_i8", p(qx), p(xs), p(qw), p(ws), p(bias), p(y), 1, 128, 11, 66, 66, 128,
@@ -358,7 +358,7 @@ def _median_s(fn, runs=5):
 
 
 def cpu_configs(rng, threads):
-    """BASELINE configs 1-4 through the CPU oracle (C, OpenMP): config 1 in full; configs 2-4, whose work is
+    """BASELINE.json configs 1-4 through the CPU oracle (C, OpenMP): config 1 in full; configs 2-4, whose work is
     independent per token row, on a row sample scaled to the full M (stated per entry).  Median of 5 runs
     after a warm-up.  Attention (config 4) is torch's CPU SDPA in fp32 on a query sample."""
     import numpy as np
@@ -743,7 +743,7 @@ def main():
     del runtime, clip, out
     torch.cuda.empty_cache()
     if not args.no_configs:
-        log("timing BASELINE configs 1-4 on their own shapes")
+        log("timing BASELINE.json configs 1-4 on their own shapes")
         result["configs"] = config_measurements(torch, hip, kitchen, enc, stream, vs_torch=args.vs_torch)
     if not args.no_cpu_baseline:
         log("timing the CPU oracle baseline sample")

@@ -61,6 +61,7 @@ SPECIAL: dict[str, tuple] = {
     "h3v_abi_version": (ctypes.c_int, []),
     "h3v_last_error": (ctypes.c_char_p, []),
     "h3v_gn_norm_pack_workspace_floats": (ctypes.c_int64, [_I, _I, _I]),
+    "h3v_tensor_quant_scratch_words": (ctypes.c_int64, []),
     "h3v_probe_mfma_ops_per_block": (ctypes.c_int64, [_I]),
     "h3v_gn_norm_pack_f16_workspace_floats": (ctypes.c_int64, [_I, _I, _I, _I, _I]),
 }

@@ -1041,6 +1041,12 @@ int run_gemm(GemmParams p, hipStream_t stream, const char* what) {
 template <Epi EP>
 int run_conv(GemmParams p, hipStream_t stream, const char* what) {
     const bool al = aligned(p.a, 16) && aligned(p.b, 16);
+    // A small conv whose 512 x 128 window tiles would occupy under half of the 256 CUs (a single
+    // 9 x 64 x 64 clip at 128 -> 128 channels: 36864 voxels = 72 tiles) runs as the implicit GEMM on
+    // 256 x 128 tiles of eight 64 x 64 wave blocks instead: twice the workgroups, 28.3 vs 36.7 us there.
+    const int64_t halo_tiles = ((int64_t)p.M / 512) * (p.N / 128);
+    if (al && p.C % 128 == 0 && halo_tiles < 128 && halo_conv_fits(p))
+        return launch_tiled<256, 128, 128, 4, 2, 2, 2, AMode::Conv, EP>(p, stream, what);
     if (halo_conv_fits(p)) {
         if (p.Wo == 256) return launch_halo<256, EP>(p, stream, what);
         if (p.Wo == 128) return launch_halo<128, EP>(p, stream, what);

@@ -8,8 +8,9 @@
 //    by the row divisor through the verified fast quotient (h3v_common.hpp);
 //  * SwiGLU + row quantizer (opt/int8_swiglu_fused.py:22-38);
 //  * per-tensor encoder activation quantizer (opt/encoder_int8.py:343-378):
-//    absmax pass with one atomic max per workgroup, then a quantize pass that
-//    derives the scale from the maximum on the fly.
+//    an absmax pass writing one partial per workgroup (no atomics, nothing to
+//    clear), then a quantize pass whose workgroups each fold the partials and
+//    derive the scale on the fly: two launches.
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
@@ -181,43 +182,58 @@ int launch_row_quant(const uint16_t* x, int64_t rows, int64_t k, int8_t* q, floa
 // ---------------------------------------------------------------------------
 // Per-tensor encoder activation quantization.
 // ---------------------------------------------------------------------------
-__global__ void fill_u32(uint32_t* p, uint32_t v) { *p = v; }
-
 constexpr int kTensorThreads = 256;
+constexpr int kTensorPartials = 1024;   // at most this many absmax partials (one per workgroup of pass 1)
 
-__global__ __launch_bounds__(kTensorThreads) void tensor_absmax(const uint16_t* __restrict__ x, int64_t n, bool vec,
-                                                                uint32_t* __restrict__ amax_bits) {
+// Pass 1: each workgroup's absmax over a grid-strided share of the tensor, written to partial[block]
+// (no atomics, nothing to clear first).  Four independent 16-byte loads in flight per lane.
+__global__ __launch_bounds__(kTensorThreads) void tensor_absmax_partial(const uint16_t* __restrict__ x, int64_t n,
+                                                                        bool vec, float* __restrict__ partial) {
     __shared__ float red[kTensorThreads / 64];
     float m = 0.0f;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t nvec = vec ? n / 8 : 0;
-    for (int64_t i = i0; i < nvec; i += stride) {
-        u16x8 a = *reinterpret_cast<const u16x8*>(x + i * 8);
+    const int64_t stride = (int64_t)gridDim.x * kTensorThreads;
+    const int64_t nvec = vec ? n / 8 : 0;
+    int64_t i = (int64_t)blockIdx.x * kTensorThreads + threadIdx.x;
+    for (; i + 3 * stride < nvec; i += 4 * stride) {
+        u16x8 a[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = *reinterpret_cast<const u16x8*>(x + (i + u * stride) * 8);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(a[u][e])));
+    }
+    for (; i < nvec; i += stride) {
+        const u16x8 a = *reinterpret_cast<const u16x8*>(x + i * 8);
 #pragma unroll
         for (int e = 0; e < 8; ++e) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(a[e])));
     }
-    for (int64_t i = nvec * 8 + i0; i < n; i += stride) m = __builtin_fmaxf(m, __builtin_fabsf(h2f(x[i])));
+    for (int64_t j = nvec * 8 + (int64_t)blockIdx.x * kTensorThreads + threadIdx.x; j < n; j += stride)
+        m = __builtin_fmaxf(m, __builtin_fabsf(h2f(x[j])));
     m = block_max(m, red);
-    // non-negative floats order like their bit patterns
-    if (threadIdx.x == 0) atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
+    if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
+// Pass 2: every workgroup folds the partials into the tensor absmax (a few KB from L2), derives the
+// scale, and quantizes its grid-strided share; workgroup 0 also stores the scale.
 __global__ __launch_bounds__(kTensorThreads) void tensor_quantize(const uint16_t* __restrict__ x, int64_t n, bool vec,
-                                                                  const uint32_t* __restrict__ amax_bits,
+                                                                  const float* __restrict__ partial, int nparts,
                                                                   int8_t* __restrict__ q, float* __restrict__ scale) {
-    const float s = e3_scale(__builtin_bit_cast(float, *amax_bits));
+    __shared__ float red[kTensorThreads / 64];
+    float m = 0.0f;
+    for (int p = threadIdx.x; p < nparts; p += kTensorThreads) m = __builtin_fmaxf(m, partial[p]);
+    const float s = e3_scale(block_max(m, red));
     if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
-    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-    int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    int64_t nvec = vec ? n / 8 : 0;
-    for (int64_t i = i0; i < nvec; i += stride) {
-        u16x8 a = *reinterpret_cast<const u16x8*>(x + i * 8);
+    const int64_t stride = (int64_t)gridDim.x * kTensorThreads;
+    const int64_t nvec = vec ? n / 8 : 0;
+    for (int64_t i = (int64_t)blockIdx.x * kTensorThreads + threadIdx.x; i < nvec; i += stride) {
+        const u16x8 a = *reinterpret_cast<const u16x8*>(x + i * 8);
         uint32_t lo = pack4(e3_quant(h2f(a[0]), s), e3_quant(h2f(a[1]), s), e3_quant(h2f(a[2]), s), e3_quant(h2f(a[3]), s));
         uint32_t hi = pack4(e3_quant(h2f(a[4]), s), e3_quant(h2f(a[5]), s), e3_quant(h2f(a[6]), s), e3_quant(h2f(a[7]), s));
         *reinterpret_cast<uint2*>(q + i * 8) = make_uint2(lo, hi);
     }
-    for (int64_t i = nvec * 8 + i0; i < n; i += stride) q[i] = (int8_t)e3_quant(h2f(x[i]), s);
+    for (int64_t j = nvec * 8 + (int64_t)blockIdx.x * kTensorThreads + threadIdx.x; j < n; j += stride)
+        q[j] = (int8_t)e3_quant(h2f(x[j]), s);
 }
 
 // ---------------------------------------------------------------------------
@@ -287,17 +303,23 @@ int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream) {
     return launch_status(what);
 }
 
-int h3v_tensor_quant_i8(const uint16_t* x, int64_t n, int8_t* q, float* scale, uint32_t* amax_scratch,
+int64_t h3v_tensor_quant_scratch_words(void) { return kTensorPartials; }
+
+int h3v_tensor_quant_i8(const uint16_t* x, int64_t n, int8_t* q, float* scale, uint32_t* scratch,
                         hipStream_t stream) {
     const char* what = "h3v_tensor_quant_i8";
-    H3V_REQUIRE(x && q && scale && amax_scratch, "%s: null pointer argument", what);
+    H3V_REQUIRE(x && q && scale && scratch, "%s: null pointer argument", what);
     H3V_REQUIRE(n > 0, "%s: activation quantization requires a nonempty tensor", what);
     const bool vec = aligned(x, 16) && aligned(q, 8);
-    int64_t want = (n / 8 + kTensorThreads - 1) / kTensorThreads;
-    unsigned blocks = (unsigned)(want < 1 ? 1 : (want > 8192 ? 8192 : want));
-    hipLaunchKernelGGL(fill_u32, dim3(1), dim3(1), 0, stream, amax_scratch, 0u);
-    hipLaunchKernelGGL(tensor_absmax, dim3(blocks), dim3(kTensorThreads), 0, stream, x, n, vec, amax_scratch);
-    hipLaunchKernelGGL(tensor_quantize, dim3(blocks), dim3(kTensorThreads), 0, stream, x, n, vec, amax_scratch, q,
+    const int64_t nvec = vec ? n / 8 : n / 8 + 1;
+    // pass 1: at least 8 vectors per lane; pass 2: at least 4 (it also writes)
+    const int64_t p1 = (nvec + 8 * kTensorThreads - 1) / (8 * kTensorThreads);
+    const int64_t p2 = (nvec + 4 * kTensorThreads - 1) / (4 * kTensorThreads);
+    const int parts = (int)(p1 < 1 ? 1 : (p1 > kTensorPartials ? kTensorPartials : p1));
+    const unsigned blocks = (unsigned)(p2 < 1 ? 1 : (p2 > 2048 ? 2048 : p2));
+    float* partial = reinterpret_cast<float*>(scratch);
+    hipLaunchKernelGGL(tensor_absmax_partial, dim3(parts), dim3(kTensorThreads), 0, stream, x, n, vec, partial);
+    hipLaunchKernelGGL(tensor_quantize, dim3(blocks), dim3(kTensorThreads), 0, stream, x, n, vec, partial, parts, q,
                        scale);
     return launch_status(what);
 }

@@ -5,8 +5,8 @@ Triton ``kernel`` / ``residual_quant`` (:16-69) is ``h3v_residual_rms_quant``:
 raw = fma(a, g, x); h = fp16(raw); inv = 1/sqrt(sum(raw^2)/K + eps) over a fixed
 reduction tree; act = fp16(h * inv * w); the comfy-kitchen row quantizer on
 act.  ``h3vae_norm_exp::residual_rms_linear`` feeds those rows to the INT8
-GEMM.  Row widths 1024, 2048 and 4096 (H3 uses 2048, BASELINE's synthetic
-configurations 1024).  ``clone_norm_quant_decoder`` (reference :87-136) builds
+GEMM.  Row widths 1024, 2048 and 4096 (H3 uses 2048, the synthetic benchmark
+shapes 1024).  ``clone_norm_quant_decoder`` (reference :87-136) builds
 ``decoder_int8.Int8Block`` blocks.
 """
 from __future__ import annotations

@@ -78,7 +78,7 @@ def test_attention_large_scores_online_max(ops, oracle):
 
 
 def test_attention_cfg4_sampled_and_against_torch_sdpa(ops, oracle):
-    """BASELINE config 4: one 256x256 tile, 16384 tokens x 16 heads; also compared with torch's SDPA."""
+    """BASELINE.json config 4: one 256x256 tile, 16384 tokens x 16 heads; also compared with torch's SDPA."""
     print("attention cfg4 [1, 16384, 16, 64]", flush=True)
     b, n, h = 1, 16384, 16
     q, k, v, qd, kd, vd = _qkv(b, n, h, seed=4)

@@ -50,6 +50,8 @@ CASES = [
     (256, 128, (1, 256, 3, 6, 130), (3, 3, 3), (1, 1, 1)),
     (128, 128, (1, 128, 4, 18, 34), (3, 3, 3), (1, 1, 1)),     # output width 32
     (256, 256, (3, 256, 5, 18, 34), (3, 3, 3), (1, 1, 1)),
+    # one padded 9 x 64 x 64 clip at 128 -> 128: 72 window tiles, so it runs on 256 x 128 implicit-GEMM tiles
+    (128, 128, (1, 128, 11, 66, 66), (3, 3, 3), (1, 1, 1)),
 ]
 
 

@@ -225,7 +225,7 @@ def test_swiglu_gemm_epilogue_is_one_fma_per_column(ops):
                                         ("cfg3 down", 16384, 1024, 4096), ("cfg4 out", 16384, 1024, 1024),
                                         ("H3 ffn-up", 7188, 16384, 2048)])
 def test_gemm_dequant_full_size_sampled_rows(ops, oracle, name, m, n, k):
-    """BASELINE configs 2-4 (and the H3 FFN-up) at full M: the fp16 epilogue of sampled rows (every M tile,
+    """BASELINE.json configs 2-4 (and the H3 FFN-up) at full M: the fp16 epilogue of sampled rows (every M tile,
     the first and last rows) bit for bit against the oracle."""
     print(f"dequant full size {name}: {m} x {n} x {k}", flush=True)
     gen = _gen(m + n + k)
@@ -249,7 +249,7 @@ def _tensor_quant_gpu(ops, x):
     xd = x.to(DEV).contiguous()
     q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
     s = torch.empty((), dtype=torch.float32, device=DEV)
-    scratch = torch.empty(1, dtype=torch.int32, device=DEV)
+    scratch = torch.full((int(ops.hip.lib().h3v_tensor_quant_scratch_words()),), -1, dtype=torch.int32, device=DEV)
     ops.hip.call("h3v_tensor_quant_i8", ops.hip.ptr(xd), x.numel(), ops.hip.ptr(q), ops.hip.ptr(s),
                  ops.hip.ptr(scratch), ops.hip.stream(DEV))
     torch.cuda.synchronize()
