@@ -270,8 +270,10 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
             do, ho, wo = (dp - k) // stride[0] + 1, (hp - k) // stride[1] + 1, (wp - k) // stride[2] + 1
             ys = torch.empty((b, cout, do, ho, wo), device=dev, dtype=f16).contiguous(
                 memory_format=torch.channels_last_3d)
-            t_c = timed(lambda: call("h3v_conv3d_f16", p(xs), p(wsp), p(bs), None, p(ys), b, cin, dp, hp, wp, cout, k, k,
-                                     k, *stride, int(causal), stream))
+            floats = int(hip.lib().h3v_conv3d_f16_workspace_floats(b, cin, dp, hp, wp, cout, k, k, k, *stride))
+            wsf = torch.empty(max(floats, 1), device=dev, dtype=torch.float32)
+            t_c = timed(lambda: call("h3v_conv3d_f16_ws", p(xs), p(wsp), p(bs), None, p(ys), b, cin, dp, hp, wp, cout, k,
+                                     k, k, *stride, int(causal), p(wsf), floats, stream))
             flops = 2 * b * do * ho * wo * cout * k ** 3 * cin
             res = {"h3v_conv3d_f16": fp16_mfma(t_c, flops)}
             if vs_torch:
@@ -286,6 +288,10 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
         out["downsample0_f16_128x17x256x256_s122"] = fp16_conv_case(1, 128, 128, 19, 258, 258, 3, (1, 2, 2), False)
         out["downsample1_f16_256x17x128x128_s222"] = fp16_conv_case(1, 256, 256, 19, 129, 129, 3, (2, 2, 2), False)
         out["nin_shortcut_f16_128to256x17x128x128"] = fp16_conv_case(1, 128, 256, 17, 128, 128, 1, (1, 1, 1), False)
+        # convs that fill under half of the CUs: K split over a workspace (suffix downsamples, conv_out)
+        out["suffix_downsample2_f16_4x256x9x64x64_s222"] = fp16_conv_case(4, 256, 256, 11, 65, 65, 3, (2, 2, 2), False)
+        out["suffix_downsample3_f16_4x512x5x32x32_s122"] = fp16_conv_case(4, 512, 512, 7, 33, 33, 3, (1, 2, 2), False)
+        out["conv_out_f16_4x1024to48x5x16x16"] = fp16_conv_case(4, 1024, 48, 7, 18, 18, 3, (1, 1, 1), True)
 
         # conv_in 3 -> 128 of one clip: tap-folded pack (3x3 taps x 3 channels -> 32, reflect border, two causal
         # zero frames) + the 3x1x1 conv over 32 channels; flops count the 81 real taps x channels

@@ -53,6 +53,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_causal_reflect_pack": [_P, _P] + [_I] * 10 + [_P],
     "h3v_tap_fold_pack": [_P, _P] + [_I] * 7 + [_P],
     "h3v_conv3d_f16": [_P, _P, _P, _P, _P] + [_I] * 13 + [_P],
+    "h3v_conv3d_f16_ws": [_P, _P, _P, _P, _P] + [_I] * 13 + [_P, _I64, _P],
     "h3v_gn_norm_pack_f16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "h3v_attention_d64": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
 }
@@ -64,6 +65,7 @@ SPECIAL: dict[str, tuple] = {
     "h3v_tensor_quant_scratch_words": (ctypes.c_int64, []),
     "h3v_probe_mfma_ops_per_block": (ctypes.c_int64, [_I]),
     "h3v_gn_norm_pack_f16_workspace_floats": (ctypes.c_int64, [_I, _I, _I, _I, _I]),
+    "h3v_conv3d_f16_workspace_floats": (ctypes.c_int64, [_I] * 12),
 }
 
 

@@ -35,7 +35,12 @@ namespace {
 enum class AMode { Gemm, Conv };
 // Dequant: fp16(fma(fp32(acc) * sx, sw, bias)); SwiGLU: paired gate/up then SiLU(gate) * up;
 // Int32: raw accumulators; F16Bias: fp16 operands with fp32 accumulators, fp16(acc + bias).
-enum class Epi { Dequant, SwiGLU, Int32, F16Bias };
+// F32Part: fp16 operands like F16Bias, the raw fp32 accumulators of one K split stored to
+// out + split * M * ldo (split-K partials, summed by splitk_reduce_f16).
+enum class Epi { Dequant, SwiGLU, Int32, F16Bias, F32Part };
+
+template <Epi EP>
+constexpr bool kF16Ops = EP == Epi::F16Bias || EP == Epi::F32Part;   // fp16 operands, fp32 accumulators
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -62,6 +67,7 @@ struct GemmParams {
     int conv_tpf;      // conv: M tiles per output frame when they do not straddle frames, else 0
     uint32_t a_bytes;  // extents of A and W in bytes (buffer resource ranges, < 4 GiB)
     uint32_t b_bytes;
+    int k_splits;      // tiled kernels: K blocks split evenly over gridDim.y = k_splits workgroups (0 or 1: none)
 };
 
 // Buffer resource word 3 for raw byte addressing (no swizzle, 32-bit format).
@@ -232,7 +238,7 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, typename AccV>
 __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM / WGM / 32][BN / WGN / 32],
                                            int8_t* smem, int m0, int n0, int tn) {
-    static_assert((EP == Epi::F16Bias) == std::is_same<AccV, f32x16>::value, "fp32 accumulators with F16Bias only");
+    static_assert(kF16Ops<EP> == std::is_same<AccV, f32x16>::value, "fp32 accumulators with fp16 operands only");
     constexpr int NW = WGM * WGN;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
@@ -247,7 +253,33 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
     // register quad.
     const int mrow = lane & 31;
     const int ncol = (lane >> 5) * 4;
-    if constexpr (EP == Epi::Int32) {
+    if constexpr (EP == Epi::F32Part) {
+        // this split's partial sums, straight from the MFMA layout: 16 bytes (4 columns) per store
+        float* part = static_cast<float*>(p.out) + (int64_t)blockIdx.y * p.M * p.ldo;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int c0 = n0 + wn * WN + j * 32 + q4 * 8 + ncol;
+                if (c0 >= p.N) continue;
+                const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
+#pragma unroll
+                for (int i = 0; i < FM; ++i) {
+                    const int row = m0 + wm * WM + i * 32 + mrow;
+                    if (row >= p.M) continue;
+                    float* dst = part + (int64_t)row * p.ldo + c0;
+                    if (full) {
+                        f32x4 v = {acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
+                        *reinterpret_cast<f32x4*>(dst) = v;
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
+                    }
+                }
+            }
+        }
+    } else if constexpr (EP == Epi::Int32) {
 #pragma unroll
         for (int j = 0; j < FN; ++j) {
 #pragma unroll
@@ -534,8 +566,17 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         boff[j] = (uint32_t)((int64_t)wrow * p.K + ((lslot ^ swz<BK>(r)) << 4));
     }
 
-    const int kb0 = (AM == AMode::Conv) ? conv_first_kblock(p, m0, BM, BK) : 0;
-    const int nk = p.K / BK - kb0;
+    // K blocks of this workgroup: split blockIdx.y of k_splits (the whole K without a split), minus the
+    // causal-zero taps of a conv tile's first frames
+    const int nsplit = p.k_splits > 1 ? p.k_splits : 1;
+    const int kper = p.K / BK / nsplit;
+    const int kend = (int)blockIdx.y * kper + kper;
+    int kb0 = (int)blockIdx.y * kper;
+    if constexpr (AM == AMode::Conv) {
+        const int skip = conv_first_kblock(p, m0, BM, BK);
+        kb0 = skip > kb0 ? skip : kb0;
+    }
+    const int nk = kend > kb0 ? kend - kb0 : 0;
 
     // A stages are issued strictly in order, so the conv's k offset is kept as a
     // running (kd, kh, kw, c0) position advanced by BK per issue: no integer
@@ -584,7 +625,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     // F16Bias: fp16 operands with p.C and p.K given in bytes (2 per element), so every k
     // offset above stays a byte offset; v_mfma_f32_32x32x16_f16 reads the same 16 bytes per
     // lane as the int8 instruction and accumulates in fp32.
-    using Acc = std::conditional_t<EP == Epi::F16Bias, f32x16, v16i>;
+    using Acc = std::conditional_t<kF16Ops<EP>, f32x16, v16i>;
     Acc acc[FM][FN];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
@@ -615,7 +656,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
         for (int i = 0; i < FM; ++i)
 #pragma unroll
             for (int j = 0; j < FN; ++j) {
-                if constexpr (EP == Epi::F16Bias)
+                if constexpr (kF16Ops<EP>)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, bf[j]),
                                                                        __builtin_bit_cast(half8, af[i]), acc[i][j], 0, 0, 0);
                 else
@@ -978,8 +1019,43 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, lds,
                                         hipGetErrorString(attr));
-    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(WGM * WGN * 64), lds, stream, p);
+    const int splits = p.k_splits > 1 ? p.k_splits : 1;
+    if ((p.K / BK) % splits != 0 || (splits > 1 && EP != Epi::F32Part))
+        return fail(H3V_EINVAL, "%s: %d K splits do not divide %d K blocks", what, splits, p.K / BK);
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid, (unsigned)splits), dim3(WGM * WGN * 64), lds, stream, p);
     return launch_status(what);
+}
+
+// Fraction of the CU slots busy over the rounds a launch of `tiles` one-per-CU workgroups takes.
+double round_fill(int64_t tiles) {
+    constexpr int64_t kCUs = 256;
+    const int64_t rounds = (tiles + kCUs - 1) / kCUs;
+    return rounds ? (double)tiles / (double)(rounds * kCUs) : 1.0;
+}
+
+// Sum of the K-split partials [S][M][N] (fp32, split-major) in split order, then the F16Bias epilogue:
+// y = fp16(sum + bias), with a residual fp16(fp32(res) + fp32(y)).  M * N and N are multiples of 4.
+__global__ __launch_bounds__(256) void splitk_reduce_f16(const float* __restrict__ part, int splits, int64_t mn, int n,
+                                                         const uint16_t* __restrict__ bias,
+                                                         const uint16_t* __restrict__ res, uint16_t* __restrict__ out) {
+    const int64_t i4 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i4 >= mn) return;
+    f32x4 v = *reinterpret_cast<const f32x4*>(part + i4);
+    for (int sp = 1; sp < splits; ++sp) {
+        const f32x4 w = *reinterpret_cast<const f32x4*>(part + sp * mn + i4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v[e] + w[e];
+    }
+    const int c = (int)(i4 % n);
+    u16x4 y;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = f2h(bias ? v[e] + h2f(bias[c + e]) : v[e]);
+    if (res) {
+        const u16x4 r = *reinterpret_cast<const u16x4*>(res + i4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = f2h(h2f(r[e]) + h2f(y[e]));
+    }
+    *reinterpret_cast<u16x4*>(out + i4) = y;
 }
 
 // Stride-1 3x3x3 convolution through conv3_halo_i8 with ES-byte elements: requires
@@ -989,6 +1065,67 @@ bool halo_conv_fits(const GemmParams& p, int es = 1) {
                        (p.C * es) % 64 == 0 && p.N % 128 == 0 &&
                        (p.Wo == 32 || p.Wo == 64 || p.Wo == 128 || p.Wo == 256) && p.Ho % (512 / p.Wo) == 0;
     return shape && aligned(p.a, 16) && aligned(p.b, 16) && (int64_t)p.Hp * p.Wp * p.C * es * 3 < ((int64_t)1 << 31);
+}
+
+enum class F16Kind { Halo256, Halo128, Halo64, Halo32, Tiled512x128, Tiled256x128, Tiled256x256, Tiled512x128k64,
+                     Tiled256x128k64, Tiled256x256k64 };
+struct F16Plan {
+    F16Kind kind;
+    int splits;
+};
+
+// K splits for a launch of `tiles` workgroups over `kblocks` K blocks: none at half a round or more;
+// otherwise the largest S <= 16 that keeps tiles * S within one round of the 256 CUs, divides the K
+// blocks and leaves each split at least 8 of them.
+int f16_splits(int64_t tiles, int kblocks) {
+    if (2 * tiles > 256) return 1;
+    int best = 1;
+    for (int sp = 2; sp <= 16; ++sp)
+        if (tiles * sp <= 256 && kblocks % sp == 0 && kblocks / sp >= 8) best = sp;
+    return best;
+}
+
+// Kernel, tile and K split of h3v_conv3d_f16 for the geometry in p (C and K in elements; the implicit
+// GEMM counts them in bytes).  Splits only when the caller supplies a workspace (may_split).
+F16Plan plan_conv_f16(const GemmParams& p, bool may_split) {
+    if (halo_conv_fits(p, 2)) {
+        if (p.Wo == 256) return {F16Kind::Halo256, 1};
+        if (p.Wo == 128) return {F16Kind::Halo128, 1};
+        if (p.Wo == 64) return {F16Kind::Halo64, 1};
+        return {F16Kind::Halo32, 1};
+    }
+    const int cb = p.C * 2;
+    const int64_t kb = (int64_t)p.K * 2;
+    const int64_t m256 = (p.M + 255) / 256;
+    if (cb % 128 == 0) {
+        const int kblocks = (int)(kb / 128);
+        if (p.N <= 128) {
+            // A K split when even 256-row tiles leave most CUs idle (conv_out: 1024 -> 48 at 5 x 16 x 16)
+            if (may_split && p.N % 4 == 0) {
+                const int sp = f16_splits(m256, kblocks);
+                if (sp > 1) return {F16Kind::Tiled256x128, sp};
+            }
+            // 512 x 128 tiles unless their last round leaves many CUs idle where 256 x 128 tiles (eight
+            // 64 x 64 wave blocks, about 10% slower per tile) fill the chip better: the stage-0
+            // downsample (544 tiles = 2.1 rounds) 353.5 -> 312.6 us, conv_out (10 tiles) 461.5 -> 285.3 us
+            if (round_fill((p.M + 511) / 512) < 0.9 * round_fill(m256)) return {F16Kind::Tiled256x128, 1};
+            return {F16Kind::Tiled512x128, 1};
+        }
+        const int64_t t256 = m256 * ((p.N + 255) / 256);
+        if (may_split && p.N % 4 == 0) {
+            const int sp = f16_splits(t256, kblocks);
+            if (sp > 1) return {F16Kind::Tiled256x256, sp};
+        }
+        // Cout > 128 with so few 256 x 256 tiles that even twice as many fit one round on the 256 CUs
+        // (the 16^2 suffix stage: 80 tiles): 256 x 128 tiles of eight 64 x 64 wave blocks.  At 144 tiles
+        // (the stride-2 downsample) the 288 smaller tiles need a second round and ran 35% slower.
+        if (2 * t256 <= 256) return {F16Kind::Tiled256x128, 1};
+        return {F16Kind::Tiled256x256, 1};
+    }
+    const bool few = p.N > 128 && 2 * m256 * ((p.N + 255) / 256) <= 256;
+    if (p.N <= 128) return {F16Kind::Tiled512x128k64, 1};
+    if (few) return {F16Kind::Tiled256x128k64, 1};
+    return {F16Kind::Tiled256x256k64, 1};
 }
 
 template <int WO, Epi EP, int ES = 1>
@@ -1174,10 +1311,10 @@ int h3v_conv3d_i8_residual(const int8_t* qx, const float* x_scale, const int8_t*
     return run_conv<Epi::Dequant>(p, stream, what);
 }
 
-int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
-                   uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw, int sd,
-                   int sh, int sw, int causal_skip, hipStream_t stream) {
-    const char* what = "h3v_conv3d_f16";
+static int conv3d_f16_common(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
+                             uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,
+                             int sd, int sh, int sw, int causal_skip, float* workspace, int64_t workspace_floats,
+                             bool may_split, hipStream_t stream, const char* what) {
     H3V_REQUIRE(x && w && out, "%s: null pointer argument", what);
     H3V_REQUIRE(residual != out, "%s: the residual must not alias the output", what);
     GemmParams p{};
@@ -1191,27 +1328,71 @@ int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, c
     p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
     H3V_REQUIRE(cin % 32 == 0 && aligned(x, 16) && aligned(w, 16),
                 "%s: requires Cin %% 32 == 0 and 16-byte aligned x and w (got Cin %d)", what, cin);
-    if (halo_conv_fits(p, 2)) {
-        if (p.Wo == 256) return launch_halo<256, Epi::F16Bias, 2>(p, stream, what);
-        if (p.Wo == 128) return launch_halo<128, Epi::F16Bias, 2>(p, stream, what);
-        if (p.Wo == 64) return launch_halo<64, Epi::F16Bias, 2>(p, stream, what);
-        return launch_halo<32, Epi::F16Bias, 2>(p, stream, what);
+    const F16Plan plan = plan_conv_f16(p, may_split);
+    switch (plan.kind) {
+        case F16Kind::Halo256: return launch_halo<256, Epi::F16Bias, 2>(p, stream, what);
+        case F16Kind::Halo128: return launch_halo<128, Epi::F16Bias, 2>(p, stream, what);
+        case F16Kind::Halo64: return launch_halo<64, Epi::F16Bias, 2>(p, stream, what);
+        case F16Kind::Halo32: return launch_halo<32, Epi::F16Bias, 2>(p, stream, what);
+        default: break;
     }
     // implicit GEMM with channels and reduction counted in bytes
     p.C = cin * 2;
     p.K = p.K * 2;
-    // Cout > 128 with so few 256 x 256 tiles that even twice as many fit one round on the 256 CUs
-    // (the 16^2 suffix stage: 80 tiles): 256 x 128 tiles of eight 64 x 64 wave blocks.  At 144 tiles
-    // (the stride-2 downsample) the 288 smaller tiles need a second round and ran 35% slower.
-    const bool few = p.N > 128 && 2 * (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256) <= 256;
-    if (p.C % 128 == 0) {
-        if (p.N <= 128) return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
-        if (few) return launch_tiled<256, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
-        return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+    if (plan.splits > 1) {
+        const int64_t need = (int64_t)plan.splits * p.M * p.N;
+        H3V_REQUIRE(workspace != nullptr && workspace_floats >= need && aligned(workspace, 16),
+                    "%s: this shape splits K %d ways and needs a 16-byte aligned workspace of %lld floats (got %lld)",
+                    what, plan.splits, (long long)need, (long long)workspace_floats);
+        H3V_REQUIRE(p.N % 4 == 0 && aligned(out, 8) && (residual == nullptr || aligned(residual, 8)),
+                    "%s: a split reduction needs Cout %% 4 == 0 and 8-byte aligned output and residual", what);
+        GemmParams q = p;
+        q.out = workspace;
+        q.bias = nullptr;
+        q.res = nullptr;
+        q.k_splits = plan.splits;
+        rc = plan.kind == F16Kind::Tiled256x256
+                 ? launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, Epi::F32Part>(q, stream, what)
+                 : launch_tiled<256, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F32Part>(q, stream, what);
+        if (rc) return rc;
+        const int64_t mn = (int64_t)p.M * p.N;
+        hipLaunchKernelGGL(splitk_reduce_f16, dim3((unsigned)((mn / 4 + 255) / 256)), dim3(256), 0, stream,
+                           (const float*)workspace, plan.splits, mn, p.N, bias, residual, out);
+        return launch_status(what);
     }
-    if (p.N <= 128) return launch_tiled<512, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
-    if (few) return launch_tiled<256, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
-    return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
+    switch (plan.kind) {
+        case F16Kind::Tiled512x128: return launch_tiled<512, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        case F16Kind::Tiled256x128: return launch_tiled<256, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        case F16Kind::Tiled256x256: return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        case F16Kind::Tiled512x128k64: return launch_tiled<512, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        case F16Kind::Tiled256x128k64: return launch_tiled<256, 128, 64, 4, 2, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
+        default: return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Conv, Epi::F16Bias>(p, stream, what);
+    }
+}
+
+int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
+                   uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw, int sd,
+                   int sh, int sw, int causal_skip, hipStream_t stream) {
+    return conv3d_f16_common(x, w, bias, residual, out, batch, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw,
+                             causal_skip, nullptr, 0, false, stream, "h3v_conv3d_f16");
+}
+
+int h3v_conv3d_f16_ws(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
+                      uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,
+                      int sd, int sh, int sw, int causal_skip, float* workspace, int64_t workspace_floats,
+                      hipStream_t stream) {
+    return conv3d_f16_common(x, w, bias, residual, out, batch, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw,
+                             causal_skip, workspace, workspace_floats, true, stream, "h3v_conv3d_f16_ws");
+}
+
+int64_t h3v_conv3d_f16_workspace_floats(int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,
+                                        int sd, int sh, int sw) {
+    GemmParams p{};
+    if (fill_conv(p, "h3v_conv3d_f16_workspace_floats", batch, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw))
+        return -1;
+    p.a = p.b = reinterpret_cast<const int8_t*>(16);   // alignment only; plan_conv_f16 reads no memory
+    const F16Plan plan = plan_conv_f16(p, true);
+    return plan.splits > 1 ? (int64_t)plan.splits * p.M * p.N : 0;
 }
 
 int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,

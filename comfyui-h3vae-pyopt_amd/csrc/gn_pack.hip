@@ -6,14 +6,19 @@
 // x: fp16 NDHWC [D, H, W, C] (batch one, C in {128, 256}).  Output q: int8 NDHWC
 // [D+2, H+2, W+2, C], frames 0 and 1 zero, spatial reflect padding of 1.
 //
-// Launch sequence (all on the caller's stream, no host synchronisation):
-//   gn_init       clears the per-(frame, channel) max/min keys and the absmax word
+// Launch sequence (all on the caller's stream, no host synchronisation, no atomic
+// counters to clear beforehand):
 //   gn_partial    grid (chunks, D): per 256-pixel chunk and group, avg and M2;
-//                 per (frame, channel) max and min of the (pre-biased) input
-//   gn_merge      grid (32, D): Chan merge of the chunks -> (mean, rstd); absmax
-//                 candidate from the per-channel extremes (below)
-//   norm_absmax   full absmax pass, only when the candidate cannot be proven exact
-//   build_lut     the int8 code of every fp16 pre-activation z under the final scale
+//                 per chunk and channel max and min of the (pre-biased) input
+//                 (fp16, exact); block (0, 0) also zeroes the absmax word and
+//                 the done counter of absmax_lut
+//   gn_merge      grid (32, D): Chan merge of the chunks -> (mean, rstd); the
+//                 per-channel extremes over the chunks give the absmax candidate
+//                 (below)
+//   absmax_lut    builds the int8 code of every fp16 pre-activation z under the
+//                 final scale; when the candidate cannot be proven exact it first
+//                 runs the full absmax pass and the last block to finish builds
+//                 the table
 //   norm_pack_lut every padded value -> int8 through that table; writes the scale
 //
 // Quantize table.  After the normalisation rounds z to fp16, the rest of the
@@ -44,15 +49,15 @@
 // ---------------------------------------------------------------------------
 // Static scratch of h3v_gn_norm_pack_i8_noalloc, for callers that cannot
 // allocate device memory.  Each GPU holds its own copy of this array for the
-// life of the process (4 MiB + 256 bytes): 64 head floats (word 0 is the absmax
+// life of the process (8 MiB + 256 bytes): 64 head floats (word 0 is the absmax
 // key) then the workspace, which covers every [D, H, W] whose
-// workspace_floats() fits (at 256 x 256 frames up to D = 61).  Every call on a
-// GPU reuses that GPU's copy; gn_init clears the keys each call, so nothing
-// carries over, but calls that overlap on one GPU (two streams, two threads)
+// workspace_floats() fits (at 256 x 256 frames up to D = 25).  Every call on a
+// GPU reuses that GPU's copy; every word a call reads was written earlier in
+// the same call, so nothing carries over, but calls that overlap on one GPU (two streams, two threads)
 // race on it.  The name `scratch` is a host-side stand-in: host code uses only
 // the device address hipGetSymbolAddress returns, looked up once per device.
 constexpr int64_t kScratchHeadFloats = 64;
-constexpr int64_t kScratchWorkspaceFloats = (int64_t)1 << 20;
+constexpr int64_t kScratchWorkspaceFloats = (int64_t)1 << 21;
 static __device__ __align__(256) float scratch[kScratchHeadFloats + kScratchWorkspaceFloats];
 
 namespace h3v {
@@ -70,31 +75,12 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
     for (int e = 0; e < 8; ++e) v[e] = h2f(a[e]);
 }
 
-// Order-preserving float <-> uint key (for atomic max / min of signed floats).
-__device__ __forceinline__ uint32_t fkey(float f) {
-    uint32_t u = __builtin_bit_cast(uint32_t, f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float fval(uint32_t k) {
-    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
-    return __builtin_bit_cast(float, u);
-}
-
-__global__ void gn_init(uint32_t* __restrict__ vmax, uint32_t* __restrict__ vmin, int n, uint32_t* __restrict__ amax) {
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) {
-        vmax[i] = 0u;
-        vmin[i] = 0xffffffffu;
-    }
-    if (i == 0) *amax = 0u;
-}
-
 // C channels, cg = C/32 channels per group, TPP = C/8 threads per pixel.
 template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
                                                   int hw, int nchunk, float* __restrict__ part_avg,
-                                                  float* __restrict__ part_m2, uint32_t* __restrict__ vmax,
-                                                  uint32_t* __restrict__ vmin) {
+                                                  float* __restrict__ part_m2, uint32_t* __restrict__ ext,
+                                                  uint32_t* __restrict__ amax_bits, uint32_t* __restrict__ done) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
     constexpr int PL = kNT / TPP;
@@ -175,8 +161,13 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
             a = __builtin_fmaxf(a, mx_s[i][tid]);
             b = __builtin_fminf(b, mn_s[i][tid]);
         }
-        atomicMax(&vmax[t * C + tid], fkey(a));
-        atomicMin(&vmin[t * C + tid], fkey(b));
+        // the extremes are input values (fp16, or fp16-rounded with the pre-bias): exact as fp16
+        ext[((int64_t)t * nchunk + j) * C + tid] = (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
+    }
+    if (j == 0 && t == 0 && tid == 0) {   // for gn_merge and absmax_lut, which run after this kernel
+        *amax_bits = 0u;
+        done[0] = 0u;
+        done[1] = 0u;
     }
     __syncthreads();
 
@@ -274,7 +265,7 @@ __device__ void gn_merge_group(const float* __restrict__ pa, const float* __rest
 }
 
 __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
-                                               const uint32_t* __restrict__ vmax, const uint32_t* __restrict__ vmin,
+                                               const uint32_t* __restrict__ ext,
                                                const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
                                                int hw, int nchunk, int c, float eps, float* __restrict__ stats,
                                                uint32_t* __restrict__ amax_bits) {
@@ -292,31 +283,58 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
         stats[(t * kGroups + g) * 2 + 1] = ms[1];
     }
     const float mean = ms[0];
-    // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map
+    // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map of the channel's
+    // extreme over all chunks (lanes stride the chunks, then a wave reduction per channel)
     float cand = 0.0f;
-    if (tid < cg) {
-        const int ch = g * cg + tid;
-        const float gm = h2f(gamma[ch]), bt = h2f(beta[ch]);
-        const float v = gm >= 0.0f ? fval(vmax[t * c + ch]) : fval(vmin[t * c + ch]);
-        const float z = rt16(((v - mean) * ms[1]) * gm + bt);
-        cand = __builtin_fabsf(rt16(silu(z)));
+    for (int e = 0; e < cg; ++e) {
+        const int ch = g * cg + e;
+        float vmx = -__builtin_inff(), vmn = __builtin_inff();
+        for (int j = tid; j < nchunk; j += 64) {
+            const uint32_t k = ext[((int64_t)t * nchunk + j) * c + ch];
+            vmx = __builtin_fmaxf(vmx, h2f((uint16_t)(k & 0xffffu)));
+            vmn = __builtin_fminf(vmn, h2f((uint16_t)(k >> 16)));
+        }
+        vmx = wave_max(vmx);
+        vmn = -wave_max(-vmn);
+        if (tid == 0) {
+            const float gm = h2f(gamma[ch]), bt = h2f(beta[ch]);
+            const float v = gm >= 0.0f ? vmx : vmn;
+            const float z = rt16(((v - mean) * ms[1]) * gm + bt);
+            cand = __builtin_fmaxf(cand, __builtin_fabsf(rt16(silu(z))));
+        }
     }
-    cand = wave_max(cand);
     // every candidate is the |value| of a real element, so it never exceeds the true absmax
     if (tid == 0) atomicMax(amax_bits, __builtin_bit_cast(uint32_t, cand));
 }
 
 __device__ __forceinline__ int reflect(int i, int n) { return i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i); }
 
-// Full absmax of all padded values; exits at once when the candidate is exact.
+// q code of table entries [first, first + count) under the scale of the final absmax.
+__device__ __forceinline__ void build_lut_range(float amax, int8_t* __restrict__ lut, int first, int count) {
+    const float s = e3_scale(amax);
+    for (int code = first + (int)threadIdx.x; code < first + count; code += kNT)
+        lut[code] = (int8_t)e3_quant(rt16(silu(h2f((uint16_t)code))), s);
+}
+
+// The quantize table of norm_pack_lut.  When the absmax candidate is exact (almost always) the final
+// scale is known at once and the first 256 blocks build 256 table entries each.  Otherwise every block
+// runs its share of the full absmax pass into done[1]; the last block to finish (counter done[0])
+// stores the final absmax and builds the whole table from it.  The candidate word is not written
+// before every block has read it, so all blocks take the same branch.  gn_partial zeroed both words.
+// Grid: at least 256 blocks.
 template <int C, bool PRE_BIAS>
-__global__ __launch_bounds__(kNT) void norm_absmax(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
-                                                   const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
-                                                   const float* __restrict__ stats, int d, int h, int w,
-                                                   uint32_t* __restrict__ amax_bits) {
+__global__ __launch_bounds__(kNT) void absmax_lut(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
+                                                  const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
+                                                  const float* __restrict__ stats, int d, int h, int w,
+                                                  uint32_t* __restrict__ amax_bits, uint32_t* __restrict__ done,
+                                                  int8_t* __restrict__ lut) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
-    if (__builtin_bit_cast(float, *amax_bits) >= kShortcutFloor) return;
+    const float cand = __builtin_bit_cast(float, *amax_bits);
+    if (cand >= kShortcutFloor) {
+        if (blockIdx.x < 65536 / kNT) build_lut_range(cand, lut, blockIdx.x * kNT, kNT);
+        return;
+    }
     const int hp = h + 2, wp = w + 2;
     const int64_t nvec = (int64_t)(d + 2) * hp * wp * TPP;
     float amax = 0.0f;
@@ -350,28 +368,36 @@ __global__ __launch_bounds__(kNT) void norm_absmax(const uint16_t* __restrict__ 
         }
     }
     __shared__ float red[kNT / 64];
+    __shared__ int last;
+    __shared__ float fin;
     amax = wave_max(amax);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
     __syncthreads();
     if (threadIdx.x == 0) {
         float m = red[0];
         for (int i = 1; i < kNT / 64; ++i) m = __builtin_fmaxf(m, red[i]);
-        atomicMax(amax_bits, __builtin_bit_cast(uint32_t, m));
+        atomicMax(&done[1], __builtin_bit_cast(uint32_t, m));   // non-negative floats order as their bits
+        __threadfence();
+        last = atomicAdd(&done[0], 1u) == gridDim.x - 1;
+        if (last) {
+            __threadfence();
+            const float full = __builtin_bit_cast(float, __hip_atomic_load(&done[1], __ATOMIC_RELAXED,
+                                                                           __HIP_MEMORY_SCOPE_AGENT));
+            fin = __builtin_fmaxf(cand, full);
+            *amax_bits = __builtin_bit_cast(uint32_t, fin);
+        }
     }
+    __syncthreads();
+    if (last) build_lut_range(fin, lut, 0, 65536);
 }
 
 constexpr int kLutFloats = 65536 / 4;    // the int8 quantize table
 
 int64_t workspace_floats(int d, int h, int w) {
     int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
-    return 2 * (int64_t)d * nchunk * kGroups + 2 * (int64_t)d * kMaxC + kLutFloats;
-}
-
-// q code of every fp16 value z under the scale derived from the final absmax.
-__global__ __launch_bounds__(kNT) void build_lut(const uint32_t* __restrict__ amax_bits, int8_t* __restrict__ lut) {
-    const int code = blockIdx.x * kNT + threadIdx.x;
-    const float s = e3_scale(__builtin_bit_cast(float, *amax_bits));
-    lut[code] = (int8_t)e3_quant(rt16(silu(h2f((uint16_t)code))), s);
+    // (avg, M2) per chunk and group; per chunk and channel the packed fp16 (max, min); the quantize table;
+    // 64 floats whose first word is absmax_lut's done counter
+    return 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC + kLutFloats + 64;
 }
 
 // PASS 1 through the table.  Each block walks whole padded output rows
@@ -463,22 +489,21 @@ void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
     const int nchunk = (hw + kChunk - 1) / kChunk;
     float* part_avg = ws;
     float* part_m2 = ws + (int64_t)d * nchunk * kGroups;
-    uint32_t* vmax = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups);
-    uint32_t* vmin = vmax + (int64_t)d * kMaxC;
-    int8_t* lut = reinterpret_cast<int8_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + 2 * (int64_t)d * kMaxC);
-    hipLaunchKernelGGL(gn_init, dim3((d * C + kNT - 1) / kNT), dim3(kNT), 0, stream, vmax, vmin, d * C, amax_bits);
+    uint32_t* ext = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups);
+    int8_t* lut = reinterpret_cast<int8_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC);
+    uint32_t* done = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC +
+                                                 kLutFloats);
+    // block (0, 0) zeroes the absmax word and the done counter: gn_merge and absmax_lut run after it
     hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
-                       part_m2, vmax, vmin);
-    hipLaunchKernelGGL(gn_merge, dim3(kGroups, d), dim3(64), 0, stream, part_avg, part_m2, vmax, vmin, gamma, beta, hw,
+                       part_m2, ext, amax_bits, done);
+    hipLaunchKernelGGL(gn_merge, dim3(kGroups, d), dim3(64), 0, stream, part_avg, part_m2, ext, gamma, beta, hw,
                        nchunk, C, eps, stats, amax_bits);
     const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
     int64_t want = (nvec + kNT - 1) / kNT;
-    // grid-strided; almost always every block exits at once (the candidate absmax is exact), so
-    // the grid stays small: dispatching 16384 blocks that only read one word cost about 4 us
-    unsigned blocks = (unsigned)(want > 1024 ? 1024 : want);
-    hipLaunchKernelGGL((norm_absmax<C, PB>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
-                       w, amax_bits);
-    hipLaunchKernelGGL(build_lut, dim3(65536 / kNT), dim3(kNT), 0, stream, amax_bits, lut);
+    // grid-strided full pass (rarely run) with at least one block per 256 table entries
+    unsigned blocks = (unsigned)(want > 1024 ? 1024 : (want < 256 ? 256 : want));
+    hipLaunchKernelGGL((absmax_lut<C, PB>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
+                       w, amax_bits, done, lut);
     // 64 KB of LDS per block: two blocks per CU; each block walks many vectors
     unsigned lut_blocks = (unsigned)(want > 512 ? 512 : want);
     hipLaunchKernelGGL((norm_pack_lut<C, PB>), dim3(lut_blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats,

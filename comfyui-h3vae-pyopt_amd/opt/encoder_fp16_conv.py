@@ -103,8 +103,15 @@ def conv3d_f16(x: torch.Tensor, w_packed: torch.Tensor, bias: Optional[torch.Ten
     b, c, d, h, w = x.shape
     out = torch.empty(_out_shape(x, w_packed, kernel_size, stride), device=x.device, dtype=x.dtype,
                       memory_format=torch.channels_last_3d)
-    _hip.call("h3v_conv3d_f16", _hip.ptr(x), _hip.ptr(w_packed), _hip.ptr(bias), _hip.ptr(residual), _hip.ptr(out),
-              b, c, d, h, w, w_packed.shape[0], *kernel_size, *stride, int(bool(causal_skip)), _hip.stream(x.device))
+    cout = w_packed.shape[0]
+    # convs too small to fill the chip split their reduction over a workspace of fp32 partial sums
+    floats = int(_hip.lib().h3v_conv3d_f16_workspace_floats(b, c, d, h, w, cout, *kernel_size, *stride))
+    if floats < 0:
+        raise ValueError(_hip.lib().h3v_last_error().decode(errors="replace"))
+    ws = torch.empty(floats, device=x.device, dtype=torch.float32) if floats else None
+    _hip.call("h3v_conv3d_f16_ws", _hip.ptr(x), _hip.ptr(w_packed), _hip.ptr(bias), _hip.ptr(residual), _hip.ptr(out),
+              b, c, d, h, w, cout, *kernel_size, *stride, int(bool(causal_skip)), _hip.ptr(ws), floats,
+              _hip.stream(x.device))
     return out
 
 

@@ -99,6 +99,26 @@ int h3v_conv3d_f16(const uint16_t* x, const uint16_t* w, const uint16_t* bias, c
                    uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw, int sd,
                    int sh, int sw, int causal_skip, hipStream_t stream);
 
+/* The same convolution with a caller workspace for a split reduction (the
+ * same model call sites as h3v_conv3d_f16).  When the implicit GEMM would
+ * leave most CUs idle (fewer tiles than half a round of the 256 CUs) and K is
+ * long, the reduction is split S ways: S workgroups per tile write fp32
+ * partial sums to workspace [S, M, cout], and a second kernel adds them in
+ * split order and applies the same epilogue (fp16(sum + bias), then the
+ * residual).  The sums' order differs from h3v_conv3d_f16's, the values stay
+ * within the same float64 bound.  workspace_floats must be at least
+ * h3v_conv3d_f16_workspace_floats() of the same geometry (16-byte aligned);
+ * a geometry that does not split ignores the workspace (it may be null). */
+int h3v_conv3d_f16_ws(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,
+                      uint16_t* out, int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,
+                      int sd, int sh, int sw, int causal_skip, float* workspace, int64_t workspace_floats,
+                      hipStream_t stream);
+
+/* fp32 workspace floats h3v_conv3d_f16_ws needs for this geometry: 0 when it
+ * does not split, -1 for an invalid geometry (h3v_last_error says why). */
+int64_t h3v_conv3d_f16_workspace_floats(int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,
+                                        int sd, int sh, int sw);
+
 /* ---- decoder attention (head_dim 64) --------------------------------------
  * Replaces the model's `perform_attention` (flash attention) called from
  * opt/decoder_fused_qk_rope.py:66-74 (`FusedQKAttention.forward`) between the
@@ -219,10 +239,10 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
  * no counterpart in the reference.  It is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc).  The workspace and the absmax word live in a static
- * device array of the library, one per GPU, 4 MiB + 256 bytes, held until the
+ * device array of the library, one per GPU, 8 MiB + 256 bytes, held until the
  * process ends; a call whose h3v_gn_norm_pack_workspace_floats(d, h, w)
- * exceeds 1048576 floats is rejected with H3V_EINVAL (256 x 256 frames: up to
- * d = 61).  The array of the current device is used, so `stream` must belong
+ * exceeds 2097152 floats is rejected with H3V_EINVAL (256 x 256 frames: up to
+ * d = 25).  The array of the current device is used, so `stream` must belong
  * to it.  Every call on one GPU shares that array; calls that overlap on one
  * GPU (two streams or threads) race.  Same inputs, outputs and results as
  * h3v_gn_norm_pack_i8. */

@@ -35,9 +35,18 @@ def test_library_loads_and_exports_every_declared_symbol(ops):
     table = set(ops.hip.SIGNATURES) | set(ops.hip.SPECIAL)
     assert set(names) == table
     assert lib.h3v_abi_version() == ops.hip.ABI_VERSION
-    # per-chunk (avg, M2) partials, per-(frame, channel) extreme keys, the 64 KB quantize table
-    assert lib.h3v_gn_norm_pack_workspace_floats(17, 256, 256) == 2 * 17 * 256 * 32 + 2 * 17 * 256 + 65536 // 4
+    # per-chunk (avg, M2) partials, per-chunk packed fp16 channel extremes (sized for 256 channels), the 64 KB
+    # quantize table, 64 floats of counters
+    assert lib.h3v_gn_norm_pack_workspace_floats(17, 256, 256) == 2 * 17 * 256 * 32 + 17 * 256 * 256 + 65536 // 4 + 64
     assert lib.h3v_gn_norm_pack_workspace_floats(0, 1, 1) == -1
+    # K splits of the FP16 conv: conv_out (1024 -> 48 on 4 x 5 x 16 x 16, 20 row tiles of 256) 12 ways,
+    # the 16^2 1024-channel conv (80 tiles of 256 x 256) 3 ways; full-chip convs and window-kernel convs none
+    ws = lib.h3v_conv3d_f16_workspace_floats
+    assert ws(4, 1024, 7, 18, 18, 48, 3, 3, 3, 1, 1, 1) == 12 * 5120 * 48
+    assert ws(4, 1024, 7, 18, 18, 1024, 3, 3, 3, 1, 1, 1) == 3 * 5120 * 1024
+    assert ws(1, 128, 19, 258, 258, 128, 3, 3, 3, 1, 2, 2) == 0
+    assert ws(4, 256, 11, 66, 66, 256, 3, 3, 3, 1, 1, 1) == 0
+    assert ws(1, 128, 2, 18, 18, 128, 3, 3, 3, 1, 1, 1) == -1
 
 
 def test_entry_points_reject_bad_arguments_before_any_launch(ops):

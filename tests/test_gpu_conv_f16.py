@@ -146,6 +146,66 @@ def test_conv3d_f16_implicit_gemm_matches_float64(fc, b, c, d, h, w, cout, kerne
     _assert_close(y, ref, mag)
 
 
+# K split over a workspace: (batch, Cin, D, H, W, Cout, causal zero frames, residual); tiles fill under half
+# a round, so S workgroups per tile write fp32 partial sums that a second kernel adds
+SPLIT_CASES = [
+    (1, 1024, 7, 18, 18, 48, False, False),     # conv_out-like: Cout 48 on 256 x 128 tiles, 16 splits
+    (1, 256, 7, 18, 18, 256, False, True),      # 256 x 256 tiles, 12 splits, with a residual
+    (2, 256, 5, 18, 18, 256, True, False),      # causal skip: frames 0 / 1 leave whole splits empty
+]
+
+
+@pytest.mark.parametrize("b,c,d,h,w,cout,causal,with_res", SPLIT_CASES)
+def test_conv3d_f16_split_reduction_matches_float64(fc, b, c, d, h, w, cout, causal, with_res):
+    print(f"conv3d_f16 split-K B={b} C={c} D={d} {h}x{w} Cout={cout} causal={causal} residual={with_res}", flush=True)
+    lib = fc._hip.lib()
+    floats = int(lib.h3v_conv3d_f16_workspace_floats(b, c, d, h, w, cout, 3, 3, 3, 1, 1, 1))
+    m = b * (d - 2) * (h - 2) * (w - 2)
+    assert floats > 0 and floats % (m * cout) == 0 and floats // (m * cout) >= 2   # the geometry splits
+    x, wt, bias = _operands(b, c, d, h, w, cout, True, seed=c + cout + d, causal_zero=causal)
+    gen = torch.Generator().manual_seed(cout)
+    res = (torch.randn(b, cout, d - 2, h - 2, w - 2, generator=gen) * 2).half() if with_res else None
+    xd = x.to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    wp = fc.pack_conv_weight_f16(wt.to(DEV))
+    rd = None if res is None else res.to(DEV).contiguous(memory_format=torch.channels_last_3d)
+    with torch.inference_mode():
+        y = fc.conv3d_f16(xd, wp, bias.to(DEV), [3, 3, 3], [1, 1, 1], causal)
+        fused = fc.conv3d_f16(xd, wp, bias.to(DEV), [3, 3, 3], [1, 1, 1], causal, rd) if with_res else None
+        torch.cuda.synchronize()
+    ref, mag = _reference(x, wt, bias)
+    _assert_close(y, ref, mag)
+    if with_res:
+        assert torch.equal(fused, rd + y)                  # the reduction's residual add == torch's fp16 add
+    # the unsplit entry (no workspace) gives values within the same bound
+    out = torch.empty_like(y)
+    fc._hip.call("h3v_conv3d_f16", fc._hip.ptr(xd), fc._hip.ptr(wp), fc._hip.ptr(bias.to(DEV)), None,
+                 fc._hip.ptr(out), b, c, d, h, w, cout, 3, 3, 3, 1, 1, 1, int(causal), fc._hip.stream(DEV))
+    torch.cuda.synchronize()
+    _assert_close(out, ref, mag)
+    # a workspace one float short is refused before anything runs
+    ws = torch.empty(floats, device=DEV, dtype=torch.float32)
+    with pytest.raises(ValueError, match="workspace"):
+        fc._hip.call("h3v_conv3d_f16_ws", fc._hip.ptr(xd), fc._hip.ptr(wp), fc._hip.ptr(bias.to(DEV)), None,
+                     fc._hip.ptr(out), b, c, d, h, w, cout, 3, 3, 3, 1, 1, 1, int(causal), fc._hip.ptr(ws),
+                     floats - 1, fc._hip.stream(DEV))
+
+
+@pytest.mark.parametrize("d,cout", [(18, 32), (10, 48)])
+def test_conv3d_f16_row_tile_choice_sampled_frames(fc, d, cout):
+    """Cout <= 128 implicit GEMM at full size: 16 output frames of 64 x 128 (131072 rows) fill whole rounds
+    with 512-row tiles, 8 frames (65536 rows, half a round) take 256-row tiles; output frames sampled
+    against float64 convs of their own three input frames."""
+    print(f"conv3d_f16 row-tile choice D={d} Cout={cout}", flush=True)
+    x, wt, bias = _operands(1, 64, d, 130, 258, cout, True, seed=d + cout, causal_zero=False)
+    y = _run(fc, x, wt, bias, causal_skip=False, stride=(1, 2, 2))
+    assert y.shape == (1, cout, d - 2, 64, 128)
+    for t in (0, (d - 2) // 2, d - 3):
+        xs = x[:, :, t:t + 3].double()
+        ref = F.conv3d(xs, wt.double(), bias.double(), stride=(1, 2, 2))
+        mag = F.conv3d(xs.abs(), wt.double().abs(), stride=(1, 2, 2))
+        _assert_close(y[:, :, t:t + 1], ref, mag)
+
+
 @pytest.mark.parametrize("b,c,d,h,w,cout,kernel", [(2, 64, 5, 10, 66, 128, (3, 3, 3)), (1, 64, 4, 10, 50, 96, (3, 3, 3)),
                                                    (3, 256, 4, 8, 8, 256, (1, 1, 1)),
                                                    (1, 64, 4, 10, 50, 100, (3, 3, 3))])   # scalar output rows
