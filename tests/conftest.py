@@ -18,6 +18,18 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an AMD MI355X (gfx950) GPU and the built HIP library")
 
 
+@pytest.fixture(scope="session", autouse=True)
+def _references_without_miopen():
+    """The model modules that serve as FP16 references call F.conv3d.  Through MIOpen its first call per
+    shape runs a solver search and kernel compile that takes minutes on a fresh box, so the references
+    use torch's own vol2col + BLAS convolution instead.  The product path never calls F.conv3d."""
+    import torch
+    enabled = torch.backends.cudnn.enabled
+    torch.backends.cudnn.enabled = False
+    yield
+    torch.backends.cudnn.enabled = enabled
+
+
 @pytest.fixture(scope="session")
 def pkg():
     import __graft_entry__
