@@ -19,8 +19,10 @@
 //                 (g, e = 0..3) of each 32-key half, so a query's 64 keys sit
 //                 in lanes l and l ^ 32 (32 each): the row max and sum are
 //                 in-lane reductions plus one exchange.
-//   online softmax in fp32 (exp2 with the scale folded into log2 e); the row
-//                 sums add the fp16-rounded weights that the P.V product uses
+//   online softmax in fp32 (exp2 with the scale folded into log2 e) against a
+//                 lazy reference maximum that moves only when a weight would
+//                 exceed 2^8; the row sums add the fp16-rounded weights that the
+//                 P.V product uses
 //   O^T += V^T . P^T   A = V^T rows from LDS (V is written transposed), B = P
 //                 in fp16: one v_permlane32_swap per dword pair turns the S
 //                 layout into the MFMA's 8 consecutive keys per lane.
@@ -45,6 +47,7 @@ constexpr int kBK = 64;       // keys per block
 // one set (152 VGPRs, 3 waves per SIMD) measured 5% slower on the H3 shape, 11% on [1, 16384, 16, 64]
 constexpr int kQuerySets = 2;
 constexpr int kThreads = 256;   // the K / V loading threads (waves 0-3); a workgroup has 8 waves
+constexpr float kLazy = 8.0f;   // log2 margin of the lazy softmax maximum (weights stay <= 2^kLazy)
 
 struct AttnParams {
     const uint16_t* q;
@@ -79,7 +82,7 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int h = blockIdx.y, b = blockIdx.z;
     const int n = p.tokens;
     const int64_t row0 = (int64_t)b * n;                 // first token row of this batch item
@@ -165,17 +168,22 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
     };
 
     f32x16 oacc[QS][2];
-    float m_run[QS], l_run[QS];
+    float m_ref[QS], mc[QS], l_run[QS];
 #pragma unroll
     for (int qs = 0; qs < QS; ++qs) {
         oacc[qs][0] = f32x16{};
         oacc[qs][1] = f32x16{};
-        m_run[qs] = -__builtin_inff();
+        m_ref[qs] = -__builtin_inff();
+        mc[qs] = -__builtin_inff();
         l_run[qs] = 0.0f;
     }
+    const float thr = kLazy / p.c;   // raw-score margin of the lazy maximum
 
     const int nblk = (n + kBK - 1) / kBK;
     const bool loader = tid < kThreads;                   // waves 0-3 (wave-uniform)
+    // The Q fragment loads complete here, once: otherwise the wait counters merged over the loop's back
+    // edge keep them pending, and the first score MFMAs of every block wait for that block's K / V loads.
+    __builtin_amdgcn_s_waitcnt(0);
     if (loader) load_block(0);
     for (int j = 0; j < nblk; ++j) {
         const int kb0 = j * kBK;
@@ -214,8 +222,14 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                         if (key >= n) s[qs][kh][r] = -__builtin_inff();
                     }
         }
-        // online softmax per set (raw-score units; the exponent folds in scale * log2 e); P in fp16
-        uint32_t pk[QS][2][8];                            // [set][half][g * 2 + dword]
+        // online softmax per set in raw-score units (the exponent folds in scale * log2 e), with a lazy
+        // reference maximum: the weights are exp2(s * c - m_ref * c), and m_ref moves (rescaling O and l by
+        // exp2((m_old - m_ref) * c)) only when a score of the block exceeds it by more than kLazy / c, i.e.
+        // when a weight would exceed 2^kLazy.  Every weight stays in [0, 256], where fp16 keeps the same
+        // relative precision, and after the first block the 64 rescale multiplies almost never run (with
+        // the exact running maximum some lane's maximum moves in nearly every block).  P in fp16.
+        bool up = false;
+        float mblk[QS];
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) {
             float mloc = s[qs][0][0];
@@ -223,10 +237,26 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
             for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) mloc = __builtin_fmaxf(mloc, s[qs][kh][r]);
-            const float m_new = __builtin_fmaxf(m_run[qs], wave_pair_max(mloc));
-            const float alpha = __builtin_amdgcn_exp2f((m_run[qs] - m_new) * p.c);
-            const float mc = m_new * p.c;
-            m_run[qs] = m_new;
+            mblk[qs] = wave_pair_max(mloc);
+            up |= mblk[qs] > m_ref[qs] + thr;   // m_ref = -inf before the first block: true there
+        }
+        if (__ballot(up)) {
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+                const float m_new = __builtin_fmaxf(m_ref[qs], mblk[qs]);
+                const float alpha = __builtin_amdgcn_exp2f((m_ref[qs] - m_new) * p.c);   // 0 from -inf, 1 if unmoved
+                m_ref[qs] = m_new;
+                mc[qs] = m_new * p.c;
+                l_run[qs] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 2; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[qs][db][r] *= alpha;
+            }
+        }
+        uint32_t pk[QS][2][8];                            // [set][half][g * 2 + dword]
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
             float lsum = 0.0f;
 #pragma unroll
             for (int kh = 0; kh < 2; ++kh)
@@ -235,7 +265,7 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                     float e4[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qs][kh][4 * g + e], p.c, -mc));
+                        e4[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[qs][kh][4 * g + e], p.c, -mc[qs]));
                     pk[qs][kh][2 * g] = pack_f16x2(e4[0], e4[1]);
                     pk[qs][kh][2 * g + 1] = pack_f16x2(e4[2], e4[3]);
                     // the row sum adds the fp16 weights the P.V product uses, two per v_dot2_f32_f16
@@ -243,15 +273,7 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                     lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[qs][kh][2 * g]), one, lsum, false);
                     lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pk[qs][kh][2 * g + 1]), one, lsum, false);
                 }
-            l_run[qs] = l_run[qs] * alpha + lsum;
-            // alpha is exactly 1 where the running maximum did not move; skip the rescale
-            // when that holds for every lane (most blocks once the maximum has settled)
-            if (__ballot(alpha != 1.0f)) {
-#pragma unroll
-                for (int db = 0; db < 2; ++db)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) oacc[qs][db][r] *= alpha;
-            }
+            l_run[qs] += lsum;
         }
 
         // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set

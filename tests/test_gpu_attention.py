@@ -77,6 +77,24 @@ def test_attention_large_scores_online_max(ops, oracle):
     _check(ops, oracle, q, k, v, out)
 
 
+@pytest.mark.parametrize("direction", [1, -1])
+def test_attention_score_ramp_moves_the_lazy_maximum(ops, oracle, direction):
+    """The kernel's reference maximum moves only when a score exceeds it by more than 8 / (scale * log2 e)
+    (a weight above 2^8).  Key norms growing with the key index make the maximum jump past that margin in
+    many blocks (the O and l rescale runs repeatedly); the reverse ramp sets it in the first block and
+    leaves later weights tiny (no rescale after block 0, deep exponents)."""
+    b, n, h = 1, 700, 2
+    q, k, v, qd, kd, vd = _qkv(b, n, h, seed=91 + direction)
+    ramp = torch.linspace(0.2, 6.0, n) if direction > 0 else torch.linspace(6.0, 0.2, n)
+    k = (k.float() * ramp.view(1, n, 1, 1)).half()
+    kd = k.to(DEV)
+    with torch.inference_mode():
+        out = ops.decoder_fused_qk_rope.attention_d64(qd, kd, vd, 0.125)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    _check(ops, oracle, q, k, v, out)
+
+
 def test_attention_cfg4_sampled_and_against_torch_sdpa(ops, oracle):
     """one 256x256 tile, 16384 tokens x 16 heads; also compared with torch's SDPA."""
     print("attention cfg4 [1, 16384, 16, 64]", flush=True)
