@@ -227,6 +227,35 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
                                                        "out_row_quant": hbm(t_oq, m * d * 3 + m * 4),
                                                        "out_gemm": mfma(t_og, 2 * m * d * d)}
 
+        # The INT8 GEMMs of the step (H3 decoder call, M = 7188) and of configs 2-4 (M = 16384) next to the
+        # vendor library's INT8 GEMM on the same operands: torch._int_mm (hipBLASLt, int32 output, no
+        # epilogue; it needs M, N, K multiples of 8, so it runs M = 7192 where ours runs 7188).  Activations
+        # are row-quantized N(0, 1), weights row-quantized N(0, 0.02), as in the step.
+        vs = {}
+        for label, mm, nn, kk in [("h3_qkv", 7188, 6144, 2048), ("h3_attn_out", 7188, 2048, 2048),
+                                  ("h3_ffn_up", 7188, 16384, 2048), ("h3_ffn_down", 7188, 2048, 8192),
+                                  ("cfg2_qkv", 16384, 3072, 1024), ("cfg3_up", 16384, 8192, 1024),
+                                  ("cfg3_down", 16384, 1024, 4096), ("cfg4_out", 16384, 1024, 1024)]:
+            xa = randn(mm, kk)
+            qa = torch.empty((mm, kk), device=dev, dtype=i8)
+            sa = torch.empty(mm, device=dev, dtype=f32)
+            call("h3v_row_quant", p(xa), mm, kk, p(qa), p(sa), stream)
+            wb, wbs = kitchen.quantize_int8_rowwise(randn(nn, kk, scale=0.02))
+            wbs = wbs.reshape(-1).contiguous()
+            bb = randn(nn, scale=0.02)
+            yb = torch.empty((mm, nn), device=dev, dtype=f16)
+            t_ours = timed(lambda: call("h3v_gemm_i8_dequant", p(qa), p(sa), p(wb), p(wbs), p(bb), p(yb), mm, nn, kk,
+                                        stream))
+            m8 = (mm + 7) // 8 * 8
+            qa8 = torch.zeros((m8, kk), device=dev, dtype=i8)
+            qa8[:mm] = qa
+            wbt = wb.t()
+            t_lib = timed(lambda: torch._int_mm(qa8, wbt))
+            vs[f"{label}_{mm}x{nn}x{kk}"] = {"h3v_gemm_i8_dequant": mfma(t_ours, 2 * mm * nn * kk),
+                                             "hipblaslt_int_mm_int32_out": mfma(t_lib, 2 * m8 * nn * kk)}
+            del xa, qa, qa8, wb, yb
+        out["int8_gemm_vs_hipblaslt"] = vs
+
         # decoder edge (opt/fp16_finalize.py): one B4 decoder call's tiles [4, 3, 28, 256, 256] fp16 -> fp32
         import ctypes
         px = randn(4, 3, 28, 256, 256)

@@ -282,27 +282,35 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
         stats[(t * kGroups + g) * 2] = ms[0];
         stats[(t * kGroups + g) * 2 + 1] = ms[1];
     }
-    const float mean = ms[0];
+    const float mean = ms[0], rstd = ms[1];
     // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map of the channel's
-    // extreme over all chunks (lanes stride the chunks, then a wave reduction per channel)
-    float cand = 0.0f;
-    for (int e = 0; e < cg; ++e) {
-        const int ch = g * cg + e;
-        float vmx = -__builtin_inff(), vmn = __builtin_inff();
-        for (int j = tid; j < nchunk; j += 64) {
-            const uint32_t k = ext[((int64_t)t * nchunk + j) * c + ch];
-            vmx = __builtin_fmaxf(vmx, h2f((uint16_t)(k & 0xffffu)));
-            vmn = __builtin_fminf(vmn, h2f((uint16_t)(k >> 16)));
-        }
-        vmx = wave_max(vmx);
-        vmn = -wave_max(-vmn);
-        if (tid == 0) {
-            const float gm = h2f(gamma[ch]), bt = h2f(beta[ch]);
-            const float v = gm >= 0.0f ? vmx : vmn;
-            const float z = rt16(((v - mean) * ms[1]) * gm + bt);
-            cand = __builtin_fmaxf(cand, __builtin_fabsf(rt16(silu(z))));
-        }
+    // extreme over all chunks.  Lane l takes channel l % cg and every (64 / cg)-th chunk from l / cg,
+    // so all of the group's extreme loads are in flight at once; lanes of one channel then combine
+    // by shuffles, and the cg candidates are evaluated in parallel lanes.  Max and min are exact in
+    // any order, so the candidate is the same as any other reduction order gives.
+    const int lpc = 64 / cg;                                  // lanes per channel (cg = 4 or 8)
+    const int e = tid % cg;
+    const int ch = g * cg + e;
+    const uint32_t* ep = ext + (int64_t)t * nchunk * c + ch;
+    float vmx = -__builtin_inff(), vmn = __builtin_inff();
+#pragma unroll 8
+    for (int j = tid / cg; j < nchunk; j += lpc) {
+        const uint32_t k = ep[(int64_t)j * c];
+        vmx = __builtin_fmaxf(vmx, h2f((uint16_t)(k & 0xffffu)));
+        vmn = __builtin_fminf(vmn, h2f((uint16_t)(k >> 16)));
     }
+    for (int off = cg; off < 64; off <<= 1) {
+        vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, off, 64));
+        vmn = __builtin_fminf(vmn, __shfl_xor(vmn, off, 64));
+    }
+    float cand = 0.0f;
+    if (tid < cg) {
+        const float gm = h2f(gamma[ch]), bt = h2f(beta[ch]);
+        const float v = gm >= 0.0f ? vmx : vmn;
+        const float z = rt16(((v - mean) * rstd) * gm + bt);
+        cand = __builtin_fabsf(rt16(silu(z)));
+    }
+    for (int off = 1; off < cg; off <<= 1) cand = __builtin_fmaxf(cand, __shfl_xor(cand, off, 64));
     // every candidate is the |value| of a real element, so it never exceeds the true absmax
     if (tid == 0) atomicMax(amax_bits, __builtin_bit_cast(uint32_t, cand));
 }
