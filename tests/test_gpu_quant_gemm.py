@@ -65,6 +65,62 @@ def test_swiglu_row_quant_matches_oracle(ops, oracle, m, k, scale):
     assert_bitwise(np_(s).view(np.uint32), rs.view(np.uint32), "scale")
 
 
+def _swiglu_gpu(ops, x):
+    m, k = x.shape[0], x.shape[1] // 2
+    q = torch.empty((m, k), dtype=torch.int8, device=DEV)
+    s = torch.empty(m, dtype=torch.float32, device=DEV)
+    xd = x.to(DEV)
+    ops.hip.call("h3v_swiglu_row_quant", ops.hip.ptr(xd), m, k, ops.hip.ptr(q), ops.hip.ptr(s), ops.hip.stream(DEV))
+    torch.cuda.synchronize()
+    return np_(q), np_(s)
+
+
+def test_swiglu_row_quant_every_gate_code(ops, oracle):
+    """Every fp16 gate code through the SwiGLU quantizer: every finite code (both zeros, subnormals,
+    +-65504; |gate| > 80 takes the IEEE SiLU path) appears as a gate in eight shuffled rows, the infinities
+    and NaNs in a ninth; up ~ N(0, 1)."""
+    codes = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    special = (codes & 0x7C00) == 0x7C00
+    rng = np.random.default_rng(8192)
+    finite = rng.permutation(codes[~special])
+    k = 8192
+    gate = np.zeros((9, k), np.uint16)
+    pad = rng.standard_normal(9 * k).astype(np.float16).view(np.uint16)
+    gate.reshape(-1)[:] = pad
+    per = (finite.size + 7) // 8
+    for r in range(8):
+        part = finite[r * per:(r + 1) * per]
+        gate[r, :part.size] = part
+    gate[8, :special.sum()] = codes[special]
+    up = rng.standard_normal((9, k)).astype(np.float16)
+    x = torch.from_numpy(np.concatenate([gate.view(np.float16), up], axis=1).copy())
+    q, s = _swiglu_gpu(ops, x)
+    rq, rs = oracle.swiglu_row_quant(x.numpy())
+    assert_bitwise(q, rq, "q")
+    assert_bitwise(s.view(np.uint32), rs.view(np.uint32), "scale")
+
+
+@pytest.mark.parametrize("m,k", [(257, 4096), (1031, 4096), (333, 1024), (70, 2048), (515, 8192)])
+def test_swiglu_row_quant_odd_rows_large_gates(ops, oracle, m, k):
+    """Odd row counts at every vector width (1024-8192) with large gates ~ N(0, 6)."""
+    x = (torch.randn(m, 2 * k, generator=_gen(m + k)) * 6.0).half()
+    q, s = _swiglu_gpu(ops, x)
+    rq, rs = oracle.swiglu_row_quant(x.numpy())
+    assert_bitwise(q, rq, "q")
+    assert_bitwise(s.view(np.uint32), rs.view(np.uint32), "scale")
+
+
+def test_swiglu_row_quant_h3_shape_bitwise(ops, oracle):
+    """The decoder FFN's SwiGLU quantizer at the H3 shape (7188 rows of [gate | up] 2 x 8192), every row
+    against the oracle; gates ~ N(0, 4)."""
+    print("swiglu row quant [7188, 2 x 8192]", flush=True)
+    x = (torch.randn(7188, 2 * 8192, generator=_gen(7188)) * 4.0).half()
+    q, s = _swiglu_gpu(ops, x)
+    rq, rs = oracle.swiglu_row_quant(x.numpy())
+    assert_bitwise(q, rq, "q")
+    assert_bitwise(s.view(np.uint32), rs.view(np.uint32), "scale")
+
+
 def _i32_gpu(ops, a, w):
     m, k = a.shape
     n = w.shape[0]
