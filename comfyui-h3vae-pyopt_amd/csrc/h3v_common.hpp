@@ -122,6 +122,17 @@ __device__ __forceinline__ int q1_quant(float a, const Q1Div& q) {
     return (int)v;
 }
 
+// q1_quant with the divisor's path chosen by the caller: FAST must equal q.fast.  A caller that branches
+// once per row on a wave-uniform q.fast runs straight-line code instead of a divergent branch per element.
+template <bool FAST>
+__device__ __forceinline__ int q1_quant_path(float a, const Q1Div& q) {
+    float v = rt16(FAST ? div_newton(a, q.d, q.r) : a / q.d);
+    v = __builtin_rintf(v);
+    if (v != v) return -128;
+    v = __builtin_fminf(127.0f, __builtin_fmaxf(-128.0f, v));
+    return (int)v;
+}
+
 // Per-tensor scale of the encoder activation quantizer: amax * fp32(1/127), 0 -> 1.
 __device__ __forceinline__ float e3_scale(float amax) {
     float s = amax * (1.0f / 127.0f);

@@ -1,7 +1,8 @@
 // Decoder row producers: residual + RMSNorm + row quantization (norm1 / norm2),
 // the block-0 RMSNorm and the final residual + LayerNorm.
 //
-// One wave per row of width K = NCH * 512 (K in {1024, 2048, 4096}); four rows
+// One wave per row of width K = NCH * 512 (K in {1024, 2048, 4096}; the
+// residual producers keep persistent waves that walk several rows); four waves
 // per 256-thread workgroup, no LDS and no workgroup barrier (measured against
 // one 256-thread workgroup per row: 20.7 vs 27.5 us at 16384 x 1024, equal at
 // 7188 x 2048).  Lane L holds the
@@ -22,8 +23,16 @@
 //   W16 recipe (norm1, docs/decoder_norm1_contract_2026-10-03.md:57-70):
 //       s1 = x1*x1; a = fma(x0,x0,s1); b = fma(x2,x2,a); s3 = x3*x3; p = s3 + b
 //   plain recipe: p = ((t0 + t1) + t2) + t3 over already rounded terms.
+#include <algorithm>
+#include <mutex>
+#include <type_traits>
+
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
+
+#ifndef WAVES_PER_CU
+#define WAVES_PER_CU 8
+#endif
 
 namespace h3v {
 namespace {
@@ -79,6 +88,15 @@ __device__ __forceinline__ void store8h(uint16_t* p, const float* v) {
 
 // N1 / F1: raw = fma(o, g, h); h_out = fp16(raw); ss = tree(raw^2);
 // inv = 1/sqrt(ss/K + eps); n = fp16((fp32(h_out) * inv) * w); row-quantize n.
+//
+// Persistent waves: wave i of the grid takes rows i, i + W, i + 2W, ... (W waves in the grid), and the
+// next row's h and o are loaded before the current row is reduced, so one row's loads overlap the
+// previous row's arithmetic (about 30 VALU operations per element).  With one wave per row every load
+// is issued at once and the arithmetic starts only when they have all arrived, which serialises the two.
+// Two register buffers alternate in a loop unrolled by two, so the buffer carried over the loop edge is
+// never copied (a copy would have to wait for its loads).  The gate and the norm weight are the same for
+// every row and load once per wave.  Kernel time at 7188 x 2048: 21.1 us against 23.6 us with one wave
+// per row, equal at 16384 x 1024 (same box); 4 or 16 persistent waves per CU were slower.
 template <int NCH, Recipe R>
 __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t* h, const uint16_t* __restrict__ o,
                                                                  const uint16_t* __restrict__ g, const uint16_t* __restrict__ w,
@@ -86,69 +104,98 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
                                                                  float* __restrict__ s, int64_t m) {
     constexpr int K = NCH * 512;
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    if (row >= m) return;
-    float raw[NCH][8];
-    float part[NCH][2];
-    // the norm weight goes out with the row loads: no second round trip after the reduction
+    const int64_t nw = (int64_t)gridDim.x * (kNT / 64);
+    int64_t row = (int64_t)blockIdx.x * (kNT / 64) + (threadIdx.x >> 6);   // wave-uniform
+    float gv[NCH][8];
     u16x8 wq[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) wq[c] = *reinterpret_cast<const u16x8*>(w + c * 512 + lane * 8);
-#pragma unroll
     for (int c = 0; c < NCH; ++c) {
-        const int col = c * 512 + lane * 8;
-        float hv[8], ov[8], gv[8];
-        load8f(h + row * K + col, hv);
-        load8f(o + row * K + col, ov);
-        load8f(g + col, gv);
+        load8f(g + c * 512 + lane * 8, gv[c]);
+        wq[c] = *reinterpret_cast<const u16x8*>(w + c * 512 + lane * 8);
+    }
+    u16x8 ha[NCH], oa[NCH], hb[NCH], ob[NCH];
+    auto load = [&](u16x8 (&hx)[NCH], u16x8 (&ox)[NCH], int64_t r) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) raw[c][e] = __builtin_fmaf(ov[e], gv[e], hv[e]);
+        for (int c = 0; c < NCH; ++c) {
+            hx[c] = *reinterpret_cast<const u16x8*>(h + r * K + c * 512 + lane * 8);
+            ox[c] = *reinterpret_cast<const u16x8*>(o + r * K + c * 512 + lane * 8);
+        }
+    };
+    auto process = [&](const u16x8 (&hx)[NCH], const u16x8 (&ox)[NCH], int64_t r) {
+        float raw[NCH][8];
+        float part[NCH][2];
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-            const float* x = &raw[c][hh * 4];
-            if constexpr (R == Recipe::W16) {
-                part[c][hh] = partial_w16(x);
-            } else {
-                float sq[4] = {x[0] * x[0], x[1] * x[1], x[2] * x[2], x[3] * x[3]};
-                part[c][hh] = partial_plain(sq);
+        for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) raw[c][e] = __builtin_fmaf(h2f(ox[c][e]), gv[c][e], h2f(hx[c][e]));
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const float* x = &raw[c][hh * 4];
+                if constexpr (R == Recipe::W16) {
+                    part[c][hh] = partial_w16(x);
+                } else {
+                    float sq[4] = {x[0] * x[0], x[1] * x[1], x[2] * x[2], x[3] * x[3]};
+                    part[c][hh] = partial_plain(sq);
+                }
             }
         }
-    }
-    // From here on only fp16-rounded values are used (h_out = fp16(raw), then n = fp16(...)): the row
-    // is held as packed fp16, half the registers of fp32, so all rows of an H3 call are resident at once.
-    u16x8 hv[NCH];
+        // from here on only fp16-rounded values are used (h_out = fp16(raw), then n = fp16(...)): the row
+        // is held as packed fp16
+        u16x8 hv[NCH];
 #pragma unroll
-    for (int c = 0; c < NCH; ++c)
+        for (int c = 0; c < NCH; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) hv[c][e] = f2h(raw[c][e]);
-    const float ss = row_tree<NCH>(part);
-    const float inv = rsqrt_rn(ss / (float)K + eps);
-    float amax = 0.0f;
+            for (int e = 0; e < 8; ++e) hv[c][e] = f2h(raw[c][e]);
+        const float ss = row_tree<NCH>(part);
+        const float inv = rsqrt_rn(ss / (float)K + eps);
+        float amax = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int col = c * 512 + lane * 8;
-        *reinterpret_cast<u16x8*>(h_out + row * K + col) = hv[c];
+        for (int c = 0; c < NCH; ++c) {
+            const int col = c * 512 + lane * 8;
+            *reinterpret_cast<u16x8*>(h_out + r * K + col) = hv[c];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float n = rt16((h2f(hv[c][e]) * inv) * h2f(wq[c][e]));
-            amax = __builtin_fmaxf(amax, __builtin_fabsf(n));
-            hv[c][e] = f2h(n);
+            for (int e = 0; e < 8; ++e) {
+                const float n = rt16((h2f(hv[c][e]) * inv) * h2f(wq[c][e]));
+                amax = __builtin_fmaxf(amax, __builtin_fabsf(n));
+                hv[c][e] = f2h(n);
+            }
         }
-    }
-    amax = wave_max(amax);
-    const float sc = q1_scale(amax);
-    const Q1Div qd = q1_div(rt16(sc));
+        amax = wave_max(amax);
+        const float sc = q1_scale(amax);
+        const Q1Div qd = q1_div(rt16(sc));
+        // the divisor is the same in every lane: one uniform branch per row picks the quotient path
+        auto store_q = [&](auto fast) {
+            constexpr bool F = decltype(fast)::value;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) {
-        const int col = c * 512 + lane * 8;
-        float v[8];
+            for (int c = 0; c < NCH; ++c) {
+                const int col = c * 512 + lane * 8;
+                float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = h2f(hv[c][e]);
-        uint32_t lo = pack4(q1_quant(v[0], qd), q1_quant(v[1], qd), q1_quant(v[2], qd), q1_quant(v[3], qd));
-        uint32_t hi = pack4(q1_quant(v[4], qd), q1_quant(v[5], qd), q1_quant(v[6], qd), q1_quant(v[7], qd));
-        *reinterpret_cast<uint2*>(q + row * K + col) = make_uint2(lo, hi);
+                for (int e = 0; e < 8; ++e) v[e] = h2f(hv[c][e]);
+                uint32_t lo = pack4(q1_quant_path<F>(v[0], qd), q1_quant_path<F>(v[1], qd), q1_quant_path<F>(v[2], qd),
+                                    q1_quant_path<F>(v[3], qd));
+                uint32_t hi = pack4(q1_quant_path<F>(v[4], qd), q1_quant_path<F>(v[5], qd), q1_quant_path<F>(v[6], qd),
+                                    q1_quant_path<F>(v[7], qd));
+                *reinterpret_cast<uint2*>(q + r * K + col) = make_uint2(lo, hi);
+            }
+        };
+        if (__builtin_amdgcn_readfirstlane((int)qd.fast)) store_q(std::true_type{});
+        else store_q(std::false_type{});
+        if (lane == 0) s[r] = sc;
+    };
+    if (row >= m) return;
+    load(ha, oa, row);
+    for (; row < m; row += 2 * nw) {
+        // Both loads are unconditional (a branch around one would make the compiler's wait counts wait
+        // for it too); a wave without a next row re-reads its current row, which L2 still holds.
+        const bool more = row + nw < m;        // wave-uniform
+        load(hb, ob, more ? row + nw : row);
+        __builtin_amdgcn_sched_barrier(0);   // keep the next row's loads ahead of this row's arithmetic
+        process(ha, oa, row);
+        load(ha, oa, row + 2 * nw < m ? row + 2 * nw : row);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) process(hb, ob, row + nw);
     }
-    if (lane == 0) s[row] = sc;
 }
 
 // N3: out = fp16((x * inv) * gamma), inv = 1/sqrt(W16(x^2)/K + eps).
@@ -227,6 +274,29 @@ __global__ __launch_bounds__(kNT) void residual_layernorm_kernel(const uint16_t*
     }
 }
 
+constexpr int kWavesPerCu = WAVES_PER_CU;
+
+constexpr int kMaxDevices = 64;
+std::mutex g_cu_mutex;
+int g_cus[kMaxDevices] = {};
+
+// CU count of the current device (looked up once per device).
+int cu_count(const char* what, int* out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(H3V_ELAUNCH, "%s: hipGetDevice failed: %s", what, hipGetErrorString(e));
+    H3V_REQUIRE(dev >= 0 && dev < kMaxDevices, "%s: device index %d out of range", what, dev);
+    std::lock_guard<std::mutex> lock(g_cu_mutex);
+    if (!g_cus[dev]) {
+        int n = 0;
+        e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess || n <= 0) return fail(H3V_ELAUNCH, "%s: CU count query failed: %s", what, hipGetErrorString(e));
+        g_cus[dev] = n;
+    }
+    *out = g_cus[dev];
+    return H3V_OK;
+}
+
 int check_row_width(const char* what, int64_t rows, int64_t k) {
     if (rows <= 0 || rows > 0x7fffffff) return fail(H3V_EINVAL, "%s: row count must be in [1, 2^31)", what);
     if (k != 1024 && k != 2048 && k != 4096)
@@ -251,7 +321,12 @@ static int residual_quant_common(const uint16_t* h, const uint16_t* o, const uin
                 "%s: fp16 pointers must be 16-byte and q 8-byte aligned", what);
     H3V_REQUIRE(h_out == h || (h_out + m * k <= o || o + m * k <= h_out),
                 "%s: h_out must not overlap o", what);
-    dim3 grid((unsigned)((m + kRowsPerBlock - 1) / kRowsPerBlock)), block(kNT);
+    int cus = 0;
+    rc = cu_count(what, &cus);
+    if (rc) return rc;
+    // persistent waves (kWavesPerCu per CU), at most one per row
+    const int64_t blocks = std::min<int64_t>((m + kRowsPerBlock - 1) / kRowsPerBlock, (int64_t)cus * kWavesPerCu / kRowsPerBlock);
+    dim3 grid((unsigned)blocks), block(kNT);
     if (w16) {
         if (k == 1024) hipLaunchKernelGGL((residual_rms_quant_kernel<2, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
         else if (k == 2048) hipLaunchKernelGGL((residual_rms_quant_kernel<4, Recipe::W16>), grid, block, 0, stream, h, o, g, w, eps, h_out, q, scale, m);
