@@ -30,9 +30,6 @@
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
-#ifndef WAVES_PER_CU
-#define WAVES_PER_CU 8
-#endif
 
 namespace h3v {
 namespace {
@@ -274,7 +271,7 @@ __global__ __launch_bounds__(kNT) void residual_layernorm_kernel(const uint16_t*
     }
 }
 
-constexpr int kWavesPerCu = WAVES_PER_CU;
+constexpr int kWavesPerCu = 8;    // persistent waves per CU of the residual producers
 
 constexpr int kMaxDevices = 64;
 std::mutex g_cu_mutex;
