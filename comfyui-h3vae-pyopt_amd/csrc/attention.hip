@@ -276,7 +276,11 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
             l_run[qs] += lsum;
         }
 
-        // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set
+        // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set.  The wave's issue
+        // priority is raised for them, so that a wave with P.V MFMAs ready issues ahead of its SIMD partner's
+        // softmax VALU work (H3 call 153.7 -> 151.5 us, cfg4 1222 -> 1200 us; around the score MFMAs as well,
+        // or at priority 2 or 3, no further change).
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int kh = c >> 1, g0 = 2 * (c & 1);
@@ -300,6 +304,7 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                     oacc[qs][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop[qs], oacc[qs][db], 0, 0, 0);
             }
         }
+        __builtin_amdgcn_s_setprio(0);
     }
 
     // normalise and store: lane l holds query q0 + 32 qs + l % 32, dims 32 db + 8 g + 4 hi + e
