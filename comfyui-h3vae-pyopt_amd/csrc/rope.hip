@@ -23,7 +23,19 @@ constexpr int kROT = 48;
 constexpr int kNT = 256;
 constexpr int kLanesPerRow = 8;
 
-__device__ __forceinline__ void norm_rope(float (&v)[8], float eps, int li, const float (&c)[8], const float (&s)[8]) {
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// One (token, head) row of q or k held by 8 lanes: RMS normalisation, then the rotate-half RoPE on the
+// first ROT dims.  Every product of the rotation multiplies two fp16 values; their fp32 product is exact
+// (11-bit significands), so rounding it to fp16 is the IEEE fp16 product, and the products run as packed
+// fp16 multiplies (two per instruction) on the normalised row kept as fp16 pairs.  The sum of the two
+// rounded products is formed in fp32 and rounded to fp16 once more, as the reference chain does.
+__device__ __forceinline__ u16x8 norm_rope(const u16x8& in, float eps, int li, const f16x2 (&c2)[4],
+                                           const f16x2 (&s2)[4]) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = h2f(in[e]);
     float p0 = ((v[0] * v[0] + v[1] * v[1]) + v[2] * v[2]) + v[3] * v[3];
     float p1 = ((v[4] * v[4] + v[5] * v[5]) + v[6] * v[6]) + v[7] * v[7];
 #pragma unroll
@@ -33,20 +45,35 @@ __device__ __forceinline__ void norm_rope(float (&v)[8], float eps, int li, cons
     }
     const float part = p0 + p1;
     const float inv = rsqrt_rn(part / (float)kDH + eps);
+    // normalised row, fp16 pairs (v_cvt_pk_f16_f32 rounds each to nearest even, as fp16(x) does)
+    uint32_t n2[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] * inv);
-    // partner lane for rotate-half over the first ROT dims: li<3 -> li+3, 3<=li<6 -> li-3
+    for (int j = 0; j < 4; ++j)
+        n2[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){v[2 * j] * inv, v[2 * j + 1] * inv}, f16x2));
+    // rotate-half partner over the first ROT dims: li < 3 -> li + 3, 3 <= li < 6 -> li - 3
     const int lane = threadIdx.x & 63;
     const int base = lane & ~(kLanesPerRow - 1);
     const int partner = li < 3 ? li + 3 : (li < 6 ? li - 3 : li);
-    float r[8];
+    uint32_t r2[4];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = __shfl(v[e], base + partner, 64);
+    for (int j = 0; j < 4; ++j) r2[j] = (uint32_t)__shfl((int)n2[j], base + partner, 64);
+    u16x8 out;
     if (li < kROT / 8) {
-        const float sign = li < kROT / 16 ? -1.0f : 1.0f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] * c[e]) + rt16((r[e] * sign) * s[e]);
+        for (int j = 0; j < 4; ++j) {
+            const f16x2 a = __builtin_bit_cast(f16x2, n2[j]) * c2[j];   // fp16(n * cos)
+            const f16x2 b = __builtin_bit_cast(f16x2, r2[j]) * s2[j];   // fp16(+-partner * sin)
+            out[2 * j] = f2h((float)a[0] + (float)b[0]);
+            out[2 * j + 1] = f2h((float)a[1] + (float)b[1]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            out[2 * j] = (uint16_t)(n2[j] & 0xffffu);
+            out[2 * j + 1] = (uint16_t)(n2[j] >> 16);
+        }
     }
+    return out;
 }
 
 __global__ __launch_bounds__(kNT) void qk_rope_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ cosv,
@@ -58,23 +85,27 @@ __global__ __launch_bounds__(kNT) void qk_rope_kernel(const uint16_t* __restrict
     const int64_t r = valid ? row : rows - 1;   // keep every lane in the shuffles
     const int64_t token = r / heads;
     const uint16_t* src = x + r * (3 * kDH) + li * 8;
-    float q[8], k[8], c[8], s[8];
     const u16x8 a = *reinterpret_cast<const u16x8*>(src);
     const u16x8 b = *reinterpret_cast<const u16x8*>(src + kDH);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) { q[e] = h2f(a[e]); k[e] = h2f(b[e]); c[e] = 1.0f; s[e] = 0.0f; }
+    // cos and the signed sin of the lane's 8 dims as fp16 pairs: the rotate-half term is -partner * sin for
+    // the first ROT/2 dims and +partner * sin for the next ROT/2 (the sign flip is exact)
+    f16x2 c2[4], s2[4];
     if (li < kROT / 8) {
         const u16x8 cc = *reinterpret_cast<const u16x8*>(cosv + token * kROT + li * 8);
-        const u16x8 ss = *reinterpret_cast<const u16x8*>(sinv + token * kROT + li * 8);
+        u16x8 ss = *reinterpret_cast<const u16x8*>(sinv + token * kROT + li * 8);
+        if (li < kROT / 16) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) { c[e] = h2f(cc[e]); s[e] = h2f(ss[e]); }
+            for (int e = 0; e < 8; ++e) ss[e] ^= 0x8000u;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            c2[j] = __builtin_bit_cast(f16x2, (uint32_t)cc[2 * j] | ((uint32_t)cc[2 * j + 1] << 16));
+            s2[j] = __builtin_bit_cast(f16x2, (uint32_t)ss[2 * j] | ((uint32_t)ss[2 * j + 1] << 16));
+        }
     }
-    norm_rope(q, eps, li, c, s);
-    norm_rope(k, eps, li, c, s);
+    const u16x8 oq = norm_rope(a, eps, li, c2, s2);
+    const u16x8 ok = norm_rope(b, eps, li, c2, s2);
     if (valid) {
-        u16x8 oq, ok;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) { oq[e] = f2h(q[e]); ok[e] = f2h(k[e]); }
         *reinterpret_cast<u16x8*>(qo + r * kDH + li * 8) = oq;
         *reinterpret_cast<u16x8*>(ko + r * kDH + li * 8) = ok;
     }
