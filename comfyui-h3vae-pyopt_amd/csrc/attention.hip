@@ -63,9 +63,6 @@ __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >>
 
 __device__ __forceinline__ float wave_pair_max(float v) { return __builtin_fmaxf(v, __shfl_xor(v, 32, 64)); }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
 // two fp32 -> packed fp16 (round to nearest even), one v_cvt_pk_f16_f32
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));

@@ -468,9 +468,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
                 uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
                 if (p.vec_out && gcol + 8 <= p.N) {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] = f2h(h2f(rv[i][e]) + h2f(v[e]));
-                    *reinterpret_cast<u16x8*>(dst) = v;
+                    *reinterpret_cast<u16x8*>(dst) = add_f16x8(rv[i], v);   // fp16(res + y), one rounding
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e)

@@ -98,11 +98,11 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     const int npix = hw - p0 < kChunk ? hw - p0 : kChunk;
     const uint16_t* base = x + ((int64_t)t * hw + p0) * C + cv * 8;
 
-    float pb[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) pb[e] = PRE_BIAS ? h2f(pre_bias[cv * 8 + e]) : 0.0f;
+    u16x8 pb{};
+    if constexpr (PRE_BIAS) pb = *reinterpret_cast<const u16x8*>(pre_bias + cv * 8);
     // The thread's whole slice of the chunk stays in registers for both passes:
-    // every load is issued up front and the data is read from memory once.
+    // every load is issued up front and the data is read from memory once.  The
+    // first pass replaces it by the pre-biased fp16 values.
     u16x8 xr[STEPS];
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
@@ -112,10 +112,6 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     auto load = [&](int s, float* v) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = h2f(xr[s][e]);
-        if constexpr (PRE_BIAS) {
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
-        }
     };
 
     float ls[GPT], vmx[8], vmn[8];
@@ -127,6 +123,7 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     for (int s = 0; s < STEPS; ++s) {
         int p = pl + s * PL;
         if (p >= npix) break;
+        if constexpr (PRE_BIAS) xr[s] = add_f16x8(xr[s], pb);   // fp16(x + b), one rounding
         float v[8];
         load(s, v);
 #pragma unroll
@@ -357,15 +354,12 @@ __global__ __launch_bounds__(kNT) void absmax_lut(const uint16_t* __restrict__ x
         if (t < 0) continue;   // causal zero frames
         const int si = reflect(ii - 1, h), sj = reflect(jj - 1, w);
         float v[8], gm[8], bt[8];
-        load8(x + (((int64_t)t * h + si) * w + sj) * C + cv * 8, v);
+        u16x8 xv = *reinterpret_cast<const u16x8*>(x + (((int64_t)t * h + si) * w + sj) * C + cv * 8);
+        if constexpr (PRE_BIAS) xv = add_f16x8(xv, *reinterpret_cast<const u16x8*>(pre_bias + cv * 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = h2f(xv[e]);
         load8(gamma + cv * 8, gm);
         load8(beta + cv * 8, bt);
-        if constexpr (PRE_BIAS) {
-            float pb[8];
-            load8(pre_bias + cv * 8, pb);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) v[e] = rt16(v[e] + pb[e]);
-        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int g = (cv * 8 + e) / CG;
@@ -437,10 +431,11 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
     const int nrow = (d + 2) * hp;
     const int rowvec = wp * TPP;                    // 8-channel vectors per padded row
     const int cv = threadIdx.x & (TPP - 1);
-    float gm[8], bt[8], pb[8] = {};
+    float gm[8], bt[8];
+    u16x8 pb{};
     load8(gamma + cv * 8, gm);
     load8(beta + cv * 8, bt);
-    if constexpr (PRE_BIAS) load8(pre_bias + cv * 8, pb);
+    if constexpr (PRE_BIAS) pb = *reinterpret_cast<const u16x8*>(pre_bias + cv * 8);
     const int g0 = cv * 8 / CG;
     int tcur = -1;
     float mean[NG], rstd[NG];
@@ -474,10 +469,10 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
                 const int j = j0 + u * kNT;
                 if (j >= rowvec) break;
                 int code[8];
+                const u16x8 xs = PRE_BIAS ? add_f16x8(xv[u], pb) : xv[u];   // fp16(x + b), one rounding
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    float ve = h2f(xv[u][e]);
-                    if constexpr (PRE_BIAS) ve = rt16(ve + pb[e]);
+                    const float ve = h2f(xs[e]);
                     const int k = (NG > 1) ? e / CG : 0;
                     code[e] = f2h(((ve - mean[k]) * rstd[k]) * gm[e] + bt[e]);
                 }
@@ -562,9 +557,10 @@ __global__ __launch_bounds__(kNT) void gn_stats_partial(const uint16_t* __restri
     const int npix = hw - p0 < G::CHUNK ? hw - p0 : G::CHUNK;
     const uint16_t* base = x + ((int64_t)t * hw + p0) * C + cv * G::CPT;
 
-    float pb[G::CPT];
+    u16x8 pb[G::NV] = {};
+    if constexpr (PRE_BIAS)
 #pragma unroll
-    for (int e = 0; e < G::CPT; ++e) pb[e] = PRE_BIAS ? h2f(pre_bias[cv * G::CPT + e]) : 0.0f;
+        for (int u = 0; u < G::NV; ++u) pb[u] = *reinterpret_cast<const u16x8*>(pre_bias + cv * G::CPT + 8 * u);
     u16x8 xr[G::STEPS][G::NV];
 #pragma unroll
     for (int s = 0; s < G::STEPS; ++s) {
@@ -578,10 +574,6 @@ __global__ __launch_bounds__(kNT) void gn_stats_partial(const uint16_t* __restri
         for (int u = 0; u < G::NV; ++u)
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[8 * u + e] = h2f(xr[s][u][e]);
-        if constexpr (PRE_BIAS) {
-#pragma unroll
-            for (int e = 0; e < G::CPT; ++e) v[e] = rt16(v[e] + pb[e]);
-        }
     };
     float ls[G::GPT];
 #pragma unroll
@@ -590,6 +582,9 @@ __global__ __launch_bounds__(kNT) void gn_stats_partial(const uint16_t* __restri
     for (int s = 0; s < G::STEPS; ++s) {
         const int p = pl + s * G::PL;
         if (p >= npix) break;
+        if constexpr (PRE_BIAS)   // fp16(x + b), one rounding; the second pass reads the biased values
+#pragma unroll
+            for (int u = 0; u < G::NV; ++u) xr[s][u] = add_f16x8(xr[s][u], pb[u]);
         float v[G::CPT];
         load(s, v);
 #pragma unroll
@@ -688,10 +683,11 @@ __global__ __launch_bounds__(kNT) void norm_pack_f16(const uint16_t* __restrict_
         return;
     }
     const int cv = threadIdx.x % TPP;
-    float gm[8], btv[8], pb[8] = {};
+    float gm[8], btv[8];
+    u16x8 pb{};
     load8(gamma + cv * 8, gm);
     load8(beta + cv * 8, btv);
-    if constexpr (PRE_BIAS) load8(pre_bias + cv * 8, pb);
+    if constexpr (PRE_BIAS) pb = *reinterpret_cast<const u16x8*>(pre_bias + cv * 8);
     const int frame = b * d + t;
     const int g0 = cv * 8 / CG;
     float mean[NG], rstd[NG];
@@ -702,12 +698,12 @@ __global__ __launch_bounds__(kNT) void norm_pack_f16(const uint16_t* __restrict_
     }
     const uint16_t* src = x + ((int64_t)frame * h + reflect(ii - 1, h)) * w * C + cv * 8;
     for (int j = threadIdx.x; j < rowvec; j += kNT) {
-        const u16x8 xv = *reinterpret_cast<const u16x8*>(src + (int64_t)reflect(j / TPP - 1, w) * C);
+        u16x8 xv = *reinterpret_cast<const u16x8*>(src + (int64_t)reflect(j / TPP - 1, w) * C);
+        if constexpr (PRE_BIAS) xv = add_f16x8(xv, pb);   // fp16(x + b), one rounding
         u16x8 out;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            float ve = h2f(xv[e]);
-            if constexpr (PRE_BIAS) ve = rt16(ve + pb[e]);
+            const float ve = h2f(xv[e]);
             const int k = (NG > 1) ? e / CG : 0;
             const float z = rt16(((ve - mean[k]) * rstd[k]) * gm[e] + btv[e]);
             out[e] = f2h(silu_fast(z));

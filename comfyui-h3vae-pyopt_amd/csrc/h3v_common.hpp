@@ -16,10 +16,22 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 typedef uint16_t u16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }
 __device__ __forceinline__ float rt16(float f) { return (float)(f16)f; }
+
+// Eight IEEE fp16 sums a + b (four v_pk_add_f16).  For fp16 operands this is bit for bit
+// fp16(float(a) + float(b)), the fp32 sum rounded to fp16: the fp32 sum of two fp16 values
+// rounds once and fp32's 24-bit significand is at least 2 * 11 + 2 bits, so rounding it again
+// to fp16 gives the correctly rounded sum (the double rounding is innocuous; checked over all
+// 2^32 pairs of finite fp16 values, overflow to infinity included).  A NaN stays a NaN.
+__device__ __forceinline__ u16x8 add_f16x8(u16x8 a, u16x8 b) {
+    return __builtin_bit_cast(u16x8, __builtin_bit_cast(f16x8, a) + __builtin_bit_cast(f16x8, b));
+}
 
 // exp(x) by Cody-Waite reduction and a degree-7 Taylor polynomial in Horner
 // form with fused multiply-adds:  n = rint(x*log2 e),

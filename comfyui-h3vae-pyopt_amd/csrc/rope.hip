@@ -23,14 +23,12 @@ constexpr int kROT = 48;
 constexpr int kNT = 256;
 constexpr int kLanesPerRow = 8;
 
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-
 // One (token, head) row of q or k held by 8 lanes: RMS normalisation, then the rotate-half RoPE on the
 // first ROT dims.  Every product of the rotation multiplies two fp16 values; their fp32 product is exact
 // (11-bit significands), so rounding it to fp16 is the IEEE fp16 product, and the products run as packed
-// fp16 multiplies (two per instruction) on the normalised row kept as fp16 pairs.  The sum of the two
-// rounded products is formed in fp32 and rounded to fp16 once more, as the reference chain does.
+// fp16 multiplies (two per instruction) on the normalised row kept as fp16 pairs.  The reference chain
+// adds the two rounded products in fp32 and rounds the sum to fp16; for fp16 operands that is the IEEE
+// fp16 sum (fp32 carries more than 2 * 11 + 2 significand bits), so the sum is a packed fp16 add too.
 __device__ __forceinline__ u16x8 norm_rope(const u16x8& in, float eps, int li, const f16x2 (&c2)[4],
                                            const f16x2 (&s2)[4]) {
     float v[8];
@@ -63,8 +61,11 @@ __device__ __forceinline__ u16x8 norm_rope(const u16x8& in, float eps, int li, c
         for (int j = 0; j < 4; ++j) {
             const f16x2 a = __builtin_bit_cast(f16x2, n2[j]) * c2[j];   // fp16(n * cos)
             const f16x2 b = __builtin_bit_cast(f16x2, r2[j]) * s2[j];   // fp16(+-partner * sin)
-            out[2 * j] = f2h((float)a[0] + (float)b[0]);
-            out[2 * j + 1] = f2h((float)a[1] + (float)b[1]);
+            // the pair is bit-cast whole: clang's __builtin_bit_cast of one element of an ext_vector reads
+            // element 0 whatever the index
+            const uint32_t y = __builtin_bit_cast(uint32_t, a + b);
+            out[2 * j] = (uint16_t)(y & 0xffffu);
+            out[2 * j + 1] = (uint16_t)(y >> 16);
         }
     } else {
 #pragma unroll
