@@ -10,15 +10,15 @@
 // counters to clear beforehand):
 //   gn_partial    grid (chunks, D): per 256-pixel chunk and group, avg and M2;
 //                 per chunk and channel max and min of the (pre-biased) input
-//                 (fp16, exact); block (0, 0) also zeroes the absmax word and
-//                 the done counter of absmax_lut
+//                 (fp16, exact); block (0, 0) also zeroes the two counters of
+//                 absmax_lut
 //   gn_merge      grid (32, D): Chan merge of the chunks -> (mean, rstd); the
-//                 per-channel extremes over the chunks give the absmax candidate
-//                 (below)
-//   absmax_lut    builds the int8 code of every fp16 pre-activation z under the
-//                 final scale; when the candidate cannot be proven exact it first
-//                 runs the full absmax pass and the last block to finish builds
-//                 the table
+//                 per-channel extremes over the chunks give the group's absmax
+//                 candidate (below), one word per (frame, group)
+//   absmax_lut    reduces the candidates, then builds the int8 code of every
+//                 fp16 pre-activation z under the final scale; when the candidate
+//                 cannot be proven exact it first runs the full absmax pass and
+//                 the last block to finish builds the table
 //   norm_pack_lut every padded value -> int8 through that table; writes the scale
 //
 // Quantize table.  After the normalisation rounds z to fp16, the rest of the
@@ -80,7 +80,7 @@ template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
                                                   int hw, int nchunk, float* __restrict__ part_avg,
                                                   float* __restrict__ part_m2, uint32_t* __restrict__ ext,
-                                                  uint32_t* __restrict__ amax_bits, uint32_t* __restrict__ done) {
+                                                  uint32_t* __restrict__ done) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
     constexpr int PL = kNT / TPP;
@@ -161,8 +161,7 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
         // the extremes are input values (fp16, or fp16-rounded with the pre-bias): exact as fp16
         ext[((int64_t)t * nchunk + j) * C + tid] = (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
     }
-    if (j == 0 && t == 0 && tid == 0) {   // for gn_merge and absmax_lut, which run after this kernel
-        *amax_bits = 0u;
+    if (j == 0 && t == 0 && tid == 0) {   // for absmax_lut, which runs after this kernel
         done[0] = 0u;
         done[1] = 0u;
     }
@@ -203,54 +202,96 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
     }
 }
 
-// One wave per (group, frame).  The group's chunk partials are staged through
-// LDS in batches and lane 0 merges them sequentially as in _merge; the lanes of
-// the group's channels then form the absmax candidates.
+// One wave per (group, frame).  lane 0 merges the group's chunk partials
+// sequentially as in _merge; the lanes of the group's channels then form the
+// absmax candidates.  Up to kMergeRegs * 64 chunks the partials are read once,
+// into registers, for both sums; more go through LDS in batches of kMergeBatch.
+constexpr int kMergeRegs = 4;
 constexpr int kMergeBatch = 1024;
+
+// LDS hand-off between the lanes of a one-wave workgroup: waits for the LDS
+// accesses only (__syncthreads() would also wait for loads still in flight).
+__device__ __forceinline__ void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Chan merge of one group's chunk partials (chunks of `chunk` pixels, the last
 // one short) by one wave: the terms of both sums are formed by all lanes and
 // lane 0 adds them in chunk order, so the result is the sequential merge of
-// _merge.  ms[0] = mean, ms[1] = rstd on return (after a barrier).
+// _merge.  `issue_loads()` runs right after the partials' loads are issued, so
+// that loads it issues stay in flight during the sums.  ms[0] = mean,
+// ms[1] = rstd on return (after a barrier).
+template <typename F>
 __device__ void gn_merge_group(const float* __restrict__ pa, const float* __restrict__ pm, int hw, int nchunk,
-                               int chunk, int cg, float eps, float* sa, float* sm, float* ms) {
+                               int chunk, int cg, float eps, float* sa, float* sm, float* ms, F&& issue_loads) {
     const int tid = threadIdx.x;
     const float total = (float)(hw * cg);
-    // pass 1: mean = (sum_j avg_j * n_j) / N
-    float san = 0.0f;
-    for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
-        const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
-        __syncthreads();
-        for (int i = tid; i < nb; i += 64) {
-            const int jj = j0 + i;
-            const int cnt = hw - jj * chunk < chunk ? hw - jj * chunk : chunk;
-            sa[i] = pa[jj] * (float)(cnt * cg);
+    auto weight = [&](int jj) { return (float)((hw - jj * chunk < chunk ? hw - jj * chunk : chunk) * cg); };
+    float san = 0.0f, sv = 0.0f;
+    if (nchunk <= 64 * kMergeRegs) {
+        // unconditional loads (an index past the last chunk re-reads it, and that value is not used), so
+        // that no branch separates them and the waits before the sums leave `issue_loads`' loads in flight
+        float a[kMergeRegs], m[kMergeRegs];
+#pragma unroll
+        for (int r = 0; r < kMergeRegs; ++r) {
+            const int jj = min(tid + 64 * r, nchunk - 1);
+            a[r] = pa[jj];
+            m[r] = pm[jj];
         }
-        __syncthreads();
+        issue_loads();
+        // pass 1: mean = (sum_j avg_j * n_j) / N
+#pragma unroll
+        for (int r = 0; r < kMergeRegs; ++r) {
+            const int jj = tid + 64 * r;
+            if (jj < nchunk) sa[jj] = a[r] * weight(jj);
+        }
+        wave_lds_sync();
         if (tid == 0) {
 #pragma unroll 16
-            for (int j = 0; j < nb; ++j) san = san + sa[j];
+            for (int j = 0; j < nchunk; ++j) san = san + sa[j];
+            ms[0] = san / total;
         }
-    }
-    if (tid == 0) ms[0] = san / total;
-    __syncthreads();
-    const float mean = ms[0];
-    // pass 2: var = (sum_j (m2_j + (n_j * d_j) * d_j)) / N
-    float sv = 0.0f;
-    for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
-        const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
-        __syncthreads();
-        for (int i = tid; i < nb; i += 64) {
-            const int jj = j0 + i;
-            const int cnt = hw - jj * chunk < chunk ? hw - jj * chunk : chunk;
-            const float dl = pa[jj] - mean;
-            const float nj = (float)(cnt * cg);
-            sm[i] = pm[jj] + (nj * dl) * dl;
+        wave_lds_sync();
+        const float mean = ms[0];
+        // pass 2: var = (sum_j (m2_j + (n_j * d_j) * d_j)) / N
+#pragma unroll
+        for (int r = 0; r < kMergeRegs; ++r) {
+            const int jj = tid + 64 * r;
+            if (jj < nchunk) {
+                const float dl = a[r] - mean;
+                sm[jj] = m[r] + (weight(jj) * dl) * dl;
+            }
         }
-        __syncthreads();
+        wave_lds_sync();
         if (tid == 0) {
 #pragma unroll 16
-            for (int j = 0; j < nb; ++j) sv = sv + sm[j];
+            for (int j = 0; j < nchunk; ++j) sv = sv + sm[j];
+        }
+    } else {
+        issue_loads();
+        for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
+            const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
+            wave_lds_sync();
+            for (int i = tid; i < nb; i += 64) sa[i] = pa[j0 + i] * weight(j0 + i);
+            wave_lds_sync();
+            if (tid == 0) {
+#pragma unroll 16
+                for (int j = 0; j < nb; ++j) san = san + sa[j];
+            }
+        }
+        if (tid == 0) ms[0] = san / total;
+        wave_lds_sync();
+        const float mean = ms[0];
+        for (int j0 = 0; j0 < nchunk; j0 += kMergeBatch) {
+            const int nb = nchunk - j0 < kMergeBatch ? nchunk - j0 : kMergeBatch;
+            wave_lds_sync();
+            for (int i = tid; i < nb; i += 64) {
+                const float dl = pa[j0 + i] - mean;
+                sm[i] = pm[j0 + i] + (weight(j0 + i) * dl) * dl;
+            }
+            wave_lds_sync();
+            if (tid == 0) {
+#pragma unroll 16
+                for (int j = 0; j < nb; ++j) sv = sv + sm[j];
+            }
         }
     }
     if (tid == 0) {
@@ -258,14 +299,14 @@ __device__ void gn_merge_group(const float* __restrict__ pa, const float* __rest
         if (var < 0.0f) var = 0.0f;
         ms[1] = rsqrt_rn(var + eps);
     }
-    __syncthreads();
+    wave_lds_sync();
 }
 
 __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
                                                const uint32_t* __restrict__ ext,
                                                const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
                                                int hw, int nchunk, int c, float eps, float* __restrict__ stats,
-                                               uint32_t* __restrict__ amax_bits) {
+                                               uint32_t* __restrict__ cands) {
     __shared__ float sa[kMergeBatch];
     __shared__ float sm[kMergeBatch];
     __shared__ float ms[2];
@@ -274,27 +315,45 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
     const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
     const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
 
-    gn_merge_group(pa, pm, hw, nchunk, kChunk, cg, eps, sa, sm, ms);
+    // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map of the channel's
+    // extreme over all chunks.  Lane l takes channel l % cg and every (64 / cg)-th chunk from l / cg,
+    // so all of the group's extreme loads are in flight at once (issued with the merge's own loads and
+    // read after the merge); lanes of one channel then combine by shuffles, and the cg candidates are
+    // evaluated in parallel lanes.  Max and min are exact in any order, so the candidate is the same as
+    // any other reduction order gives.
+    const int lpc = 64 / cg;                                  // lanes per channel (cg = 4 or 8)
+    const int e = tid % cg;
+    const int ch = g * cg + e;
+    const uint32_t* ep = ext + (int64_t)t * nchunk * c + ch;
+    constexpr int kExtRegs = 64 * kMergeRegs / 8;             // chunks per lane at cg = 8
+    const bool held = nchunk <= 64 * kMergeRegs;
+    uint32_t ek[kExtRegs];
+    gn_merge_group(pa, pm, hw, nchunk, kChunk, cg, eps, sa, sm, ms, [&] {
+        if (held) {
+#pragma unroll
+            for (int r = 0; r < kExtRegs; ++r)   // a clamped index re-reads the last chunk: max / min unchanged
+                ek[r] = ep[(int64_t)min(tid / cg + r * lpc, nchunk - 1) * c];
+        }
+    });
     if (tid == 0) {
         stats[(t * kGroups + g) * 2] = ms[0];
         stats[(t * kGroups + g) * 2 + 1] = ms[1];
     }
     const float mean = ms[0], rstd = ms[1];
-    // absmax candidate: fp16(silu(zmax)) per channel, zmax from the monotone map of the channel's
-    // extreme over all chunks.  Lane l takes channel l % cg and every (64 / cg)-th chunk from l / cg,
-    // so all of the group's extreme loads are in flight at once; lanes of one channel then combine
-    // by shuffles, and the cg candidates are evaluated in parallel lanes.  Max and min are exact in
-    // any order, so the candidate is the same as any other reduction order gives.
-    const int lpc = 64 / cg;                                  // lanes per channel (cg = 4 or 8)
-    const int e = tid % cg;
-    const int ch = g * cg + e;
-    const uint32_t* ep = ext + (int64_t)t * nchunk * c + ch;
     float vmx = -__builtin_inff(), vmn = __builtin_inff();
+    if (held) {
+#pragma unroll
+        for (int r = 0; r < kExtRegs; ++r) {
+            vmx = __builtin_fmaxf(vmx, h2f((uint16_t)(ek[r] & 0xffffu)));
+            vmn = __builtin_fminf(vmn, h2f((uint16_t)(ek[r] >> 16)));
+        }
+    } else {
 #pragma unroll 8
-    for (int j = tid / cg; j < nchunk; j += lpc) {
-        const uint32_t k = ep[(int64_t)j * c];
-        vmx = __builtin_fmaxf(vmx, h2f((uint16_t)(k & 0xffffu)));
-        vmn = __builtin_fminf(vmn, h2f((uint16_t)(k >> 16)));
+        for (int j = tid / cg; j < nchunk; j += lpc) {
+            const uint32_t k = ep[(int64_t)j * c];
+            vmx = __builtin_fmaxf(vmx, h2f((uint16_t)(k & 0xffffu)));
+            vmn = __builtin_fminf(vmn, h2f((uint16_t)(k >> 16)));
+        }
     }
     for (int off = cg; off < 64; off <<= 1) {
         vmx = __builtin_fmaxf(vmx, __shfl_xor(vmx, off, 64));
@@ -309,7 +368,9 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
     }
     for (int off = 1; off < cg; off <<= 1) cand = __builtin_fmaxf(cand, __shfl_xor(cand, off, 64));
     // every candidate is the |value| of a real element, so it never exceeds the true absmax
-    if (tid == 0) atomicMax(amax_bits, __builtin_bit_cast(uint32_t, cand));
+    // one word per (frame, group), reduced by absmax_lut: a plain store where a single atomic word would
+    // serialise every workgroup of the launch
+    if (tid == 0) cands[t * kGroups + g] = __builtin_bit_cast(uint32_t, cand);
 }
 
 __device__ __forceinline__ int reflect(int i, int n) { return i < 0 ? -i : (i >= n ? 2 * n - 2 - i : i); }
@@ -321,22 +382,38 @@ __device__ __forceinline__ void build_lut_range(float amax, int8_t* __restrict__
         lut[code] = (int8_t)e3_quant(rt16(silu(h2f((uint16_t)code))), s);
 }
 
-// The quantize table of norm_pack_lut.  When the absmax candidate is exact (almost always) the final
-// scale is known at once and the first 256 blocks build 256 table entries each.  Otherwise every block
-// runs its share of the full absmax pass into done[1]; the last block to finish (counter done[0])
-// stores the final absmax and builds the whole table from it.  The candidate word is not written
-// before every block has read it, so all blocks take the same branch.  gn_partial zeroed both words.
+// The quantize table of norm_pack_lut.  Every block first reduces gn_merge's (frame, group) candidates
+// to the absmax candidate (unsigned max of the bit patterns: non-negative floats order as their bits and
+// a NaN candidate ranks above every number, so it forces the full pass).  When the candidate is exact
+// (almost always) the final scale is known at once: block 0 stores it and the first 256 blocks build 256
+// table entries each.  Otherwise every block runs its share of the full absmax pass into done[1]; the
+// last block to finish (counter done[0]) stores the final absmax and builds the whole table from it.
+// All blocks compute the same candidate, so all take the same branch.  gn_partial zeroed both counters.
 // Grid: at least 256 blocks.
 template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void absmax_lut(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
                                                   const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
                                                   const float* __restrict__ stats, int d, int h, int w,
+                                                  const uint32_t* __restrict__ cands,
                                                   uint32_t* __restrict__ amax_bits, uint32_t* __restrict__ done,
                                                   int8_t* __restrict__ lut) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
-    const float cand = __builtin_bit_cast(float, *amax_bits);
+    __shared__ uint32_t cred[kNT / 64];
+    uint32_t cb = 0u;
+    for (int i = threadIdx.x; i < d * kGroups; i += kNT) cb = cands[i] > cb ? cands[i] : cb;
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)cb, off, 64);
+        cb = o > cb ? o : cb;
+    }
+    if ((threadIdx.x & 63) == 0) cred[threadIdx.x >> 6] = cb;
+    __syncthreads();
+    cb = cred[0];
+#pragma unroll
+    for (int i = 1; i < kNT / 64; ++i) cb = cred[i] > cb ? cred[i] : cb;
+    const float cand = __builtin_bit_cast(float, cb);
     if (cand >= kShortcutFloor) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) *amax_bits = cb;
         if (blockIdx.x < 65536 / kNT) build_lut_range(cand, lut, blockIdx.x * kNT, kNT);
         return;
     }
@@ -398,8 +475,8 @@ constexpr int kLutFloats = 65536 / 4;    // the int8 quantize table
 int64_t workspace_floats(int d, int h, int w) {
     int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
     // (avg, M2) per chunk and group; per chunk and channel the packed fp16 (max, min); the quantize table;
-    // 64 floats whose first word is absmax_lut's done counter
-    return 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC + kLutFloats + 64;
+    // 64 floats whose first words are absmax_lut's counters; the absmax candidate of every (frame, group)
+    return 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC + kLutFloats + 64 + (int64_t)d * kGroups;
 }
 
 // PASS 1 through the table.  Each block walks whole padded output rows
@@ -496,17 +573,18 @@ void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
     int8_t* lut = reinterpret_cast<int8_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC);
     uint32_t* done = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC +
                                                  kLutFloats);
-    // block (0, 0) zeroes the absmax word and the done counter: gn_merge and absmax_lut run after it
+    uint32_t* cands = done + 64;
+    // block (0, 0) zeroes absmax_lut's counters; gn_merge writes every candidate word
     hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
-                       part_m2, ext, amax_bits, done);
+                       part_m2, ext, done);
     hipLaunchKernelGGL(gn_merge, dim3(kGroups, d), dim3(64), 0, stream, part_avg, part_m2, ext, gamma, beta, hw,
-                       nchunk, C, eps, stats, amax_bits);
+                       nchunk, C, eps, stats, cands);
     const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
     int64_t want = (nvec + kNT - 1) / kNT;
     // grid-strided full pass (rarely run) with at least one block per 256 table entries
     unsigned blocks = (unsigned)(want > 1024 ? 1024 : (want < 256 ? 256 : want));
     hipLaunchKernelGGL((absmax_lut<C, PB>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
-                       w, amax_bits, done, lut);
+                       w, cands, amax_bits, done, lut);
     // 64 KB of LDS per block: two blocks per CU; each block walks many vectors
     unsigned lut_blocks = (unsigned)(want > 512 ? 512 : want);
     hipLaunchKernelGGL((norm_pack_lut<C, PB>), dim3(lut_blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats,
@@ -650,7 +728,7 @@ __global__ __launch_bounds__(64) void gn_stats_merge(const float* __restrict__ p
     const int g = blockIdx.x, t = blockIdx.y;
     const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
     const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
-    gn_merge_group(pa, pm, hw, nchunk, chunk, c / kGroups, eps, sa, sm, ms);
+    gn_merge_group(pa, pm, hw, nchunk, chunk, c / kGroups, eps, sa, sm, ms, [] {});
     if (threadIdx.x == 0) {
         stats[(t * kGroups + g) * 2] = ms[0];
         stats[(t * kGroups + g) * 2 + 1] = ms[1];

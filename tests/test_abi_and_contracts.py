@@ -36,8 +36,9 @@ def test_library_loads_and_exports_every_declared_symbol(ops):
     assert set(names) == table
     assert lib.h3v_abi_version() == ops.hip.ABI_VERSION
     # per-chunk (avg, M2) partials, per-chunk packed fp16 channel extremes (sized for 256 channels), the 64 KB
-    # quantize table, 64 floats of counters
-    assert lib.h3v_gn_norm_pack_workspace_floats(17, 256, 256) == 2 * 17 * 256 * 32 + 17 * 256 * 256 + 65536 // 4 + 64
+    # quantize table, 64 floats of counters, one absmax candidate word per (frame, group)
+    assert lib.h3v_gn_norm_pack_workspace_floats(17, 256, 256) == \
+        2 * 17 * 256 * 32 + 17 * 256 * 256 + 65536 // 4 + 64 + 17 * 32
     assert lib.h3v_gn_norm_pack_workspace_floats(0, 1, 1) == -1
     # K splits of the FP16 conv: conv_out (1024 -> 48 on 4 x 5 x 16 x 16, 20 row tiles of 256) 12 ways,
     # the 16^2 1024-channel conv (80 tiles of 256 x 256) 3 ways; full-chip convs and window-kernel convs none
