@@ -59,6 +59,10 @@ struct GemmParams {
     const float* sw;   // per weight row
     const uint16_t* bias;  // fp16 per weight row, nullable
     const uint16_t* res;   // fp16 residual in the output's layout, nullable: out = fp16(fp32(y) + fp32(res))
+    const uint16_t* res_bias;  // fp16 per column, nullable (with res): out = fp16(fp32(res) + (fp32(y) + fp32(res_bias)))
+    // conv3_halo_i8<..., PAD = true>: output [B, Do + pad_front, Ho + top + bottom, Wo + left + right, N],
+    // a reflect border of 0 or 1 on each side (see write_tile)
+    int pad_front, pad_top, pad_bottom, pad_left, pad_right;
     void* out;
     int64_t ldo;
     int tiles_m, tiles_n;
@@ -235,7 +239,7 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 // int32 accumulators of the workgroup's BM x BN tile at (m0, n0), weight tile
 // tn, is dequantized (or stored raw) to the output.  LDS_BYTES of LDS (the
 // operand rings, idle by now) stage the fp16 tile.
-template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, typename AccV>
+template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, int PADWO = 0, typename AccV>
 __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM / WGM / 32][BN / WGN / 32],
                                            int8_t* smem, int m0, int n0, int tn) {
     static_assert(kF16Ops<EP> == std::is_same<AccV, f32x16>::value, "fp32 accumulators with fp16 operands only");
@@ -426,6 +430,48 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
         else convert(std::false_type{});
         const int gcol0 = (EP == Epi::SwiGLU) ? tn * (BN / 2) : n0;
         uint16_t* out = static_cast<uint16_t*>(p.out);
+        // Padded output (PADWO = Wo, a tile of whole output rows of one frame): output pixel (t, i, j) of
+        // batch item b goes to [b, t + pad_front, i + top, j + left] of [B, Do + pad_front, Ho + top +
+        // bottom, Wo + left + right, N], and the reflect border of 0 or 1 per side is written with it: row
+        // 1 again as row 0 (top), row Ho - 2 as row Ho + top (bottom), likewise columns.  That is the input
+        // layout of the causal downsample conv that reads it.  Frames below pad_front are not written.
+        int64_t pframe = 0;   // first padded pixel row of the tile's frame
+        int oh0 = 0;
+        uint16_t* tile_out = out;   // padded position of the tile's output pixel (0, 0), channel 0
+        if constexpr (PADWO > 0) {
+            const int fpix = p.Ho * PADWO;
+            const int fr = m0 / fpix;
+            oh0 = (m0 - fr * fpix) / PADWO;
+            const int bi = fr / p.Do, od = fr - bi * p.Do;
+            pframe = ((int64_t)bi * (p.Do + p.pad_front) + od + p.pad_front) * (p.Ho + p.pad_top + p.pad_bottom);
+            tile_out = out + ((pframe + oh0 + p.pad_top) * (PADWO + p.pad_left + p.pad_right) + p.pad_left) * p.ldo;
+        }
+        // one 8-column chunk of output row r (grow = m0 + r); every caller has checked vec_out and N
+        auto store_chunk = [&](int r, int grow, int gcol, const u16x8& v) {
+            if constexpr (PADWO == 0) {
+                *reinterpret_cast<u16x8*>(out + (int64_t)grow * p.ldo + gcol) = v;
+            } else {
+                const int ri = r / PADWO, ow = r - ri * PADWO;
+                const int wp = PADWO + p.pad_left + p.pad_right;
+                // a tile spans 512 / Wo rows: the offset from tile_out stays below 2^31 elements
+                *reinterpret_cast<u16x8*>(tile_out + (ri * wp + ow) * (int)p.ldo + gcol) = v;
+                const int oh = oh0 + ri;
+                const bool rt = p.pad_top && oh == 1, rb = p.pad_bottom && oh == p.Ho - 2;
+                const bool cl = p.pad_left && ow == 1, cr = p.pad_right && ow == PADWO - 2;
+                if (rt | rb | cl | cr) {   // border pixels: the reflected copies
+                    // padded rows / columns that hold this pixel (-1: none)
+                    const int r0 = oh + p.pad_top, r1 = rt ? 0 : -1, r2 = rb ? p.Ho + p.pad_top : -1;
+                    const int c0 = ow + p.pad_left, c1 = cl ? 0 : -1, c2 = cr ? PADWO + p.pad_left : -1;
+                    auto put = [&](int pr, int pc) {
+                        if (pr >= 0 && pc >= 0)
+                            *reinterpret_cast<u16x8*>(out + ((pframe + pr) * wp + pc) * p.ldo + gcol) = v;
+                    };
+                    put(r0, c1); put(r0, c2);
+                    put(r1, c0); put(r1, c1); put(r1, c2);
+                    put(r2, c0); put(r2, c1); put(r2, c2);
+                }
+            }
+        };
         if (p.res == nullptr) {
             lds_barrier();   // the output tile is complete in LDS
 #pragma unroll 4
@@ -434,10 +480,10 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 const int grow = m0 + r, gcol = gcol0 + ch * 8;
                 if (grow >= p.M || gcol >= p.N) continue;
                 const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
-                uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
-                if (p.vec_out && gcol + 8 <= p.N) {
-                    *reinterpret_cast<u16x8*>(dst) = v;
+                if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
+                    store_chunk(r, grow, gcol, v);
                 } else {
+                    uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         if (gcol + e < p.N) dst[e] = v[e];
@@ -466,15 +512,23 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 const int grow = m0 + r, gcol = gcol0 + ch * 8;
                 if (idx >= BM * RCH || grow >= p.M || gcol >= p.N) continue;
                 u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
-                uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
-                if (p.vec_out && gcol + 8 <= p.N) {
-                    *reinterpret_cast<u16x8*>(dst) = add_f16x8(rv[i], v);   // fp16(res + y), one rounding
+                if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
+                    if (p.res_bias) {   // fp16(res + (y + b)): both adds in fp32, one rounding
+                        const u16x8 rb = *reinterpret_cast<const u16x8*>(p.res_bias + gcol);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[e] = f2h(h2f(rv[i][e]) + (h2f(v[e]) + h2f(rb[e])));
+                    } else {
+                        v = add_f16x8(rv[i], v);   // fp16(res + y), one rounding
+                    }
+                    store_chunk(r, grow, gcol, v);
                 } else {
+                    uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         if (gcol + e < p.N) {
                             const int64_t o = (int64_t)grow * p.ldo + gcol + e;
-                            dst[e] = f2h(h2f(p.res[o]) + h2f(v[e]));
+                            const float y = p.res_bias ? h2f(v[e]) + h2f(p.res_bias[gcol + e]) : h2f(v[e]);
+                            dst[e] = f2h(h2f(p.res[o]) + y);
                         }
                 }
             }
@@ -753,7 +807,7 @@ constexpr int halo_lds_bytes(int wo) {
 // ES = 1: int8 operands, v_mfma_i32_32x32x32_i8, int32 accumulators (32 channels per 32-byte slice);
 // ES = 2: fp16 operands, v_mfma_f32_32x32x16_f16, fp32 accumulators (16 channels per slice).  Both
 // MFMAs read 16 bytes per lane in the same row / k-half layout, so staging and fragments are shared.
-template <int WO, Epi EP, int ES = 1>
+template <int WO, Epi EP, int ES = 1, bool PAD = false>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
     using Acc = std::conditional_t<ES == 1, v16i, f32x16>;
@@ -944,7 +998,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
         run_stage(std::integral_constant<int, 1>{}, s + 1);
     }
 
-    write_tile<BM, BN, WGM, WGN, LDS, EP>(p, acc, smem, m0, n0, tn);
+    write_tile<BM, BN, WGM, WGN, LDS, EP, (PAD ? WO : 0)>(p, acc, smem, m0, n0, tn);
 }
 
 // Shape-general path (any K, any channel count, unaligned pointers): one thread
@@ -1126,7 +1180,7 @@ F16Plan plan_conv_f16(const GemmParams& p, bool may_split) {
     return {F16Kind::Tiled256x256k64, 1};
 }
 
-template <int WO, Epi EP, int ES = 1>
+template <int WO, Epi EP, int ES = 1, bool PAD = false>
 int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.tiles_m = p.M / 512;
     p.tiles_n = p.N / 128;
@@ -1143,7 +1197,8 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.b_bytes = (uint32_t)b_bytes;
     constexpr int lds = halo_lds_bytes(WO);
     static_assert(lds <= 163840, "LDS exceeds 160 KB");
-    auto kernel = &conv3_halo_i8<WO, EP, ES>;
+    auto kernel = &conv3_halo_i8<WO, EP, ES, PAD>;
+    if (PAD && !p.vec_out) return fail(H3V_EINVAL, "%s: the padded output needs 16-byte aligned out and residual", what);
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
     if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, lds,
@@ -1307,6 +1362,42 @@ int h3v_conv3d_i8_residual(const int8_t* qx, const float* x_scale, const int8_t*
     p.res = residual;
     p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
     return run_conv<Epi::Dequant>(p, stream, what);
+}
+
+int h3v_conv3d_i8_residual_padded(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                                  const uint16_t* bias, const uint16_t* residual, const uint16_t* residual_bias,
+                                  uint16_t* out, int batch, int cin, int d, int h, int w, int cout, int causal_skip,
+                                  int front, int top, int bottom, int left, int right, hipStream_t stream) {
+    const char* what = "h3v_conv3d_i8_residual_padded";
+    H3V_REQUIRE(qx && x_scale && qw && w_scale && out, "%s: null pointer argument", what);
+    H3V_REQUIRE(residual || !residual_bias, "%s: residual_bias needs a residual", what);
+    H3V_REQUIRE(residual != out, "%s: the residual must not alias the output", what);
+    H3V_REQUIRE(front >= 0 && front <= 16, "%s: front must be in [0, 16] (got %d)", what, front);
+    H3V_REQUIRE(cout <= 65536, "%s: at most 65536 output channels (got %d)", what, cout);
+    H3V_REQUIRE((top | bottom | left | right) >= 0 && (top | bottom | left | right) <= 1,
+                "%s: the reflect border is 0 or 1 on each side (got %d, %d, %d, %d)", what, top, bottom, left, right);
+    GemmParams p{};
+    int rc = fill_conv(p, what, batch, cin, d, h, w, cout, 3, 3, 3, 1, 1, 1);
+    if (rc) return rc;
+    p.a = qx; p.b = qw; p.sx = x_scale; p.sx_stride = 0; p.sw = w_scale; p.bias = bias; p.out = out;
+    p.res = residual;
+    p.res_bias = residual_bias;
+    p.pad_front = front;
+    p.pad_top = top; p.pad_bottom = bottom; p.pad_left = left; p.pad_right = right;
+    p.causal_skip = causal_skip ? 1 : 0;
+    H3V_REQUIRE(halo_conv_fits(p) && p.Ho >= 2 && p.Wo >= 2,
+                "%s: needs Cin %% 64 == 0, Cout %% 128 == 0, output width 32, 64, 128 or 256 and output height a "
+                "multiple of 512 / width, at least 2 (got Cin %d, Cout %d, output %d x %d)", what, cin, cout, p.Ho,
+                p.Wo);
+    H3V_REQUIRE(aligned(out, 16) && (!residual || aligned(residual, 16)) &&
+                    (!residual_bias || aligned(residual_bias, 16)),
+                "%s: out, residual and residual_bias need 16-byte alignment", what);
+    switch (p.Wo) {
+        case 256: return launch_halo<256, Epi::Dequant, 1, true>(p, stream, what);
+        case 128: return launch_halo<128, Epi::Dequant, 1, true>(p, stream, what);
+        case 64: return launch_halo<64, Epi::Dequant, 1, true>(p, stream, what);
+        default: return launch_halo<32, Epi::Dequant, 1, true>(p, stream, what);
+    }
 }
 
 static int conv3d_f16_common(const uint16_t* x, const uint16_t* w, const uint16_t* bias, const uint16_t* residual,

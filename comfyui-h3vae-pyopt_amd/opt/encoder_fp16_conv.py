@@ -272,6 +272,39 @@ class PointwiseConv(nn.Module):
         return y.view(b, d, h, w, -1).permute(0, 4, 1, 2, 3)
 
 
+_PADDED_INPUT = "_h3v_padded_input"
+
+
+def tag_padded_input(padded, front, border):
+    """The interior ``padded[:, :, front:, top:top + H, left:left + W]`` of a padded conv input that a
+    producer wrote directly, tagged so that ``PaddedCausalConv`` with the same front and border uses
+    ``padded`` as it is instead of packing the interior again.  The view holds the unpadded tensor's
+    values, so any other consumer sees the ordinary output."""
+    top, bottom, left, right = border
+    h = padded.shape[3] - top - bottom
+    w = padded.shape[4] - left - right
+    view = padded[:, :, front:, top:top + h, left:left + w]
+    setattr(view, _PADDED_INPUT, (padded, int(front), tuple(border)))
+    return view
+
+
+def padded_input_of(x, front, border):
+    """The tagged padded buffer behind ``x`` when it was written for this front and border, else None.
+    (Views made under inference mode do not record their base, so the check compares the view's data
+    pointer and strides with the interior of the tagged buffer.)"""
+    tag = getattr(x, _PADDED_INPUT, None)
+    if tag is None:
+        return None
+    padded, tfront, tborder = tag
+    if tfront != front or tborder != tuple(border):
+        return None
+    top, _, left, _ = tborder
+    inner = padded[:, :, front:, top:top + x.shape[3], left:left + x.shape[4]]
+    if x.shape != inner.shape or x.stride() != inner.stride() or x.data_ptr() != inner.data_ptr():
+        return None
+    return padded
+
+
 class PaddedCausalConv(nn.Module):
     """Zero frames in front + reflect border + valid conv (conv_in, the downsample convs).
 
@@ -298,6 +331,9 @@ class PaddedCausalConv(nn.Module):
             return conv3d_f16(tap_fold_pack(x, front), self.packed_weight(self.weight), self.bias, [3, 1, 1],
                               [1, 1, 1], front == 2)
         top, bottom, left, right = self.border
+        written = padded_input_of(x, front, self.border)
+        if written is not None:   # the producing conv already wrote this conv's padded input
+            return self.conv(written, causal_skip=front == 2)
         if x.shape[1] % 8 or max(top, bottom) >= x.shape[3] or max(left, right) >= x.shape[4]:
             raise ValueError(f"padded causal convolution: input {tuple(x.shape)} needs C % 8 == 0 and a reflect "
                              f"border {self.border} smaller than H, W")

@@ -139,6 +139,9 @@ class BiasFusedResidualBlock(torch.nn.Module):
         # None keeps the FP16 encoder mode.
         self.int8_first = None
         self.int8_second = None
+        # The padded conv that reads this block's output (the stage's downsample), when the block is the
+        # last of its stage: the INT8 second conv then writes that conv's padded input directly.
+        self.padded_consumer = None
 
     def _residual_body(self, x, second_bias):
         if self.int8_first is not None and self.int8_first.fuse_norm:
@@ -153,6 +156,18 @@ class BiasFusedResidualBlock(torch.nn.Module):
         return (self.int8_second(second_input) if self.int8_second is not None
                 else self.second.conv(second_input, with_bias=second_bias is not None, causal_skip=True))
 
+    def _padded_form(self, out_like):
+        """(front, border) when the INT8 second conv can write the padded input of ``padded_consumer``
+        for an output shaped like ``out_like``, else None."""
+        consumer = self.padded_consumer
+        if consumer is None or self.int8_second is None or not self.int8_second.fuse_norm:
+            return None
+        from .encoder_int8 import padded_output_fits
+        _, c, _, h, w = out_like.shape
+        if not padded_output_fits(self.int8_second.config.in_channels, c, h, w):
+            return None
+        return consumer.padded_input_form(out_like)
+
     def forward(self, x, zq=None):
         """(shortcut(x) or x) + body(x), the add fused into the second conv's epilogue where that conv is a
         kernel of this package (bit-identical to the separate fp16 add of the reference, :141)."""
@@ -161,6 +176,13 @@ class BiasFusedResidualBlock(torch.nn.Module):
         residual = self.shortcut_conv(x) if self.shortcut_conv is not None else x
         if self.int8_first is not None and self.int8_first.fuse_norm:
             h = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
+            form = self._padded_form(residual)
+            if form is not None:
+                from .encoder_fp16_conv import tag_padded_input
+                padded = self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias,
+                                                       self.second.eps, pre_bias=self.first.bias, residual=residual,
+                                                       pad_front=form[0], pad_border=form[1])
+                return tag_padded_input(padded, *form)
             return self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias, self.second.eps,
                                                  pre_bias=self.first.bias, residual=residual)
         if self.int8_first is None:

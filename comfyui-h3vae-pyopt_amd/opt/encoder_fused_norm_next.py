@@ -12,6 +12,7 @@ import torch
 
 from .encoder_fused_norm_bias import BiasFusedResidualBlock
 from .encoder_fused_residual_pack import ResidualDownsampleBlock
+from .encoder_internal_padding import ImplicitTemporalPadConv3d
 from .encoder_staged_batch import EncoderPrefix
 
 VARIANTS = ("bias", "extend_bias", "extend_bias_pack")
@@ -31,4 +32,10 @@ def next_fused_prefix(encoder, variant="extend_bias_pack"):
     if variant == "extend_bias_pack":
         prefix.stages[1].block[-1] = ResidualDownsampleBlock(encoder.down[1].block[-1], encoder.down[1].downsample)
         del prefix.stages[1].downsample
+        # A stage-0 downsample conv run as pack + native conv lets the stage's last block write that
+        # conv's padded input directly (INT8 mode).
+        down0 = getattr(prefix.stages[0], "downsample", None)
+        conv0 = getattr(down0, "conv", None)
+        if isinstance(conv0, ImplicitTemporalPadConv3d):
+            prefix.stages[0].block[-1].padded_consumer = conv0
     return prefix

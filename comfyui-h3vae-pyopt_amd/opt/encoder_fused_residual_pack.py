@@ -70,6 +70,19 @@ class ResidualDownsampleBlock(BiasFusedResidualBlock):
     def forward(self, x, zq=None):
         if zq is not None:
             raise ValueError("Unconditional inference only")
+        if self.int8_first is not None and self.int8_first.fuse_norm and self.int8_second.fuse_norm:
+            from .encoder_int8 import padded_output_fits
+            h, w = x.shape[3:]
+            if padded_output_fits(self.int8_second.config.in_channels, self.int8_second.config.out_channels, h, w):
+                # The second conv writes the pack's output itself: fp16(x + (conv + second.bias)) into the
+                # downsample's padded input (two zero frames, bottom / right reflect); bit-identical to the
+                # conv followed by residual_downsample_pack, without re-reading the conv output.
+                h1 = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
+                padded = self.int8_second.forward_norm(h1, self.second.norm_weight, self.second.norm_bias,
+                                                       self.second.eps, pre_bias=self.first.bias, residual=x,
+                                                       residual_bias=self.second.bias, pad_front=2,
+                                                       pad_border=(0, 1, 0, 1))
+                return self.down(padded)
         # second.bias is added by the pack, not by the second convolution
         h = self._residual_body(x, None)
         h = residual_downsample_pack(h, x, self.second.bias)

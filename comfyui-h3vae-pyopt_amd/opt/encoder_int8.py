@@ -13,7 +13,10 @@ the hot path):
   (``h3v_conv3d_i8`` / ``h3v_conv3d_i8_residual``); no im2col tensor and no
   FP16 fallback;
 * ``int8_valid_conv3d`` / ``HipInt8Conv3d`` (:453-506, :622-717) are the generic
-  entry and module wrapper, with the source module's padding done explicitly.
+  entry and module wrapper, with the source module's padding done explicitly;
+* ``_conv3d_from_quantized_padded`` (no counterpart: the reference pads in a
+  separate kernel) writes a stage's last conv straight into its downsample's
+  padded input (``h3v_conv3d_i8_residual_padded``).
 
 Activations and outputs are channels-last-3d (NDHWC).
 """
@@ -199,6 +202,46 @@ def _conv3d_from_quantized(qx, activation_scale, qweight, weight_scale, *, confi
         raise ValueError("residual must be an fp16 tensor of the convolution output's shape on its device")
     residual = residual.contiguous(memory_format=_CL3D)
     _hip.call("h3v_conv3d_i8_residual", *head, _hip.ptr(residual), _hip.ptr(out), *geometry, _hip.stream(qx.device))
+    return out
+
+
+def padded_output_fits(in_channels: int, out_channels: int, out_h: int, out_w: int) -> bool:
+    """Whether ``h3v_conv3d_i8_residual_padded`` takes a stride-1 3x3x3 conv of this geometry (the
+    window-in-LDS kernel: Cin % 64 == 0, Cout % 128 == 0, output width 32/64/128/256, output height a
+    multiple of 512 / width and at least 2)."""
+    return (in_channels % 64 == 0 and out_channels % 128 == 0 and out_w in (32, 64, 128, 256)
+            and out_h >= 2 and out_h % (512 // out_w) == 0)
+
+
+def _conv3d_from_quantized_padded(qx, activation_scale, qweight, weight_scale, *, bias, residual, residual_bias,
+                                  front: int, border):
+    """The stride-1 3x3x3 conv of a producer's int8 output written into the padded input of a causal
+    reflect-padded downsample: [B, Cout, Do + front, Ho + top + bottom, Wo + left + right]
+    (channels-last-3d) with the ``front`` leading frames zero and a reflect border ``border`` = (top,
+    bottom, left, right) of 0 or 1 per side.  ``residual`` (the output's shape, nullable) is added as
+    ``residual + out`` in fp16 would, or, with ``residual_bias``, as one rounding of ``residual + (out +
+    residual_bias)`` in fp32."""
+    _hip.require_gfx950(qx.device, "INT8 implicit conv")
+    config = Int8Conv3DConfig(qx.shape[1], qweight.shape[0], (3, 3, 3), (1, 1, 1))
+    b, cout, do, ho, wo = config.output_shape(qx.shape)
+    qx = qx.contiguous(memory_format=_CL3D)
+    top, bottom, left, right = (int(v) for v in border)
+    out = torch.empty((b, cout, do + front, ho + top + bottom, wo + left + right), dtype=torch.float16,
+                      device=qx.device, memory_format=_CL3D)
+    if front:
+        out[:, :, :front].zero_()
+    if residual is not None:
+        if tuple(residual.shape) != (b, cout, do, ho, wo) or residual.dtype != torch.float16 \
+                or residual.device != out.device:
+            raise ValueError("residual must be an fp16 tensor of the convolution output's shape on its device")
+        residual = residual.contiguous(memory_format=_CL3D)
+    if residual_bias is not None and (residual is None or tuple(residual_bias.shape) != (cout,)
+                                      or residual_bias.dtype != torch.float16):
+        raise ValueError("residual_bias needs a residual and must be an fp16 vector of the output channels")
+    _hip.call("h3v_conv3d_i8_residual_padded", _hip.ptr(qx), _hip.ptr(activation_scale), _hip.ptr(qweight),
+              _hip.ptr(weight_scale), _hip.ptr(bias), _hip.ptr(residual),
+              _hip.ptr(None if residual_bias is None else residual_bias.contiguous()), _hip.ptr(out),
+              *qx.shape, cout, 1, int(front), top, bottom, left, right, _hip.stream(qx.device))
     return out
 
 

@@ -118,6 +118,36 @@ def _int8_norm_conv3d_residual_fake(x, norm_weight, norm_bias, pre_bias, eps, qw
                        memory_format=torch.channels_last_3d)
 
 
+@torch.library.custom_op("h3vae_encoder::int8_norm_conv3d_residual_padded", mutates_args=(), device_types="cuda")
+def int8_norm_conv3d_residual_padded(x: torch.Tensor, norm_weight: torch.Tensor, norm_bias: torch.Tensor,
+                                     pre_bias: torch.Tensor | None, eps: float, qweight: torch.Tensor,
+                                     weight_scale: torch.Tensor, bias: torch.Tensor | None,
+                                     residual: torch.Tensor | None, residual_bias: torch.Tensor | None,
+                                     front: int, border: list[int]) -> torch.Tensor:
+    """The last conv of an encoder stage written as the padded input of the stage's causal stride-2
+    downsample: ``[B, Cout, D + front, H + top + bottom, W + left + right]``, zero leading frames, a reflect
+    border (top, bottom, left, right) of 0 or 1 per side.  The
+    residual add is that of ``int8_norm_conv3d_residual``, or with ``residual_bias`` the stage-1 residual
+    pack's ``residual + (out + bias)`` (opt/encoder_fused_residual_pack.py:12-33); the pack kernel that
+    would re-read the conv output (there, or ``causal_reflect_pack`` before the stage-0 downsample) is
+    not run."""
+    from .encoder_int8 import _conv3d_from_quantized_padded
+    from .encoder_int8_norm import quantized_temporal_norm_pad
+
+    qx, scale = quantized_temporal_norm_pad(x, norm_weight, norm_bias, eps, pre_bias=pre_bias)
+    return _conv3d_from_quantized_padded(qx, scale, qweight, weight_scale, bias=bias, residual=residual,
+                                         residual_bias=residual_bias, front=int(front), border=border)
+
+
+@int8_norm_conv3d_residual_padded.register_fake
+def _int8_norm_conv3d_residual_padded_fake(x, norm_weight, norm_bias, pre_bias, eps, qweight, weight_scale, bias,
+                                           residual, residual_bias, front, border):
+    b, _, d, h, w = x.shape
+    top, bottom, left, right = border
+    return torch.empty((b, qweight.shape[0], d + int(front), h + top + bottom, w + left + right), device=x.device,
+                       dtype=x.dtype, memory_format=torch.channels_last_3d)
+
+
 class Int8FusedValidConv3d(nn.Module):
     """Static-weight INT8 wrapper for an already-padded fused Conv3d call."""
 
@@ -164,8 +194,11 @@ class Int8FusedValidConv3d(nn.Module):
         self.bias.data = original_bias.to(device=self.bias.device, dtype=torch.float16)
         return result
 
-    def forward_norm(self, x, norm_weight, norm_bias, eps, pre_bias=None, residual=None):
-        """Fused producer + conv; ``residual`` adds the block's closing residual in the conv epilogue."""
+    def forward_norm(self, x, norm_weight, norm_bias, eps, pre_bias=None, residual=None, residual_bias=None,
+                     pad_front=None, pad_border=None):
+        """Fused producer + conv; ``residual`` adds the block's closing residual in the conv epilogue.
+        ``pad_front`` and ``pad_border`` (with ``residual_bias`` optional) return the padded input of the
+        stage's downsample instead (``int8_norm_conv3d_residual_padded``)."""
         if not self.fuse_norm:
             raise RuntimeError("INT8 norm fusion is not enabled for this convolution")
         if x.dtype != torch.float16:
@@ -173,6 +206,12 @@ class Int8FusedValidConv3d(nn.Module):
         if x.device != self.qweight.device:
             raise RuntimeError("INT8 encoder activation and qweight must be on the same device")
         bias = self.bias if self.apply_bias else None
+        if pad_front is not None:
+            return int8_norm_conv3d_residual_padded(x, norm_weight, norm_bias, pre_bias, eps, self.qweight,
+                                                    self.weight_scale, bias, residual, residual_bias, int(pad_front),
+                                                    [int(v) for v in pad_border])
+        if residual_bias is not None:
+            raise ValueError("residual_bias is only taken with pad_front")
         if residual is not None:
             return int8_norm_conv3d_residual(x, norm_weight, norm_bias, pre_bias, eps, self.qweight,
                                              self.weight_scale, bias, residual)

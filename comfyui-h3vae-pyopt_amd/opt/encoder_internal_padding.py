@@ -54,6 +54,14 @@ class ImplicitTemporalPadConv3d(torch.nn.Module):
     def forward(self, x):
         return self.native(x, self.front_video if x.shape[2] > 1 else self.front_image)
 
+    def padded_input_form(self, x):
+        """(front, border) of the padded input this conv builds for ``x`` when its reflect border is 0 or 1
+        per side, the form ``h3v_conv3d_i8_residual_padded`` writes, else None."""
+        native = self.native
+        if native.folded or any(b not in (0, 1) for b in native.border) or min(x.shape[3:]) < 2:
+            return None
+        return (self.front_video if x.shape[2] > 1 else self.front_image), native.border
+
 
 @dataclass
 class _Swap:

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define H3V_ABI_VERSION 1
+#define H3V_ABI_VERSION 2
 
 #define H3V_OK 0
 #define H3V_EINVAL 1   /* shape / dtype / alignment / contract violation */
@@ -205,6 +205,30 @@ int h3v_conv3d_i8_residual(const int8_t* qx, const float* x_scale, const int8_t*
                            const uint16_t* bias, const uint16_t* residual, uint16_t* out, int batch, int cin, int d,
                            int h, int w, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
                            hipStream_t stream);
+
+/* The last convolution of an encoder stage with its output written straight
+ * into the padded input of the stage's causal stride-2 downsample, so that no
+ * pack kernel re-reads it.  Replaces the conv + pack pairs of
+ * opt/encoder_fused_residual_pack.py:12-46 (stage 1: the second conv without
+ * bias, then residual_downsample_pack; border 0, 1, 0, 1) and, for the stage-0
+ * downsample, the block's residual conv followed by the zero frames and
+ * reflect padding of opt/encoder_internal_padding.py:27-36 (border 1, 1, 1, 1).
+ * A stride-1 3x3x3 conv (kd = kh = kw = 3): y = the fp16 output of
+ * h3v_conv3d_i8 (bias nullable); with residual (fp16 NDHWC [batch, do, ho, wo,
+ * cout]) v = fp16(fp32(residual) + fp32(y)), or with residual_bias (fp16
+ * [cout], the pack's bias) v = fp16(fp32(residual) + (fp32(y) +
+ * fp32(residual_bias))), one rounding.  out: fp16 NDHWC [batch, do + front,
+ * ho + top + bottom, wo + left + right, cout] with a reflect border of 0 or 1
+ * per side: out[b, front + t, top + i, left + j] = v[b, t, i, j]; row 1 is
+ * repeated as row 0 (top), row ho - 2 as row ho + top (bottom), likewise the
+ * columns; frames below `front` are not written (the caller zeroes them).
+ * Requires Cin % 64 == 0, Cout % 128 == 0, wo in {32, 64, 128, 256}, ho a
+ * multiple of 512 / wo and >= 2, 16-byte aligned out / residual /
+ * residual_bias, front in [0, 16]. */
+int h3v_conv3d_i8_residual_padded(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                                  const uint16_t* bias, const uint16_t* residual, const uint16_t* residual_bias,
+                                  uint16_t* out, int batch, int cin, int d, int h, int w, int cout, int causal_skip,
+                                  int front, int top, int bottom, int left, int right, hipStream_t stream);
 
 /* Raw int32 accumulators of the same convolution (exactness checks). */
 int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,

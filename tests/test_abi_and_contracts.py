@@ -70,6 +70,19 @@ def test_entry_points_reject_bad_arguments_before_any_launch(ops):
         ops.hip.call("h3v_tensor_quant_i8", 16, 0, 16, 16, 16, None)
     with pytest.raises(ValueError, match="blocks in"):
         ops.hip.call("h3v_probe_mfma_rate", 16, 16, 16, 16, 0, 1, 16, 16, None)
+    pad = ("h3v_conv3d_i8_residual_padded", 16, 32, 48, 64, None)
+    with pytest.raises(ValueError, match="output width"):   # output width 30 is not a window-kernel width
+        ops.hip.call(*pad, 80, None, 96, 1, 128, 4, 10, 32, 128, 1, 2, 1, 1, 1, 1, None)
+    with pytest.raises(ValueError, match="needs a residual"):
+        ops.hip.call(*pad, None, 80, 96, 1, 128, 4, 18, 34, 128, 1, 2, 0, 1, 0, 1, None)
+    with pytest.raises(ValueError, match="alias"):
+        ops.hip.call(*pad, 96, None, 96, 1, 128, 4, 18, 34, 128, 1, 2, 0, 1, 0, 1, None)
+    with pytest.raises(ValueError, match="front"):
+        ops.hip.call(*pad, 80, None, 96, 1, 128, 4, 18, 34, 128, 1, -1, 0, 1, 0, 1, None)
+    with pytest.raises(ValueError, match="reflect border"):
+        ops.hip.call(*pad, 80, None, 96, 1, 128, 4, 18, 34, 128, 1, 2, 0, 2, 0, 1, None)
+    with pytest.raises(ValueError, match="16-byte"):
+        ops.hip.call(*pad, 80, None, 98, 1, 128, 4, 18, 34, 128, 1, 2, 1, 1, 1, 1, None)
     # 4 operand sets x 8 MFMAs x 8 waves x 32^3 MACs x 2 ops per iteration
     assert ops.hip.lib().h3v_probe_mfma_ops_per_block(1) == 4 * 8 * 8 * 32 ** 3 * 2
 
@@ -152,6 +165,11 @@ def test_encoder_fake_shapes(ops):
                                torch.empty(128, dtype=torch.float16, device="meta"), None, 1e-6, qw,
                                torch.empty(256, device="meta"), None)
     assert tuple(y.shape) == (1, 256, 5, 8, 10)
+    assert y.is_contiguous(memory_format=torch.channels_last_3d)
+    y = integ.int8_norm_conv3d_residual_padded(x, torch.empty(128, dtype=torch.float16, device="meta"),
+                                               torch.empty(128, dtype=torch.float16, device="meta"), None, 1e-6, qw,
+                                               torch.empty(256, device="meta"), None, None, None, 2, [0, 1, 0, 1])
+    assert tuple(y.shape) == (1, 256, 7, 9, 11)      # two leading frames, one reflected row and column
     assert y.is_contiguous(memory_format=torch.channels_last_3d)
 
 
