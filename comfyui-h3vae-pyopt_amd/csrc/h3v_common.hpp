@@ -134,15 +134,30 @@ __device__ __forceinline__ int q1_quant(float a, const Q1Div& q) {
     return (int)v;
 }
 
-// q1_quant with the divisor's path chosen by the caller: FAST must equal q.fast.  A caller that branches
-// once per row on a wave-uniform q.fast runs straight-line code instead of a divergent branch per element.
+// The quotient of q1_quant (before its fp16 rounding), the divisor's path chosen by the caller:
+// FAST must equal q.fast.
 template <bool FAST>
-__device__ __forceinline__ int q1_quant_path(float a, const Q1Div& q) {
-    float v = rt16(FAST ? div_newton(a, q.d, q.r) : a / q.d);
-    v = __builtin_rintf(v);
-    if (v != v) return -128;
-    v = __builtin_fminf(127.0f, __builtin_fmaxf(-128.0f, v));
-    return (int)v;
+__device__ __forceinline__ float q1_quot(float a, const Q1Div& q) {
+    return FAST ? div_newton(a, q.d, q.r) : a / q.d;
+}
+
+// q1_quant's code chain for four quotients x, packed as four int8 codes (x0 in the low byte):
+// fp16(x) rounded to nearest even, that fp16 value rounded to the nearest integer (ties to even),
+// NaN -> -128, clamp [-128, 127].  Done in packed fp16: max(h, -128) sends a quotient's (quiet) NaN
+// to -128 (IEEE maxNum) and min(., 127) clamps; clamping before the integer rounding gives the same
+// codes at +-127.5 and -128.5.  Adding 1536 then moves [-128, 127] into [1408, 1663], where fp16
+// values are one apart, so the add itself rounds to the nearest integer, ties to even, and the low
+// byte of the sum's bit pattern is the code in two's complement.  Equal to q1_quant's chain for
+// every fp16 value h (all 65536 checked, NaN and infinities included).
+__device__ __forceinline__ uint32_t q1_codes4(float x0, float x1, float x2, float x3) {
+    const f16x2 lo = __builtin_convertvector((f32x2){x0, x1}, f16x2);
+    const f16x2 hi = __builtin_convertvector((f32x2){x2, x3}, f16x2);
+    const f16x2 vmin = {(f16)-128.0f, (f16)-128.0f}, vmax = {(f16)127.0f, (f16)127.0f};
+    const f16x2 mag = {(f16)1536.0f, (f16)1536.0f};
+    const f16x2 a = __builtin_elementwise_min(__builtin_elementwise_max(lo, vmin), vmax) + mag;
+    const f16x2 b = __builtin_elementwise_min(__builtin_elementwise_max(hi, vmin), vmax) + mag;
+    // bytes 0 and 2 of a (codes 0, 1), then bytes 0 and 2 of b (codes 2, 3)
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, b), __builtin_bit_cast(uint32_t, a), 0x06040200u);
 }
 
 // Per-tensor scale of the encoder activation quantizer: amax * fp32(1/127), 0 -> 1.

@@ -169,10 +169,10 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
                 float v[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = h2f(hv[c][e]);
-                uint32_t lo = pack4(q1_quant_path<F>(v[0], qd), q1_quant_path<F>(v[1], qd), q1_quant_path<F>(v[2], qd),
-                                    q1_quant_path<F>(v[3], qd));
-                uint32_t hi = pack4(q1_quant_path<F>(v[4], qd), q1_quant_path<F>(v[5], qd), q1_quant_path<F>(v[6], qd),
-                                    q1_quant_path<F>(v[7], qd));
+                const uint32_t lo = q1_codes4(q1_quot<F>(v[0], qd), q1_quot<F>(v[1], qd), q1_quot<F>(v[2], qd),
+                                              q1_quot<F>(v[3], qd));
+                const uint32_t hi = q1_codes4(q1_quot<F>(v[4], qd), q1_quot<F>(v[5], qd), q1_quot<F>(v[6], qd),
+                                              q1_quot<F>(v[7], qd));
                 *reinterpret_cast<uint2*>(q + r * K + col) = make_uint2(lo, hi);
             }
         };

@@ -29,10 +29,19 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return m;
 }
 
-// Quantize 8 values against the row divisor and store them as two 32-bit words.
+// Quantize 8 values against the row divisor and store them as two 32-bit words.  The divisor is the
+// same in every lane of the row: one uniform branch picks the quotient path.
 __device__ __forceinline__ void store_q8(int8_t* dst, const float* v, const Q1Div& d) {
-    uint32_t lo = pack4(q1_quant(v[0], d), q1_quant(v[1], d), q1_quant(v[2], d), q1_quant(v[3], d));
-    uint32_t hi = pack4(q1_quant(v[4], d), q1_quant(v[5], d), q1_quant(v[6], d), q1_quant(v[7], d));
+    uint32_t lo, hi;
+    if (__builtin_amdgcn_readfirstlane((int)d.fast)) {
+        lo = q1_codes4(q1_quot<true>(v[0], d), q1_quot<true>(v[1], d), q1_quot<true>(v[2], d), q1_quot<true>(v[3], d));
+        hi = q1_codes4(q1_quot<true>(v[4], d), q1_quot<true>(v[5], d), q1_quot<true>(v[6], d), q1_quot<true>(v[7], d));
+    } else {
+        lo = q1_codes4(q1_quot<false>(v[0], d), q1_quot<false>(v[1], d), q1_quot<false>(v[2], d),
+                       q1_quot<false>(v[3], d));
+        hi = q1_codes4(q1_quot<false>(v[4], d), q1_quot<false>(v[5], d), q1_quot<false>(v[6], d),
+                       q1_quot<false>(v[7], d));
+    }
     *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
 }
 
@@ -239,9 +248,11 @@ __global__ __launch_bounds__(kTensorThreads) void tensor_quantize(const uint16_t
 // ---------------------------------------------------------------------------
 // Self-test of the fast quotients against IEEE division, over every operand the
 // kernels can pass them: counts[0] = fp32 quotient mismatches and counts[1] =
-// quantized-code mismatches over all fp16 numerators (infinities excluded: a row
-// holding one has an infinite divisor and takes the IEEE path) and all finite
-// positive fp16 divisors; counts[2] = SiLU mismatches over all 65536 fp16 codes.
+// quantized-code mismatches (the fast quotient with the scalar code chain, and
+// with the packed-fp16 code chain the kernels use) over all fp16 numerators
+// (infinities excluded: a row holding one has an infinite divisor and takes the
+// IEEE path) and all finite positive fp16 divisors; counts[2] = SiLU mismatches
+// over all 65536 fp16 codes.
 // ---------------------------------------------------------------------------
 __global__ void zero_counts(uint32_t* c) {
     if (threadIdx.x < 3) c[threadIdx.x] = 0u;
@@ -264,7 +275,10 @@ __global__ __launch_bounds__(256) void selftest_q1_div(uint32_t* __restrict__ co
             const float d = h2f((uint16_t)dc);
             const Q1Div qd = q1_div(d);
             if (!same_bits(div_newton(a, d, qd.r), a / d)) ++bad_div;
-            if (q1_quant(a, qd) != q1_quant(a, d)) ++bad_q;
+            // the kernels' code path: the fast quotient, then the packed-fp16 code chain
+            const int ref = q1_quant(a, d);
+            const int packed = (int)(int8_t)(q1_codes4(q1_quot<true>(a, qd), 0.0f, 0.0f, 0.0f) & 0xFFu);
+            if (q1_quant(a, qd) != ref || packed != ref) ++bad_q;
         }
     }
     if (bad_div) atomicAdd(&counts[0], bad_div);

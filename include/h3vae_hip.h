@@ -57,9 +57,10 @@ int h3v_swiglu_row_quant(const uint16_t* x, int64_t rows, int64_t cols, int8_t* 
 /* Device self-test of the fast quotients the quantizers use instead of IEEE
  * division (no counterpart in the reference; it backs the bit-exactness claim).
  * counts: 3 uint32 of device memory, overwritten with the number of mismatches
- * against IEEE division: [0] fp32 quotients and [1] int8 codes over every fp16
- * numerator (infinities excluded) and every finite positive fp16 divisor, [2]
- * SiLU over every fp16 argument.  All three are zero on a correct build. */
+ * against IEEE division: [0] fp32 quotients and [1] int8 codes (scalar and
+ * packed-fp16 code chains) over every fp16 numerator (infinities excluded) and
+ * every finite positive fp16 divisor, [2] SiLU over every fp16 argument.  All
+ * three are zero on a correct build. */
 int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream);
 
 /* ---- encoder suffix / FP16 mode: GroupNorm + SiLU + pad producer, fp16 out ----
