@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kTensorThreads) void tensor_quantize(const uint16_t
 // Self-test of the fast quotients against IEEE division, over every operand the
 // kernels can pass them: counts[0] = fp32 quotient mismatches and counts[1] =
 // quantized-code mismatches (the fast quotient with the scalar code chain, and
-// with the packed-fp16 code chain the kernels use) over all fp16 numerators
+// the kernels' path: a * fl(1 / d) with the packed-fp16 code chain) over all fp16 numerators
 // (infinities excluded: a row holding one has an infinite divisor and takes the
 // IEEE path) and all finite positive fp16 divisors; counts[2] = SiLU mismatches
 // over all 65536 fp16 codes.
@@ -275,7 +275,7 @@ __global__ __launch_bounds__(256) void selftest_q1_div(uint32_t* __restrict__ co
             const float d = h2f((uint16_t)dc);
             const Q1Div qd = q1_div(d);
             if (!same_bits(div_newton(a, d, qd.r), a / d)) ++bad_div;
-            // the kernels' code path: the fast quotient, then the packed-fp16 code chain
+            // the kernels' code path: the reciprocal-multiply quotient, then the packed-fp16 code chain
             const int ref = q1_quant(a, d);
             const int packed = (int)(int8_t)(q1_codes4(q1_quot<true>(a, qd), 0.0f, 0.0f, 0.0f) & 0xFFu);
             if (q1_quant(a, qd) != ref || packed != ref) ++bad_q;
