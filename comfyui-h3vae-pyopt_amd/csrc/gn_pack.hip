@@ -107,7 +107,7 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
         const int p = pl + s * PL;
-        if (p < npix) xr[s] = *reinterpret_cast<const u16x8*>(base + (int64_t)p * C);
+        if (p < npix) xr[s] = load_nt(base + (int64_t)p * C);
     }
     auto load = [&](int s, float* v) {
 #pragma unroll
@@ -539,7 +539,7 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int j = j0 + u * kNT;
-                if (j < rowvec) xv[u] = *reinterpret_cast<const u16x8*>(src + (int64_t)reflect((j >> LOG_TPP) - 1, w) * C);
+                if (j < rowvec) xv[u] = load_nt(src + (int64_t)reflect((j >> LOG_TPP) - 1, w) * C);
             }
 #pragma unroll
             for (int u = 0; u < U; ++u) {
@@ -645,7 +645,7 @@ __global__ __launch_bounds__(kNT) void gn_stats_partial(const uint16_t* __restri
         const int p = pl + s * G::PL;
         if (p < npix)
 #pragma unroll
-            for (int u = 0; u < G::NV; ++u) xr[s][u] = *reinterpret_cast<const u16x8*>(base + (int64_t)p * C + 8 * u);
+            for (int u = 0; u < G::NV; ++u) xr[s][u] = load_nt(base + (int64_t)p * C + 8 * u);
     }
     auto load = [&](int s, float* v) {
 #pragma unroll
@@ -776,7 +776,7 @@ __global__ __launch_bounds__(kNT) void norm_pack_f16(const uint16_t* __restrict_
     }
     const uint16_t* src = x + ((int64_t)frame * h + reflect(ii - 1, h)) * w * C + cv * 8;
     for (int j = threadIdx.x; j < rowvec; j += kNT) {
-        u16x8 xv = *reinterpret_cast<const u16x8*>(src + (int64_t)reflect(j / TPP - 1, w) * C);
+        u16x8 xv = load_nt(src + (int64_t)reflect(j / TPP - 1, w) * C);
         if constexpr (PRE_BIAS) xv = add_f16x8(xv, pb);   // fp16(x + b), one rounding
         u16x8 out;
 #pragma unroll

@@ -24,6 +24,13 @@ __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_c
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }
 __device__ __forceinline__ float rt16(float f) { return (float)(f16)f; }
 
+// A 16-byte load marked non-temporal (global_load ... nt): for streams read once whose lines need
+// not stay in the caches.  A large activation read this way (the GroupNorm producers' input, 285 MB
+// at stage 0) streams at about 7 TB/s instead of 6.3.
+__device__ __forceinline__ u16x8 load_nt(const uint16_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u16x8*>(p));
+}
+
 // Eight IEEE fp16 sums a + b (four v_pk_add_f16).  For fp16 operands this is bit for bit
 // fp16(float(a) + float(b)), the fp32 sum rounded to fp16: the fp32 sum of two fp16 values
 // rounds once and fp32's 24-bit significand is at least 2 * 11 + 2 bits, so rounding it again

@@ -114,8 +114,8 @@ __global__ __launch_bounds__(kNT) void residual_rms_quant_kernel(const uint16_t*
     auto load = [&](u16x8 (&hx)[NCH], u16x8 (&ox)[NCH], int64_t r) {
 #pragma unroll
         for (int c = 0; c < NCH; ++c) {
-            hx[c] = *reinterpret_cast<const u16x8*>(h + r * K + c * 512 + lane * 8);
-            ox[c] = *reinterpret_cast<const u16x8*>(o + r * K + c * 512 + lane * 8);
+            hx[c] = load_nt(h + r * K + c * 512 + lane * 8);
+            ox[c] = load_nt(o + r * K + c * 512 + lane * 8);
         }
     };
     auto process = [&](const u16x8 (&hx)[NCH], const u16x8 (&ox)[NCH], int64_t r) {

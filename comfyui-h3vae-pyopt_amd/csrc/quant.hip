@@ -65,9 +65,9 @@ __global__ __launch_bounds__(kRowThreads) void row_quant_wave(const uint16_t* __
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         const int col = c * 512 + lane * 8;
-        v[c] = *reinterpret_cast<const u16x8*>(xr + col);
+        v[c] = load_nt(xr + col);
         if constexpr (SWIGLU) {
-            const u16x8 u = *reinterpret_cast<const u16x8*>(xr + K + col);
+            const u16x8 u = load_nt(xr + K + col);
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[c][e] = f2h(swiglu_value(v[c][e], u[e]));
         }
@@ -102,9 +102,9 @@ __global__ __launch_bounds__(kRowThreads) void row_quant_vec(const uint16_t* __r
     for (int c = 0; c < CH; ++c) {
         int idx = (c * kRowThreads + (int)threadIdx.x) * 8;
         if (idx < K) {
-            u16x8 a = *reinterpret_cast<const u16x8*>(xr + idx);
+            u16x8 a = load_nt(xr + idx);
             if constexpr (SWIGLU) {
-                u16x8 b = *reinterpret_cast<const u16x8*>(xr + K + idx);
+                u16x8 b = load_nt(xr + K + idx);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[c][e] = swiglu_value(a[e], b[e]);
             } else {
