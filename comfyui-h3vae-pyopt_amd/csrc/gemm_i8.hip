@@ -238,8 +238,11 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 // Epilogue of the tiled kernels: the wave's (BM/WGM) x (BN/WGN) block of
 // int32 accumulators of the workgroup's BM x BN tile at (m0, n0), weight tile
 // tn, is dequantized (or stored raw) to the output.  LDS_BYTES of LDS (the
-// operand rings, idle by now) stage the fp16 tile.
-template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, int PADWO = 0, typename AccV>
+// operand rings, idle by now) stage the fp16 tile.  SROWS: row r of the
+// wave's accumulator block i is wave row r * FM + i (strided rows of the
+// conv3_halo_i8 variant that reuses A fragments across kw taps) instead of
+// i * 32 + r.
+template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, int PADWO = 0, bool SROWS = false, typename AccV>
 __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM / WGM / 32][BN / WGN / 32],
                                            int8_t* smem, int m0, int n0, int tn) {
     static_assert(kF16Ops<EP> == std::is_same<AccV, f32x16>::value, "fp32 accumulators with fp16 operands only");
@@ -247,6 +250,8 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int RING = LDS_BYTES;
+    static_assert(!SROWS || ((EP == Epi::Dequant || EP == Epi::Int32) && FM == 4),
+                  "strided rows: int8 epilogues of 128-row wave blocks");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
@@ -257,6 +262,8 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
     // register quad.
     const int mrow = lane & 31;
     const int ncol = (lane >> 5) * 4;
+    // tile row of this lane's rows in accumulator block i
+    auto trow = [&](int i) { return wm * WM + (SROWS ? mrow * FM + i : i * 32 + mrow); };
     if constexpr (EP == Epi::F32Part) {
         // this split's partial sums, straight from the MFMA layout: 16 bytes (4 columns) per store
         float* part = static_cast<float*>(p.out) + (int64_t)blockIdx.y * p.M * p.ldo;
@@ -293,7 +300,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
 #pragma unroll
                 for (int i = 0; i < FM; ++i) {
-                    const int row = m0 + wm * WM + i * 32 + mrow;
+                    const int row = m0 + trow(i);
                     if (row >= p.M) continue;
                     int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
                     if (full) {
@@ -320,15 +327,18 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
         constexpr int SWM = (RCH < 32 ? RCH : 32) - 1;
         static_assert(RCH >= 8 && BM * OUTW * 2 <= RING, "output tile must fit the LDS ring");
         int8_t* ep = smem;
+        // chunk swizzle key of tile row r: the rows one store instruction writes (32 consecutive
+        // rows, or with SROWS rows FM apart) get distinct keys
+        auto skey = [](int r) { return (SROWS ? r >> 2 : r) & SWM; };
         auto put = [&](int r, int c, const u16x4& v) {   // c: tile column, a multiple of 4
             const int ch = c >> 3;
-            *reinterpret_cast<u16x4*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4) + ((c & 4) << 1)) = v;
+            *reinterpret_cast<u16x4*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4) + ((c & 4) << 1)) = v;
         };
         const bool has_bias = p.bias != nullptr;
         float sxr[FM];
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            const int row = m0 + wm * WM + i * 32 + mrow;
+            const int row = m0 + trow(i);
             sxr[i] = (EP != Epi::F16Bias && row < p.M) ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
         }
         // one instantiation per bias presence (uniform per launch)
@@ -397,7 +407,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                             float u = rt16(g1_reg<HB>(acc[i][2 * j + 1][q4 * 4 + e], sxr[i], qsw[q + 1][e], qb[q + 1][e]));
                             v[e] = f2h(silu(g) * u);
                         }
-                        put(wm * WM + i * 32 + mrow, tc, v);
+                        put(trow(i), tc, v);
                     }
                 }
             }
@@ -420,7 +430,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                                 v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]));
                             }
                         }
-                        put(wm * WM + i * 32 + mrow, tc, v);
+                        put(trow(i), tc, v);
                     }
                 }
             }
@@ -479,7 +489,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 const int r = idx / RCH, ch = idx - r * RCH;
                 const int grow = m0 + r, gcol = gcol0 + ch * 8;
                 if (grow >= p.M || gcol >= p.N) continue;
-                const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
+                const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
                 if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
                     store_chunk(r, grow, gcol, v);
                 } else {
@@ -511,7 +521,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 const int r = idx / RCH, ch = idx - r * RCH;
                 const int grow = m0 + r, gcol = gcol0 + ch * 8;
                 if (idx >= BM * RCH || grow >= p.M || gcol >= p.N) continue;
-                u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ (r & SWM)) << 4));
+                u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
                 if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
                     if (p.res_bias) {   // fp16(res + (y + b)): both adds in fp32, one rounding
                         const u16x8 rb = *reinterpret_cast<const u16x8*>(p.res_bias + gcol);
@@ -784,6 +794,30 @@ constexpr int halo_lds_bytes(int wo) {
     return ring > 512 * 128 * 2 ? ring : 512 * 128 * 2;
 }
 
+// Compile-time loop: f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// 16-byte slot (0..15) of half h of window pixel px inside its 256-byte line of 8 pixels, in the
+// strided-pixel variant of conv3_halo_i8.  Its fragment reads take pixels px0 + 4r (r = 0..15 in one
+// 16-lane group) and one half: two pixels of each of 8 consecutive lines, at line offsets a and
+// a + 4 (a = px0 & 3).  With L the line, b = (px >> 2) & 1 and a = px & 3, the slot is
+// ((b ^ (L >> 2)) & 1) << 3 | ((2a + h) ^ (b << 2) ^ (L & 3)): its low three bits are distinct over
+// the eight (L & 3, b) pairs of any 8 consecutive lanes (8-lane groups on 32 banks), and bit 3
+// separates lines L and L + 4, so 16 lanes hit 16 distinct slots (16-lane groups on 64 banks).  It
+// is a bijection of (px & 7, h) onto the line's 16 slots and depends on the column only, so the kh
+// shift (whole window rows, each a whole number of lines) keeps it.
+__device__ __forceinline__ int sp_slot(int px, int h) {
+    const int L = px >> 3, b = (px >> 2) & 1;
+    return (((b ^ (L >> 2)) & 1) << 3) | ((2 * (px & 3) + h) ^ (b << 2) ^ (L & 3));
+}
+
 // Stride-1 3x3x3 convolution with the input window of a tile held in LDS.
 //
 // A tile is BM = 512 consecutive output voxels = RO = 512 / WO whole output
@@ -807,9 +841,21 @@ constexpr int halo_lds_bytes(int wo) {
 // ES = 1: int8 operands, v_mfma_i32_32x32x32_i8, int32 accumulators (32 channels per 32-byte slice);
 // ES = 2: fp16 operands, v_mfma_f32_32x32x16_f16, fp32 accumulators (16 channels per slice).  Both
 // MFMAs read 16 bytes per lane in the same row / k-half layout, so staging and fragments are shared.
-template <int WO, Epi EP, int ES = 1, bool PAD = false>
+//
+// SP (strided pixels; int8 dequant or int32 output, WO >= 128, channels a multiple of 128): row r of a wave's accumulator
+// block i is the wave's output pixel 4r + i.  A wave's 128 pixels lie in one output row, and tap
+// (kh, kw) reads window pixels ow0 + 4r + i + kw: block i of tap kw is "virtual block" V[i + kw] of
+// the six V[v] = pixels ow0 + 4r + v (v = 0..5) of window row kh.  One kh's three taps read six A
+// fragments instead of twelve (4 fragment reads per 8 MFMAs instead of 6); the window lines are
+// swizzled by sp_slot for the stride-4 reads.  The blocks rotate through eight register slots, V[v]
+// of the g-th kh in slot (6g + v) % 8: a kh's last tap reads slots base + 2 .. base + 5, so the next
+// kh's first four blocks load into base + 6 .. base + 9 while it runs, as many registers as the
+// plain double buffer.
+template <int WO, Epi EP, int ES = 1, bool PAD = false, bool SP = false>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
+    static_assert(!SP || (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128),
+                  "strided pixels: int8, whole-row waves");
     using Acc = std::conditional_t<ES == 1, v16i, f32x16>;
     constexpr int BM = 512, BN = 128, WGM = 4, WGN = 2, NWD = 4;
     constexpr int WM = BM / WGM, WN = BN / WGN;
@@ -865,9 +911,21 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < NH; ++j) {
             const int s16 = (dw + NWD * j) * 64 + lane;       // 16-byte slot of the window buffer
-            const int pix = s16 >> 1;
-            int hr = pix / HPL, px = pix - hr * HPL;
-            const int half = (s16 & 1) ^ ((px >> 3) & 1);
+            int hr, px, half;
+            if constexpr (SP) {   // inverse of sp_slot inside the slot's 256-byte line
+                hr = s16 / (2 * HPL);
+                const int w = s16 - hr * (2 * HPL);
+                const int L = w >> 4, sl = w & 15;
+                const int b = ((sl >> 3) ^ (L >> 2)) & 1;
+                const int t = (sl & 7) ^ (b << 2) ^ (L & 3);
+                px = 8 * L + 4 * b + (t >> 1);
+                half = t & 1;
+            } else {
+                const int pix = s16 >> 1;
+                hr = pix / HPL;
+                px = pix - hr * HPL;
+                half = (s16 & 1) ^ ((px >> 3) & 1);
+            }
             // padding slots load a valid in-window pixel; they are never read
             if (hr >= HR) hr = HR - 1;
             if (px > WO + 1) px = WO + 1;
@@ -897,17 +955,6 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     // the 16-byte half (lane >> 5) of its pixel / weight row
     const int frow = lane & 31;
     const int fhi = lane >> 5;
-    int aaddr[FM][3];
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-        const int r = wm * WM + i * 32 + frow;
-        const int orow = r / WO, ow = r % WO;
-#pragma unroll
-        for (int kw = 0; kw < 3; ++kw) {
-            const int px = ow + kw;
-            aaddr[i][kw] = (orow * HPL + px) * 32 + ((fhi ^ ((px >> 3) & 1)) << 4);
-        }
-    }
     int baddr[FN];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
@@ -920,6 +967,119 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = Acc{};
+
+    // stage s covers depth tap kd0 + s / CQ and channel slice s % CQ; the issue
+    // position is kept as a running (kd, cq) pair
+    int ikd = kd0, icq = 0;
+    auto issue_next = [&](int slot) {
+        issue(ikd, icq, slot);
+        if (++icq == CQ) {
+            icq = 0;
+            ++ikd;
+        }
+    };
+    constexpr int NMFMA = FM * FN;
+
+    if constexpr (SP) {
+        static_assert(FM == 4 && WM == 128 && WO % WM == 0, "strided pixels: 4 blocks of 32 rows per wave");
+        const int orow = (wm * WM) / WO, ow0 = (wm * WM) % WO;
+        int vaddr[6];   // LDS offset of virtual block V[v] in window row kh = 0
+#pragma unroll
+        for (int v = 0; v < 6; ++v) {
+            const int px = ow0 + 4 * frow + v;   // at most WO + 1
+            vaddr[v] = orow * ROWB + (px >> 3) * 256 + (sp_slot(px, fhi) << 4);
+        }
+        v4i av[8], bq[2][FN];
+        auto ld_a = [&](int slot, int kh, int v, v4i& dst) {
+            dst = *reinterpret_cast<const v4i*>(smem + slot * STAGE + vaddr[v] + kh * ROWB);
+        };
+        auto ld_b = [&](int slot, int t9, v4i (&bf)[FN]) {
+            const int8_t* sb = smem + slot * STAGE + t9 * (BN * 32);
+#pragma unroll
+            for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const v4i*>(sb + baddr[j]);
+        };
+        issue_next(0);
+        issue_next(1);
+        wait_vmcnt<NH + NWT>();                               // stage 0 landed, stage 1 may be in flight
+        lds_barrier();
+#pragma unroll
+        for (int v = 0; v < 4; ++v) ld_a(0, 0, v, av[v]);
+        ld_b(0, 0, bq[0]);
+        // Stage Q of a group of four (LDS slot Q & 1; the register slots rotate with period four
+        // stages): tap (kh, kw) multiplies V[kw .. kw + 3] of its kh, then loads what the next tap
+        // adds: V[4] after kw = 0, V[5] after kw = 1, the next kh's V[0 .. 3] after kw = 2 (from the
+        // next stage's LDS slot after the stage's last tap), each with the next tap's weights.
+        auto run_stage = [&](auto q_c, int s) {
+            constexpr int Q = decltype(q_c)::value;
+            constexpr int SL = Q & 1;
+            static_for<9>([&](auto t_c) {
+                constexpr int T9 = decltype(t_c)::value;
+                constexpr int KH = T9 / 3, KW = T9 % 3;
+                constexpr int BASE = (2 * Q + 6 * KH) & 7;    // register slot of V[0] of this kh
+                constexpr int NB = (BASE + 6) & 7;            // register slot of V[0] of the next kh
+                constexpr int CUR = (Q + T9) & 1;
+                constexpr int NR = FN + (KW == 2 ? 4 : 1);    // fragment reads issued under this tap
+                auto mfma_tap = [&]() {
+#pragma unroll
+                    for (int i = 0; i < FM; ++i)
+#pragma unroll
+                        for (int j = 0; j < FN; ++j)
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bq[CUR][j], av[(BASE + KW + i) & 7],
+                                                                              acc[i][j], 0, 0, 0);
+                };
+                if constexpr (T9 == 8) {
+                    const bool more = s + 1 < nst;
+                    if (more) {
+                        wait_vmcnt<0>();                      // stage s+1 landed
+                        lds_barrier();                        // and every wave is done with slot SL
+                        if (s + 2 < nst) issue_next(SL);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfma_tap();
+                    if (more) {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) ld_a(SL ^ 1, 0, v, av[(NB + v) & 7]);
+                        ld_b(SL ^ 1, 0, bq[CUR ^ 1]);
+                    }
+                } else {
+                    mfma_tap();
+                    if constexpr (KW < 2) {
+                        ld_a(SL, KH, 4 + KW, av[(BASE + 4 + KW) & 7]);
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) ld_a(SL, KH + 1, v, av[(NB + v) & 7]);
+                    }
+                    ld_b(SL, T9 + 1, bq[CUR ^ 1]);
+                }
+#pragma unroll
+                for (int g = 0; g < NR; ++g) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, NMFMA / NR, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            });
+        };
+        for (int s = 0; s < nst; s += 4) {   // nst % 4 == 0: launch_halo takes SP only for C % 128 == 0
+            run_stage(std::integral_constant<int, 0>{}, s);
+            run_stage(std::integral_constant<int, 1>{}, s + 1);
+            run_stage(std::integral_constant<int, 2>{}, s + 2);
+            run_stage(std::integral_constant<int, 3>{}, s + 3);
+        }
+        write_tile<BM, BN, WGM, WGN, LDS, EP, (PAD ? WO : 0), true>(p, acc, smem, m0, n0, tn);
+        return;
+    }
+
+    int aaddr[FM][3];
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+        const int r = wm * WM + i * 32 + frow;
+        const int orow = r / WO, ow = r % WO;
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw) {
+            const int px = ow + kw;
+            aaddr[i][kw] = (orow * HPL + px) * 32 + ((fhi ^ ((px >> 3) & 1)) << 4);
+        }
+    }
 
     auto load_frags = [&](int slot, int t9, v4i (&af)[FM], v4i (&bf)[FN]) {
         const int8_t* s = smem + slot * STAGE;
@@ -942,17 +1102,6 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
             }
     };
 
-    // stage s covers depth tap kd0 + s / CQ and channel slice s % CQ; the issue
-    // position is kept as a running (kd, cq) pair
-    int ikd = kd0, icq = 0;
-    auto issue_next = [&](int slot) {
-        issue(ikd, icq, slot);
-        if (++icq == CQ) {
-            icq = 0;
-            ++ikd;
-        }
-    };
-
     v4i fa[2][FM], fb[2][FN];
     issue_next(0);
     issue_next(1);
@@ -961,7 +1110,6 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     load_frags(0, 0, fa[0], fb[0]);
 
     constexpr int NFRAG = FM + FN;
-    constexpr int NMFMA = FM * FN;
     // One stage: 9 taps, fragments double-buffered in registers across taps
     // (and across the stage boundary: the last tap's MFMAs hide the reads of the
     // next stage's first fragments).  With 9 taps the register buffer parity
@@ -1197,12 +1345,18 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.b_bytes = (uint32_t)b_bytes;
     constexpr int lds = halo_lds_bytes(WO);
     static_assert(lds <= 163840, "LDS exceeds 160 KB");
-    auto kernel = &conv3_halo_i8<WO, EP, ES, PAD>;
     if (PAD && !p.vec_out) return fail(H3V_EINVAL, "%s: the padded output needs 16-byte aligned out and residual", what);
-    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+    // the strided-pixel variant where it applies: int8 dequant, whole-row waves, stages in groups of four
+    constexpr bool kSp = ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128;
+    const bool sp = kSp && p.C % 128 == 0;
+    auto kernel = sp ? &conv3_halo_i8<WO, EP, ES, PAD, kSp> : &conv3_halo_i8<WO, EP, ES, PAD, false>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, false>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, lds,
-                                        hipGetErrorString(attr));
+    static const hipError_t attr_sp = kSp ? hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, kSp>),
+                                                                hipFuncAttributeMaxDynamicSharedMemorySize, lds)
+                                          : hipSuccess;
+    const hipError_t ae = attr != hipSuccess ? attr : attr_sp;
+    if (ae != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, lds, hipGetErrorString(ae));
     hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(512), lds, stream, p);
     return launch_status(what);
 }
