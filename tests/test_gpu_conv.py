@@ -78,6 +78,28 @@ def test_conv_all_ones_kat(ops):
     assert (acc == 3456).all()
 
 
+@pytest.mark.parametrize("b,c,d,h,w,co,samples", [
+    # 12 channel slices (the strided-pixel kernel runs its stages in groups of four), Wo 128: 128 tiles
+    (1, 384, 10, 66, 130, 128, [(0, 0), (0, 1), (0, 7)]),
+    # Wo 256, three weight tiles, two batch items: 192 tiles
+    (2, 128, 4, 34, 258, 384, [(0, 0), (1, 1)]),
+])
+def test_conv_strided_pixel_shapes_sampled(ops, oracle, b, c, d, h, w, co, samples):
+    """Window convs large enough (at least 128 tiles) to run the strided-pixel window kernel rather than
+    the small-conv implicit GEMM: exact int32 against the oracle on the first output rows of sampled
+    (batch, frame) pairs, with the causal skip."""
+    gen = _gen(c + co + w)
+    qx = torch.randint(-127, 128, (b, d, h, w, c), generator=gen, dtype=torch.int8)
+    qx[:, :2] = 0
+    qw = torch.randint(-127, 128, (co, 27 * c), generator=gen, dtype=torch.int8)
+    print(f"strided-pixel window conv {b}x{c}x{d}x{h}x{w} -> {co}", flush=True)
+    acc = _conv_i32_gpu(ops, qx, qw, (3, 3, 3), (1, 1, 1), True)
+    rows = 512 // (w - 2)                                        # output rows of one tile
+    for bi, t in samples:
+        want = oracle.conv3d_acc(qx[bi:bi + 1, t:t + 3, :2 * rows + 2].numpy(), qw.numpy(), (3, 3, 3), (1, 1, 1))
+        assert np.array_equal(acc[bi:bi + 1, t:t + 1, :2 * rows], want), f"batch {bi} frame {t}"
+
+
 def test_conv_h3_stage0_shape_sampled(ops, oracle):
     """Real stage-0 layer: [1,128,19,258,258] int8 -> [1,17,256,256,128], causal skip; frames sampled."""
     gen = _gen(11)
