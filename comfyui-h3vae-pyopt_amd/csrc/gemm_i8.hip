@@ -241,8 +241,11 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 // operand rings, idle by now) stage the fp16 tile.  SROWS: row r of the
 // wave's accumulator block i is wave row r * FM + i (strided rows of the
 // conv3_halo_i8 variant that reuses A fragments across kw taps) instead of
-// i * 32 + r.
-template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, int PADWO = 0, bool SROWS = false, typename AccV>
+// i * 32 + r.  TILEW > 0: the tile is 512 / TILEW output rows of TILEW pixels each (a column block
+// of output rows p.Wo wide) starting at row m0, so tile row r is output row
+// m0 + (r / TILEW) * p.Wo + r % TILEW; 0: the tile's rows are consecutive from m0.
+template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, int PADWO = 0, bool SROWS = false, int TILEW = 0,
+          typename AccV>
 __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM / WGM / 32][BN / WGN / 32],
                                            int8_t* smem, int m0, int n0, int tn) {
     static_assert(kF16Ops<EP> == std::is_same<AccV, f32x16>::value, "fp32 accumulators with fp16 operands only");
@@ -262,8 +265,9 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
     // register quad.
     const int mrow = lane & 31;
     const int ncol = (lane >> 5) * 4;
-    // tile row of this lane's rows in accumulator block i
+    // tile row of this lane's rows in accumulator block i, and the output row of tile row r
     auto trow = [&](int i) { return wm * WM + (SROWS ? mrow * FM + i : i * 32 + mrow); };
+    auto gidx = [&](int r) { return TILEW ? m0 + (r / TILEW) * p.Wo + r % TILEW : m0 + r; };
     if constexpr (EP == Epi::F32Part) {
         // this split's partial sums, straight from the MFMA layout: 16 bytes (4 columns) per store
         float* part = static_cast<float*>(p.out) + (int64_t)blockIdx.y * p.M * p.ldo;
@@ -300,7 +304,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
 #pragma unroll
                 for (int i = 0; i < FM; ++i) {
-                    const int row = m0 + trow(i);
+                    const int row = gidx(trow(i));
                     if (row >= p.M) continue;
                     int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
                     if (full) {
@@ -338,7 +342,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
         float sxr[FM];
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
-            const int row = m0 + trow(i);
+            const int row = gidx(trow(i));
             sxr[i] = (EP != Epi::F16Bias && row < p.M) ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
         }
         // one instantiation per bias presence (uniform per launch)
@@ -446,25 +450,27 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
         // 1 again as row 0 (top), row Ho - 2 as row Ho + top (bottom), likewise columns.  That is the input
         // layout of the causal downsample conv that reads it.  Frames below pad_front are not written.
         int64_t pframe = 0;   // first padded pixel row of the tile's frame
-        int oh0 = 0;
+        int oh0 = 0, ow0 = 0;
         uint16_t* tile_out = out;   // padded position of the tile's output pixel (0, 0), channel 0
+        constexpr int TWP = TILEW ? TILEW : (PADWO > 0 ? PADWO : 1);   // pixels per tile row
         if constexpr (PADWO > 0) {
             const int fpix = p.Ho * PADWO;
             const int fr = m0 / fpix;
             oh0 = (m0 - fr * fpix) / PADWO;
+            ow0 = (m0 - fr * fpix) - oh0 * PADWO;
             const int bi = fr / p.Do, od = fr - bi * p.Do;
             pframe = ((int64_t)bi * (p.Do + p.pad_front) + od + p.pad_front) * (p.Ho + p.pad_top + p.pad_bottom);
-            tile_out = out + ((pframe + oh0 + p.pad_top) * (PADWO + p.pad_left + p.pad_right) + p.pad_left) * p.ldo;
+            tile_out = out + ((pframe + oh0 + p.pad_top) * (PADWO + p.pad_left + p.pad_right) + p.pad_left + ow0) * p.ldo;
         }
-        // one 8-column chunk of output row r (grow = m0 + r); every caller has checked vec_out and N
+        // one 8-column chunk of tile row r (output row grow = gidx(r)); every caller has checked vec_out and N
         auto store_chunk = [&](int r, int grow, int gcol, const u16x8& v) {
             if constexpr (PADWO == 0) {
                 *reinterpret_cast<u16x8*>(out + (int64_t)grow * p.ldo + gcol) = v;
             } else {
-                const int ri = r / PADWO, ow = r - ri * PADWO;
+                const int ri = r / TWP, owr = r - ri * TWP, ow = ow0 + owr;
                 const int wp = PADWO + p.pad_left + p.pad_right;
-                // a tile spans 512 / Wo rows: the offset from tile_out stays below 2^31 elements
-                *reinterpret_cast<u16x8*>(tile_out + (ri * wp + ow) * (int)p.ldo + gcol) = v;
+                // a tile spans 512 / TWP rows: the offset from tile_out stays below 2^31 elements
+                *reinterpret_cast<u16x8*>(tile_out + (ri * wp + owr) * (int)p.ldo + gcol) = v;
                 const int oh = oh0 + ri;
                 const bool rt = p.pad_top && oh == 1, rb = p.pad_bottom && oh == p.Ho - 2;
                 const bool cl = p.pad_left && ow == 1, cr = p.pad_right && ow == PADWO - 2;
@@ -487,7 +493,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
 #pragma unroll 4
             for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
                 const int r = idx / RCH, ch = idx - r * RCH;
-                const int grow = m0 + r, gcol = gcol0 + ch * 8;
+                const int grow = gidx(r), gcol = gcol0 + ch * 8;
                 if (grow >= p.M || gcol >= p.N) continue;
                 const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
                 if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
@@ -510,7 +516,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
             for (int i = 0; i < PER; ++i) {
                 const int idx = tid + i * NT;
                 const int r = idx / RCH, ch = idx - r * RCH;
-                const int grow = m0 + r, gcol = gcol0 + ch * 8;
+                const int grow = gidx(r), gcol = gcol0 + ch * 8;
                 if (idx < BM * RCH && grow < p.M && p.vec_out && gcol + 8 <= p.N)
                     rv[i] = *reinterpret_cast<const u16x8*>(p.res + (int64_t)grow * p.ldo + gcol);
             }
@@ -519,7 +525,7 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
             for (int i = 0; i < PER; ++i) {
                 const int idx = tid + i * NT;
                 const int r = idx / RCH, ch = idx - r * RCH;
-                const int grow = m0 + r, gcol = gcol0 + ch * 8;
+                const int grow = gidx(r), gcol = gcol0 + ch * 8;
                 if (idx >= BM * RCH || grow >= p.M || gcol >= p.N) continue;
                 u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
                 if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
@@ -851,18 +857,24 @@ __device__ __forceinline__ int sp_slot(int px, int h) {
 // of the g-th kh in slot (6g + v) % 8: a kh's last tap reads slots base + 2 .. base + 5, so the next
 // kh's first four blocks load into base + 6 .. base + 9 while it runs, as many registers as the
 // plain double buffer.
-template <int WO, Epi EP, int ES = 1, bool PAD = false, bool SP = false>
+//
+// TW < WO (with SP; Wo 256 as column blocks of 128): a tile is RO = 512 / TW output rows of a TW-pixel
+// column block, so its window is RO + 2 rows of TW + 2 pixels (6 x 130 instead of 4 x 258 pixels at
+// Wo 256: 7 window DMA instructions per issuing wave and stage instead of 9).
+template <int WO, Epi EP, int ES = 1, bool PAD = false, bool SP = false, int TW = WO>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
-    static_assert(!SP || (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128),
+    static_assert(!SP || (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && TW >= 128),
                   "strided pixels: int8, whole-row waves");
+    static_assert(TW == WO || (SP && WO % TW == 0), "column blocks: strided-pixel kernel only");
     using Acc = std::conditional_t<ES == 1, v16i, f32x16>;
     constexpr int BM = 512, BN = 128, WGM = 4, WGN = 2, NWD = 4;
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int RO = BM / WO;                               // output rows per tile
+    constexpr int RO = BM / TW;                               // output rows per tile
+    constexpr int NCB = WO / TW;                              // column blocks per output row
     constexpr int HR = RO + 2;                                // window rows
-    constexpr int HPL = (WO + 2 + 15) / 16 * 16;              // LDS pixels per window row
+    constexpr int HPL = (TW + 2 + 15) / 16 * 16;              // LDS pixels per window row
     constexpr int ROWB = HPL * 32;                            // LDS bytes per window row
     constexpr int HB = (HR * ROWB + 4095) / 4096 * 4096;      // window bytes (whole instructions per issuing wave)
     constexpr int WB = 9 * BN * 32;                           // weight bytes of a stage
@@ -871,7 +883,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int LDS = 2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2;
     static_assert(WO == 32 || WO == 64 || WO == 128 || WO == 256, "output width");
     static_assert(LDS <= 163840, "LDS");
-    static_assert(LDS == halo_lds_bytes(WO), "host and kernel LDS sizes");
+    static_assert(LDS == halo_lds_bytes(TW), "host and kernel LDS sizes");
     static_assert(NH + NWT < 64, "outstanding DMA must fit vmcnt");
 
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
@@ -881,18 +893,21 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int wm = wave / WGN, wn = wave % WGN;
 
-    // tile -> (row block, frame, weight tile); the weight tiles of one window are
-    // adjacent, then the frames of one row block (they share input rows in L2)
+    // tile -> (row block, column block, frame, weight tile); the weight tiles of one window are
+    // adjacent, then the frames of one row and column block (they share input rows in L2)
     int id = xcd_remap(blockIdx.x, gridDim.x);
     const int tn = id % p.tiles_n;
     id /= p.tiles_n;
     const int nfr = p.M / (p.Ho * WO);                        // batch * Do
     const int fr = id % nfr;
-    const int rb = id / nfr;
+    id /= nfr;
+    const int cb = id % NCB;
+    const int rb = id / NCB;
     const int od = fr % p.Do;
     const int bi = fr / p.Do;
     const int oh0 = rb * RO;
-    const int m0 = (fr * p.Ho + oh0) * WO;
+    const int owb = cb * TW;                                  // first output column of the tile
+    const int m0 = (fr * p.Ho + oh0) * WO + owb;
     const int n0 = tn * BN;
     const int CB = p.C * ES;                                  // bytes per pixel
     const int CQ = CB / 32;                                   // 32-byte channel slices
@@ -907,7 +922,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     // per-lane DMA source offsets; the stage adds kd and the channel slice as the uniform offset
     uint32_t hoff[NH], woff[NWT];
     {
-        const uint32_t tile_base = (uint32_t)(((int64_t)(bi * p.Dp + od) * p.Hp + oh0) * p.Wp * CB);
+        const uint32_t tile_base = (uint32_t)((((int64_t)(bi * p.Dp + od) * p.Hp + oh0) * p.Wp + owb) * CB);
 #pragma unroll
         for (int j = 0; j < NH; ++j) {
             const int s16 = (dw + NWD * j) * 64 + lane;       // 16-byte slot of the window buffer
@@ -928,7 +943,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
             }
             // padding slots load a valid in-window pixel; they are never read
             if (hr >= HR) hr = HR - 1;
-            if (px > WO + 1) px = WO + 1;
+            if (px > TW + 1) px = TW + 1;
             hoff[j] = tile_base + (uint32_t)((hr * p.Wp + px) * CB + half * 16);
         }
 #pragma unroll
@@ -981,12 +996,12 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int NMFMA = FM * FN;
 
     if constexpr (SP) {
-        static_assert(FM == 4 && WM == 128 && WO % WM == 0, "strided pixels: 4 blocks of 32 rows per wave");
-        const int orow = (wm * WM) / WO, ow0 = (wm * WM) % WO;
+        static_assert(FM == 4 && WM == 128 && TW % WM == 0, "strided pixels: 4 blocks of 32 rows per wave");
+        const int orow = (wm * WM) / TW, ow0 = (wm * WM) % TW;
         int vaddr[6];   // LDS offset of virtual block V[v] in window row kh = 0
 #pragma unroll
         for (int v = 0; v < 6; ++v) {
-            const int px = ow0 + 4 * frow + v;   // at most WO + 1
+            const int px = ow0 + 4 * frow + v;   // at most TW + 1
             vaddr[v] = orow * ROWB + (px >> 3) * 256 + (sp_slot(px, fhi) << 4);
         }
         v4i av[8], bq[2][FN];
@@ -1065,7 +1080,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
             run_stage(std::integral_constant<int, 2>{}, s + 2);
             run_stage(std::integral_constant<int, 3>{}, s + 3);
         }
-        write_tile<BM, BN, WGM, WGN, LDS, EP, (PAD ? WO : 0), true>(p, acc, smem, m0, n0, tn);
+        write_tile<BM, BN, WGM, WGN, LDS, EP, (PAD ? WO : 0), true, (TW < WO ? TW : 0)>(p, acc, smem, m0, n0, tn);
         return;
     }
 
@@ -1343,21 +1358,25 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
                     (long long)a_bytes, (long long)b_bytes);
     p.a_bytes = (uint32_t)a_bytes;
     p.b_bytes = (uint32_t)b_bytes;
-    constexpr int lds = halo_lds_bytes(WO);
-    static_assert(lds <= 163840, "LDS exceeds 160 KB");
     if (PAD && !p.vec_out) return fail(H3V_EINVAL, "%s: the padded output needs 16-byte aligned out and residual", what);
-    // the strided-pixel variant where it applies: int8 dequant, whole-row waves, stages in groups of four
+    // the strided-pixel variant where it applies (int8 dequant or int32, whole-row waves, stages in
+    // groups of four), on column blocks of 128 pixels at Wo 256
     constexpr bool kSp = ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128;
-    const bool sp = kSp && p.C % 128 == 0;
-    auto kernel = sp ? &conv3_halo_i8<WO, EP, ES, PAD, kSp> : &conv3_halo_i8<WO, EP, ES, PAD, false>;
+    constexpr int kTw = kSp ? 128 : WO;
+    constexpr int lds = halo_lds_bytes(WO), lds_sp = halo_lds_bytes(kTw);
+    static_assert(lds <= 163840 && lds_sp <= 163840, "LDS exceeds 160 KB");
+    const bool sp = kSp && p.C % 128 == 0 && p.Ho % (512 / kTw) == 0;   // whole 4-row tiles of the column blocks
+    auto kernel = sp ? &conv3_halo_i8<WO, EP, ES, PAD, kSp, kTw> : &conv3_halo_i8<WO, EP, ES, PAD, false>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, false>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-    static const hipError_t attr_sp = kSp ? hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, kSp>),
-                                                                hipFuncAttributeMaxDynamicSharedMemorySize, lds)
-                                          : hipSuccess;
+    static const hipError_t attr_sp =
+        kSp ? hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, kSp, kTw>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, lds_sp)
+            : hipSuccess;
     const hipError_t ae = attr != hipSuccess ? attr : attr_sp;
-    if (ae != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, lds, hipGetErrorString(ae));
-    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(512), lds, stream, p);
+    if (ae != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %d bytes of LDS: %s", what, sp ? lds_sp : lds,
+                                      hipGetErrorString(ae));
+    hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(512), sp ? lds_sp : lds, stream, p);
     return launch_status(what);
 }
 

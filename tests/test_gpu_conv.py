@@ -112,8 +112,9 @@ def test_conv_h3_stage0_shape_sampled(ops, oracle):
         assert np.array_equal(acc[:, t:t + 1, :32], want), f"frame {t}"
 
 
-# (d, h, w, c): implicit-GEMM tiles, then the window-in-LDS kernel (Wo = 128)
-@pytest.mark.parametrize("d,h,w,c", [(5, 12, 20, 256), (4, 6, 130, 128)])
+# (d, h, w, c): implicit-GEMM tiles (the second one a window-kernel geometry too small for the window kernel:
+# 4 tiles), then the window kernel's strided-pixel form on 128-column blocks of Wo 256 (128 tiles)
+@pytest.mark.parametrize("d,h,w,c", [(5, 12, 20, 256), (4, 6, 130, 128), (6, 34, 258, 128)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_conv_dequant_epilogue(ops, oracle, with_bias, d, h, w, c):
     gen = _gen(5)
@@ -133,8 +134,10 @@ def test_conv_dequant_epilogue(ops, oracle, with_bias, d, h, w, c):
     assert_bitwise(np_(out), want, "conv out")
 
 
-# the residual block's closing add fused into the epilogue: window kernel, implicit GEMM, scalar fallback
-@pytest.mark.parametrize("d,h,w,c,n", [(4, 6, 130, 128, 128), (5, 12, 20, 256, 256), (4, 7, 9, 7, 19)])
+# the residual block's closing add fused into the epilogue: implicit GEMM (a small window geometry and a
+# plain one), scalar fallback, and the window kernel (128 tiles at Wo 256)
+@pytest.mark.parametrize("d,h,w,c,n", [(4, 6, 130, 128, 128), (5, 12, 20, 256, 256), (4, 7, 9, 7, 19),
+                                       (6, 66, 258, 128, 128)])
 def test_conv_residual_epilogue(ops, oracle, d, h, w, c, n):
     print(f"conv residual epilogue D={d} {h}x{w} C={c} N={n}", flush=True)
     gen = _gen(9 + c)
