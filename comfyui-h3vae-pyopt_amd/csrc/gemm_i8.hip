@@ -793,9 +793,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     write_tile<BM, BN, WGM, WGN, RING, EP>(p, acc, smem, m0, n0, tn);
 }
 
-// LDS of conv3_halo_i8<WO>: two stages of window + weights, or the fp16 output tile if larger.
-constexpr int halo_lds_bytes(int wo) {
-    const int hb = ((512 / wo + 2) * ((wo + 2 + 15) / 16 * 16) * 32 + 4095) / 4096 * 4096;
+// Window row pitch in pixels of conv3_halo_i8 for tiles TW pixels wide: TW + 2 rounded up to 16 (the
+// plain swizzle works on 16-pixel groups) or, in the strided-pixel variant, to 8 (whole 256-byte lines).
+constexpr int halo_hpl(int tw, bool sp) { return sp ? (tw + 2 + 7) / 8 * 8 : (tw + 2 + 15) / 16 * 16; }
+
+// LDS of conv3_halo_i8 with TW-pixel tile rows: two stages of window + weights, or the fp16 output
+// tile if larger.
+constexpr int halo_lds_bytes(int tw, bool sp) {
+    const int hb = ((512 / tw + 2) * halo_hpl(tw, sp) * 32 + 4095) / 4096 * 4096;
     const int ring = 2 * (hb + 9 * 128 * 32);
     return ring > 512 * 128 * 2 ? ring : 512 * 128 * 2;
 }
@@ -858,14 +863,15 @@ __device__ __forceinline__ int sp_slot(int px, int h) {
 // kh's first four blocks load into base + 6 .. base + 9 while it runs, as many registers as the
 // plain double buffer.
 //
-// TW < WO (with SP; Wo 256 as column blocks of 128): a tile is RO = 512 / TW output rows of a TW-pixel
-// column block, so its window is RO + 2 rows of TW + 2 pixels (6 x 130 instead of 4 x 258 pixels at
-// Wo 256: 7 window DMA instructions per issuing wave and stage instead of 9).
+// TW < WO (with SP: column blocks of 64 pixels): a tile is RO = 512 / TW output rows of a TW-pixel
+// column block, so its window is RO + 2 rows of TW + 2 pixels (10 x 66 instead of 4 x 258 pixels at
+// Wo 256: 6 window DMA instructions per issuing wave and stage instead of 9).  A wave's 128 pixels
+// are then 128 / TW rows of the block; each group of four (4r .. 4r + 3) stays in one row.
 template <int WO, Epi EP, int ES = 1, bool PAD = false, bool SP = false, int TW = WO>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
-    static_assert(!SP || (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && TW >= 128),
-                  "strided pixels: int8, whole-row waves");
+    static_assert(!SP || (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && (TW % 128 == 0 || 128 % TW == 0)),
+                  "strided pixels: int8, waves of whole tile rows");
     static_assert(TW == WO || (SP && WO % TW == 0), "column blocks: strided-pixel kernel only");
     using Acc = std::conditional_t<ES == 1, v16i, f32x16>;
     constexpr int BM = 512, BN = 128, WGM = 4, WGN = 2, NWD = 4;
@@ -874,7 +880,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int RO = BM / TW;                               // output rows per tile
     constexpr int NCB = WO / TW;                              // column blocks per output row
     constexpr int HR = RO + 2;                                // window rows
-    constexpr int HPL = (TW + 2 + 15) / 16 * 16;              // LDS pixels per window row
+    constexpr int HPL = halo_hpl(TW, SP);                     // LDS pixels per window row
     constexpr int ROWB = HPL * 32;                            // LDS bytes per window row
     constexpr int HB = (HR * ROWB + 4095) / 4096 * 4096;      // window bytes (whole instructions per issuing wave)
     constexpr int WB = 9 * BN * 32;                           // weight bytes of a stage
@@ -883,7 +889,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int LDS = 2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2;
     static_assert(WO == 32 || WO == 64 || WO == 128 || WO == 256, "output width");
     static_assert(LDS <= 163840, "LDS");
-    static_assert(LDS == halo_lds_bytes(TW), "host and kernel LDS sizes");
+    static_assert(LDS == halo_lds_bytes(TW, SP), "host and kernel LDS sizes");
     static_assert(NH + NWT < 64, "outstanding DMA must fit vmcnt");
 
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
@@ -996,12 +1002,13 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int NMFMA = FM * FN;
 
     if constexpr (SP) {
-        static_assert(FM == 4 && WM == 128 && TW % WM == 0, "strided pixels: 4 blocks of 32 rows per wave");
-        const int orow = (wm * WM) / TW, ow0 = (wm * WM) % TW;
+        static_assert(FM == 4 && WM == 128 && TW % 4 == 0, "strided pixels: 4 blocks of 32 rows per wave");
+        const int t0 = wm * WM + 4 * frow;                    // tile pixel of this lane's group of four
+        const int orow = t0 / TW, ow0 = t0 % TW;
         int vaddr[6];   // LDS offset of virtual block V[v] in window row kh = 0
 #pragma unroll
         for (int v = 0; v < 6; ++v) {
-            const int px = ow0 + 4 * frow + v;   // at most TW + 1
+            const int px = ow0 + v;              // at most TW + 1: the group's row, never the next one
             vaddr[v] = orow * ROWB + (px >> 3) * 256 + (sp_slot(px, fhi) << 4);
         }
         v4i av[8], bq[2][FN];
@@ -1359,13 +1366,13 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.a_bytes = (uint32_t)a_bytes;
     p.b_bytes = (uint32_t)b_bytes;
     if (PAD && !p.vec_out) return fail(H3V_EINVAL, "%s: the padded output needs 16-byte aligned out and residual", what);
-    // the strided-pixel variant where it applies (int8 dequant or int32, whole-row waves, stages in
-    // groups of four), on column blocks of 128 pixels at Wo 256
+    // the strided-pixel variant where it applies (int8 dequant or int32, Wo 128 or 256, stages in
+    // groups of four), on column blocks of 64 pixels
     constexpr bool kSp = ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128;
-    constexpr int kTw = kSp ? 128 : WO;
-    constexpr int lds = halo_lds_bytes(WO), lds_sp = halo_lds_bytes(kTw);
+    constexpr int kTw = kSp ? 64 : WO;
+    constexpr int lds = halo_lds_bytes(WO, false), lds_sp = halo_lds_bytes(kTw, true);
     static_assert(lds <= 163840 && lds_sp <= 163840, "LDS exceeds 160 KB");
-    const bool sp = kSp && p.C % 128 == 0 && p.Ho % (512 / kTw) == 0;   // whole 4-row tiles of the column blocks
+    const bool sp = kSp && p.C % 128 == 0 && p.Ho % (512 / kTw) == 0;   // whole 8-row tiles of the column blocks
     auto kernel = sp ? &conv3_halo_i8<WO, EP, ES, PAD, kSp, kTw> : &conv3_halo_i8<WO, EP, ES, PAD, false>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, false>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);

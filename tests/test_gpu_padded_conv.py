@@ -36,7 +36,8 @@ CASES = [(1, 128, 128, 3, 8, 64, 2, (1, 1, 1, 1), "residual"),        # stage-0 
          (1, 256, 256, 3, 4, 128, 2, (0, 1, 0, 1), "residual_bias"),  # stage-1 form: residual + pack bias
          (2, 64, 128, 2, 16, 32, 1, (1, 0, 0, 1), "none"),
          (1, 128, 128, 2, 2, 256, 0, (1, 1, 1, 1), "residual"),       # two rows: rows 0 and 1 both borders
-         (1, 128, 128, 2, 8, 256, 2, (1, 1, 1, 1), "residual"),       # 4-row tiles of 128-column blocks
+         (1, 128, 128, 2, 8, 256, 2, (1, 1, 1, 1), "residual"),       # 8-row tiles of 64-column blocks
+         (1, 256, 256, 2, 8, 128, 2, (0, 1, 0, 1), "residual_bias"),  # the same at the stage-1 form
          (1, 128, 256, 3, 8, 64, 2, (0, 1, 0, 1), "residual_bias"),
          (1, 128, 128, 3, 8, 64, 2, (0, 0, 0, 0), "residual")]
 
