@@ -253,8 +253,8 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int RING = LDS_BYTES;
-    static_assert(!SROWS || ((EP == Epi::Dequant || EP == Epi::Int32) && FM == 4),
-                  "strided rows: int8 epilogues of 128-row wave blocks");
+    static_assert(!SROWS || ((EP == Epi::Dequant || EP == Epi::Int32 || EP == Epi::F16Bias) && FM == 4),
+                  "strided rows: window-conv epilogues of 128-row wave blocks");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
@@ -853,7 +853,8 @@ __device__ __forceinline__ int sp_slot(int px, int h) {
 // ES = 2: fp16 operands, v_mfma_f32_32x32x16_f16, fp32 accumulators (16 channels per slice).  Both
 // MFMAs read 16 bytes per lane in the same row / k-half layout, so staging and fragments are shared.
 //
-// SP (strided pixels; int8 dequant or int32 output, WO >= 128, channels a multiple of 128): row r of a wave's accumulator
+// SP (strided pixels; int8 dequant or int32 output at WO >= 128, fp16 at WO 64; 128-byte channel
+// multiples): row r of a wave's accumulator
 // block i is the wave's output pixel 4r + i.  A wave's 128 pixels lie in one output row, and tap
 // (kh, kw) reads window pixels ow0 + 4r + i + kw: block i of tap kw is "virtual block" V[i + kw] of
 // the six V[v] = pixels ow0 + 4r + v (v = 0..5) of window row kh.  One kh's three taps read six A
@@ -870,8 +871,9 @@ __device__ __forceinline__ int sp_slot(int px, int h) {
 template <int WO, Epi EP, int ES = 1, bool PAD = false, bool SP = false, int TW = WO>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
-    static_assert(!SP || (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && (TW % 128 == 0 || 128 % TW == 0)),
-                  "strided pixels: int8, waves of whole tile rows");
+    static_assert(!SP || (((ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32)) || (ES == 2 && EP == Epi::F16Bias)) &&
+                          (TW % 128 == 0 || 128 % TW == 0)),
+                  "strided pixels: waves of whole tile rows");
     static_assert(TW == WO || (SP && WO % TW == 0), "column blocks: strided-pixel kernel only");
     using Acc = std::conditional_t<ES == 1, v16i, f32x16>;
     constexpr int BM = 512, BN = 128, WGM = 4, WGN = 2, NWD = 4;
@@ -1045,9 +1047,15 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
 #pragma unroll
                     for (int i = 0; i < FM; ++i)
 #pragma unroll
-                        for (int j = 0; j < FN; ++j)
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bq[CUR][j], av[(BASE + KW + i) & 7],
-                                                                              acc[i][j], 0, 0, 0);
+                        for (int j = 0; j < FN; ++j) {
+                            if constexpr (ES == 1)
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bq[CUR][j], av[(BASE + KW + i) & 7],
+                                                                                  acc[i][j], 0, 0, 0);
+                            else
+                                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                    __builtin_bit_cast(half8, bq[CUR][j]), __builtin_bit_cast(half8, av[(BASE + KW + i) & 7]),
+                                    acc[i][j], 0, 0, 0);
+                        }
                 };
                 if constexpr (T9 == 8) {
                     const bool more = s + 1 < nst;
@@ -1366,13 +1374,14 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     p.a_bytes = (uint32_t)a_bytes;
     p.b_bytes = (uint32_t)b_bytes;
     if (PAD && !p.vec_out) return fail(H3V_EINVAL, "%s: the padded output needs 16-byte aligned out and residual", what);
-    // the strided-pixel variant where it applies (int8 dequant or int32, Wo 128 or 256, stages in
-    // groups of four), on column blocks of 64 pixels
-    constexpr bool kSp = ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128;
+    // the strided-pixel variant where it applies (int8 dequant or int32 at Wo 128 or 256, fp16 at Wo 64;
+    // stages in groups of four), on column blocks of 64 pixels
+    constexpr bool kSp = (ES == 1 && (EP == Epi::Dequant || EP == Epi::Int32) && WO >= 128) ||
+                         (ES == 2 && EP == Epi::F16Bias && WO == 64);
     constexpr int kTw = kSp ? 64 : WO;
     constexpr int lds = halo_lds_bytes(WO, false), lds_sp = halo_lds_bytes(kTw, true);
     static_assert(lds <= 163840 && lds_sp <= 163840, "LDS exceeds 160 KB");
-    const bool sp = kSp && p.C % 128 == 0 && p.Ho % (512 / kTw) == 0;   // whole 8-row tiles of the column blocks
+    const bool sp = kSp && (p.C * ES) % 128 == 0 && p.Ho % (512 / kTw) == 0;   // whole 8-row tiles of the column blocks
     auto kernel = sp ? &conv3_halo_i8<WO, EP, ES, PAD, kSp, kTw> : &conv3_halo_i8<WO, EP, ES, PAD, false>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, false>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
