@@ -831,43 +831,42 @@ __device__ __forceinline__ int sp_slot(int px, int h) {
 
 // Stride-1 3x3x3 convolution with the input window of a tile held in LDS.
 //
-// A tile is BM = 512 consecutive output voxels = RO = 512 / WO whole output
-// rows of one frame, times BN = 128 output channels.  For one depth tap kd and
-// one 32-channel slice the nine (kh, kw) taps of every voxel in the tile read
-// the same RO + 2 input rows, so a stage stages that window once ([RO + 2]
-// rows of WO + 2 pixels, 32 bytes each) together with the nine taps' weights
-// ([9][128][32]) and runs 9 MFMA K steps on it; the implicit-GEMM kernel above
-// fetches every input row up to nine times per depth tap instead.  LDS-DMA
-// instructions, whose issue is what holds the matrix pipe back, drop 2.6x.
-// Stages run kd-major (kd0..2) then channel slice, double-buffered: one
+// A tile is BM = 512 output voxels of one frame, RO = 512 / TW output rows of a
+// TW-pixel column block (TW = WO: whole rows), times BN = 128 output channels.
+// For one depth tap kd and one 32-byte channel slice the nine (kh, kw) taps of
+// every voxel in the tile read the same RO + 2 input rows of TW + 2 pixels, so a
+// stage stages that window once (32 bytes per pixel) together with the nine
+// taps' weights ([9][128][32]) and runs 9 MFMA K steps on it; the implicit-GEMM
+// kernel above fetches every input row up to nine times per depth tap instead.
+// LDS-DMA instructions, whose issue is what holds the matrix pipe back, drop
+// 2.6x.  Stages run kd-major (kd0..2) then channel slice, double-buffered: one
 // barrier per 9 taps.  Causal-zero depth taps (output frames 0 and 1 of the
 // fused producer's input) are skipped per tile; the tile is one frame.
 //
 // Window layout: pixel (row hr, column px) at LDS pixel hr * HPL + px with
-// HPL = WO + 2 rounded up to 16, so a (kh, kw) shift of the window is a
-// uniform offset for kh and a per-lane one for kw; each pixel's two 16-byte
-// halves are swapped when (px >> 3) & 1, which keeps the 16-lane fragment
-// reads (16 consecutive pixels, one half) on 16 distinct 16-byte bank groups.
-// Weight rows (tap, n) are swizzled the same way by (n >> 3) & 1.
+// HPL = TW + 2 rounded up (halo_hpl), so a (kh, kw) shift of the window is a
+// uniform offset for kh and a per-lane one for kw.  Plain kernel: each pixel's
+// two 16-byte halves are swapped when (px >> 3) & 1, which keeps the 16-lane
+// fragment reads (16 consecutive pixels, one half) on 16 distinct 16-byte bank
+// groups.  Weight rows (tap, n) are swizzled the same way by (n >> 3) & 1.
 // ES = 1: int8 operands, v_mfma_i32_32x32x32_i8, int32 accumulators (32 channels per 32-byte slice);
 // ES = 2: fp16 operands, v_mfma_f32_32x32x16_f16, fp32 accumulators (16 channels per slice).  Both
 // MFMAs read 16 bytes per lane in the same row / k-half layout, so staging and fragments are shared.
 //
-// SP (strided pixels; int8 dequant or int32 output at WO >= 128, fp16 at WO 64; 128-byte channel
-// multiples): row r of a wave's accumulator
-// block i is the wave's output pixel 4r + i.  A wave's 128 pixels lie in one output row, and tap
-// (kh, kw) reads window pixels ow0 + 4r + i + kw: block i of tap kw is "virtual block" V[i + kw] of
-// the six V[v] = pixels ow0 + 4r + v (v = 0..5) of window row kh.  One kh's three taps read six A
+// SP (strided pixels; int8 dequant or int32 output at WO >= 128, fp16 at WO 64; channel bytes a
+// multiple of 128): row r of a wave's accumulator block i is the wave's tile pixel 4r + i, and each
+// group of four (4r .. 4r + 3) lies in one output row.  Tap (kh, kw) reads window pixels
+// px0 + i + kw (px0 the group's first column): block i of tap kw is "virtual block" V[i + kw] of
+// the six V[v] = pixels px0 + v (v = 0..5) of window row kh.  One kh's three taps read six A
 // fragments instead of twelve (4 fragment reads per 8 MFMAs instead of 6); the window lines are
 // swizzled by sp_slot for the stride-4 reads.  The blocks rotate through eight register slots, V[v]
 // of the g-th kh in slot (6g + v) % 8: a kh's last tap reads slots base + 2 .. base + 5, so the next
 // kh's first four blocks load into base + 6 .. base + 9 while it runs, as many registers as the
 // plain double buffer.
 //
-// TW < WO (with SP: column blocks of 64 pixels): a tile is RO = 512 / TW output rows of a TW-pixel
-// column block, so its window is RO + 2 rows of TW + 2 pixels (10 x 66 instead of 4 x 258 pixels at
-// Wo 256: 6 window DMA instructions per issuing wave and stage instead of 9).  A wave's 128 pixels
-// are then 128 / TW rows of the block; each group of four (4r .. 4r + 3) stays in one row.
+// TW < WO (with SP: column blocks of 64 pixels): the window of a tile is RO + 2 = 10 rows of 66
+// pixels instead of 4 rows of 258 at Wo 256: 6 window DMA instructions per issuing wave and stage
+// instead of 9.  A wave's 128 pixels are two rows of the block.
 template <int WO, Epi EP, int ES = 1, bool PAD = false, bool SP = false, int TW = WO>
 __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     static_assert((ES == 2) == (EP == Epi::F16Bias), "fp16 operands use the F16Bias epilogue");
