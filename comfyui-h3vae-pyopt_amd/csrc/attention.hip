@@ -27,10 +27,12 @@
 //                 in fp16: one v_permlane32_swap per dword pair turns the S
 //                 layout into the MFMA's 8 consecutive keys per lane.
 //
-// LDS: K [64 keys][64 dims] and V^T [64 dims][64 keys] fp16, 128-byte rows
-// whose 16-byte chunks are XOR-swizzled by (row >> 1) & 7, so the 16-lane
-// fragment reads hit 16 distinct 4-bank groups.  The next block's K and V
-// are loaded into registers while the current one is computed.
+// LDS: three slots of K [64 keys][64 dims] and V^T [64 dims][64 keys] fp16,
+// 128-byte rows whose 16-byte chunks are XOR-swizzled by (row >> 1) & 7, so the
+// 16-lane fragment reads hit 16 distinct 4-bank groups.  K and V of block j + 2
+// are loaded into registers while block j is computed and stored into their
+// slot after the next barrier; waves 4-7 run one phase behind waves 0-3 (see
+// the main loop).
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
@@ -48,6 +50,7 @@ constexpr int kBK = 64;       // keys per block
 constexpr int kQuerySets = 2;
 constexpr int kThreads = 256;   // the K / V loading threads (waves 0-3); a workgroup has 8 waves
 constexpr float kLazy = 8.0f;   // log2 margin of the lazy softmax maximum (weights stay <= 2^kLazy)
+constexpr int kSlots = 3;       // K / V^T blocks resident in LDS (block j in slot j % 3)
 
 struct AttnParams {
     const uint16_t* q;
@@ -74,8 +77,9 @@ __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
 template <int QS>
 __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
     constexpr int BQ = 256 * QS;
-    __shared__ __attribute__((aligned(16))) uint16_t ks[kBK * kD];   // [key][dim]
-    __shared__ __attribute__((aligned(16))) uint16_t vt[kD * kBK];   // [dim][key]
+    constexpr int KV = kBK * kD;                                      // elements of one K or V^T block
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kSlots * KV];   // [slot][key][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kSlots * KV];   // [slot][dim][key]
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -145,12 +149,14 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
             vreg[i][1] = w.y;
         }
     };
-    auto store_block = [&]() {
+    auto store_block = [&](int slot) {
+        uint16_t* const kd = ks + slot * KV;
+        uint16_t* const vd = vt + slot * KV;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int c = tid + kThreads * i;
             const int key = c >> 3, dch = c & 7;
-            *reinterpret_cast<u32x4*>(ks + key * kD + 8 * swz(key, dch)) = kreg[i];
+            *reinterpret_cast<u32x4*>(kd + key * kD + 8 * swz(key, dch)) = kreg[i];
         }
         // dim j of the 4: keys 0-1 from the low (j even) or high (j odd) halves of vreg[0..1][j >> 1],
         // keys 2-3 likewise from vreg[2..3]; v_perm_b32 picks the two halves into one dword
@@ -160,7 +166,7 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
             const uint32_t lo = __builtin_amdgcn_perm(vreg[1][j >> 1], vreg[0][j >> 1], sel);
             const uint32_t hi = __builtin_amdgcn_perm(vreg[3][j >> 1], vreg[2][j >> 1], sel);
             const int d = 4 * vdg + j;
-            *reinterpret_cast<uint2*>(vt + d * kBK + 8 * swz(d, vkg >> 1) + 4 * (vkg & 1)) = make_uint2(lo, hi);
+            *reinterpret_cast<uint2*>(vd + d * kBK + 8 * swz(d, vkg >> 1) + 4 * (vkg & 1)) = make_uint2(lo, hi);
         }
     };
 
@@ -178,22 +184,12 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
 
     const int nblk = (n + kBK - 1) / kBK;
     const bool loader = tid < kThreads;                   // waves 0-3 (wave-uniform)
-    // The Q fragment loads complete here, once: otherwise the wait counters merged over the loop's back
-    // edge keep them pending, and the first score MFMAs of every block wait for that block's K / V loads.
-    __builtin_amdgcn_s_waitcnt(0);
-    if (loader) load_block(0);
-    for (int j = 0; j < nblk; ++j) {
-        const int kb0 = j * kBK;
-        __syncthreads();                                  // every wave is done with the previous block
-        if (loader) store_block();
-        __syncthreads();
-        if (loader && j + 1 < nblk) load_block(kb0 + kBK);   // next block in flight during this one
-        // a wave whose 32 queries all lie past the end (the last workgroup of a head) only helps
-        // with the shared K / V loads and barriers
-        if (!wave_active) continue;
 
-        // S = K . Q^T for the 64 keys of the block (two 32-key halves), each K fragment used by every set
-        f32x16 s[QS][2];
+    // S = K . Q^T for the 64 keys of block j (two 32-key halves), each K fragment used by every set;
+    // keys past the end (last block only) are -inf
+    auto scores = [&](int j, int slot, f32x16 (&s)[QS][2]) {
+        const int kb0 = j * kBK;
+        const uint16_t* const kb = ks + slot * KV;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
 #pragma unroll
@@ -201,13 +197,12 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
             const int row = 32 * kh + (lane & 31);
 #pragma unroll
             for (int kc = 0; kc < 4; ++kc) {
-                const half8 a = *reinterpret_cast<const half8*>(ks + row * kD + 8 * swz(row, 2 * kc + hi));
+                const half8 a = *reinterpret_cast<const half8*>(kb + row * kD + 8 * swz(row, 2 * kc + hi));
 #pragma unroll
                 for (int qs = 0; qs < QS; ++qs)
                     s[qs][kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qf[qs][kc], s[qs][kh], 0, 0, 0);
             }
         }
-        // keys past the end (last block only): -inf
         if (kb0 + kBK > n) {
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs)
@@ -219,12 +214,14 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                         if (key >= n) s[qs][kh][r] = -__builtin_inff();
                     }
         }
-        // online softmax per set in raw-score units (the exponent folds in scale * log2 e), with a lazy
-        // reference maximum: the weights are exp2(s * c - m_ref * c), and m_ref moves (rescaling O and l by
-        // exp2((m_old - m_ref) * c)) only when a score of the block exceeds it by more than kLazy / c, i.e.
-        // when a weight would exceed 2^kLazy.  Every weight stays in [0, 256], where fp16 keeps the same
-        // relative precision, and after the first block the 64 rescale multiplies almost never run (with
-        // the exact running maximum some lane's maximum moves in nearly every block).  P in fp16.
+    };
+    // online softmax per set in raw-score units (the exponent folds in scale * log2 e), with a lazy
+    // reference maximum: the weights are exp2(s * c - m_ref * c), and m_ref moves (rescaling O and l by
+    // exp2((m_old - m_ref) * c)) only when a score of the block exceeds it by more than kLazy / c, i.e.
+    // when a weight would exceed 2^kLazy.  Every weight stays in [0, 256], where fp16 keeps the same
+    // relative precision, and after the first block the 64 rescale multiplies almost never run (with
+    // the exact running maximum some lane's maximum moves in nearly every block).  P in fp16.
+    auto softmax = [&](const f32x16 (&s)[QS][2], uint32_t (&pk)[QS][2][8]) {
         bool up = false;
         float mblk[QS];
 #pragma unroll
@@ -251,7 +248,6 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                     for (int r = 0; r < 16; ++r) oacc[qs][db][r] *= alpha;
             }
         }
-        uint32_t pk[QS][2][8];                            // [set][half][g * 2 + dword]
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) {
             float lsum = 0.0f;
@@ -272,11 +268,13 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                 }
             l_run[qs] += lsum;
         }
-
-        // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set.  The wave's issue
-        // priority is raised for them, so that a wave with P.V MFMAs ready issues ahead of its SIMD partner's
-        // softmax VALU work (H3 call 153.7 -> 151.5 us, cfg4 1222 -> 1200 us; around the score MFMAs as well,
-        // or at priority 2 or 3, no further change).
+    };
+    // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set.  The wave's issue
+    // priority is raised for them, so that a wave with P.V MFMAs ready issues ahead of its SIMD partner's
+    // softmax VALU work (H3 call 153.7 -> 151.5 us, cfg4 1222 -> 1200 us; around the score MFMAs as well,
+    // or at priority 2 or 3, no further change).
+    auto pv = [&](int slot, const uint32_t (&pk)[QS][2][8]) {
+        const uint16_t* const vb = vt + slot * KV;
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -295,13 +293,63 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
 #pragma unroll
             for (int db = 0; db < 2; ++db) {
                 const int row = 32 * db + (lane & 31);
-                const half8 a = *reinterpret_cast<const half8*>(vt + row * kBK + 8 * swz(row, 2 * c + hi));
+                const half8 a = *reinterpret_cast<const half8*>(vb + row * kBK + 8 * swz(row, 2 * c + hi));
 #pragma unroll
                 for (int qs = 0; qs < QS; ++qs)
                     oacc[qs][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop[qs], oacc[qs][db], 0, 0, 0);
             }
         }
         __builtin_amdgcn_s_setprio(0);
+    };
+
+    // One barrier per block, three LDS slots.  Waves 0-3 (the loaders) run block j as scores, softmax,
+    // P.V after barrier j; waves 4-7 run the P.V of block j - 1 and then the scores and softmax of block
+    // j, carrying the packed weights P over the barrier.  On each SIMD one wave's softmax VALU work then
+    // runs beside its partner's MFMAs for two of the three phases instead of both waves running the
+    // same phase; every query sees the same operations in the same order.  After barrier j the loaders
+    // store block j + 1 into slot (j + 1) % 3, which last held block j - 2: its readers finished before
+    // barrier j (waves 4-7 read it in their iteration j - 1); block j + 1 is read only after barrier
+    // j + 1.  The two groups run separate loops with one barrier per iteration each.
+    // The Q fragment loads complete here, once: otherwise the wait counters merged over the loop's back
+    // edge keep them pending, and the first score MFMAs of every block wait for that block's K / V loads.
+    __builtin_amdgcn_s_waitcnt(0);
+    uint32_t pk[QS][2][8];                                // [set][half][g * 2 + dword]
+    if (loader) {
+        load_block(0);
+        store_block(0);
+        if (nblk > 1) load_block(kBK);
+        int slot = 0;                                     // slot of block j
+        for (int j = 0; j < nblk; ++j) {
+            __syncthreads();                              // block j stored; blocks before j - 1 no longer read
+            const int nslot = slot == kSlots - 1 ? 0 : slot + 1;
+            if (j + 1 < nblk) {
+                store_block(nslot);
+                if (j + 2 < nblk) load_block((j + 2) * kBK);   // block j + 2 in flight during this one
+            }
+            // a wave whose 32 queries all lie past the end (the last workgroup of a head) only helps
+            // with the shared K / V loads and barriers
+            if (wave_active) {
+                f32x16 s[QS][2];
+                scores(j, slot, s);
+                softmax(s, pk);
+                pv(slot, pk);
+            }
+            slot = nslot;
+        }
+    } else {
+        int slot = 0, pslot = 0;                          // slots of blocks j and j - 1
+        for (int j = 0; j < nblk; ++j) {
+            __syncthreads();
+            if (wave_active) {
+                if (j > 0) pv(pslot, pk);
+                f32x16 s[QS][2];
+                scores(j, slot, s);
+                softmax(s, pk);
+            }
+            pslot = slot;
+            slot = slot == kSlots - 1 ? 0 : slot + 1;
+        }
+        if (wave_active) pv(pslot, pk);                   // the last block (no store follows it)
     }
 
     // normalise and store: lane l holds query q0 + 32 qs + l % 32, dims 32 db + 8 g + 4 hi + e
