@@ -269,13 +269,11 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
             l_run[qs] += lsum;
         }
     };
-    // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set.  The wave's issue
-    // priority is raised for them, so that a wave with P.V MFMAs ready issues ahead of its SIMD partner's
-    // softmax VALU work (H3 call 153.7 -> 151.5 us, cfg4 1222 -> 1200 us; around the score MFMAs as well,
-    // or at priority 2 or 3, no further change).
+    // O^T += V^T . P^T over four 16-key chunks, each V^T fragment used by every set.  (With both wave
+    // groups in one phase a raised issue priority for these MFMAs had paid, 153.7 -> 151.5 us on the H3
+    // call; with the groups a phase apart it costs: 146.8 us without it against 149.5 us.)
     auto pv = [&](int slot, const uint32_t (&pk)[QS][2][8]) {
         const uint16_t* const vb = vt + slot * KV;
-        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int kh = c >> 1, g0 = 2 * (c & 1);
@@ -299,7 +297,6 @@ __global__ __launch_bounds__(2 * kThreads) void fmha_d64(AttnParams p) {
                     oacc[qs][db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bop[qs], oacc[qs][db], 0, 0, 0);
             }
         }
-        __builtin_amdgcn_s_setprio(0);
     };
 
     // One barrier per block, three LDS slots.  Waves 0-3 (the loaders) run block j as scores, softmax,
