@@ -747,7 +747,8 @@ def main():
                                    "source": "reference README.md:43,53-54"},
         "outputs_finite": finite,
         "roofline": {
-            "kernel": "conv3_halo_i8<256,Dequant> (stage-0 conv C128->128, [1,128,19,258,258] int8, no residual)",
+            "kernel": "conv3_halo_i8<256,Dequant,SP,64> (stage-0 conv C128->128, strided pixels on 64-pixel column blocks, "
+                      "[1,128,19,258,258] int8, no residual)",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": INT8_PEAK_TOPS,
