@@ -62,7 +62,8 @@ def parse():
     p.add_argument("--configs-only", action="store_true",
                    help="run only the per-config kernel timings and print them as JSON (for rocprofv3 kernel traces)")
     p.add_argument("--traffic-sample", action="store_true",
-                   help="run only a 1 GiB elementwise copy and three stage-0 fused layers (for rocprofv3 --pmc)")
+                   help="run only a 1 GiB elementwise copy and the step's and configs' INT8 convs and GEMMs, "
+                        "3 launches each (for rocprofv3 --pmc)")
     p.add_argument("--frames", type=int, default=124, help=argparse.SUPPRESS)
     p.add_argument("--depth", type=int, default=DEC_BLOCKS, help=argparse.SUPPRESS)
     return p.parse_args()
@@ -158,9 +159,10 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
         bias = randn(128, scale=0.1)
         qx = torch.empty(xn.numel(), device=dev, dtype=i8)
         xs = torch.empty(1, device=dev, dtype=f32)
-        amax = torch.empty(int(hip.lib().h3v_tensor_quant_scratch_words()), device=dev, dtype=torch.int32)
+        words = int(hip.lib().h3v_tensor_quant_scratch_words())
+        amax = torch.empty(words, device=dev, dtype=torch.int32)
         y = torch.empty((9, 64, 64, 128), device=dev, dtype=f16)
-        t_q = timed(lambda: call("h3v_tensor_quant_i8", p(xn), xn.numel(), p(qx), p(xs), p(amax), stream))
+        t_q = timed(lambda: call("h3v_tensor_quant_i8", p(xn), xn.numel(), p(qx), p(xs), p(amax), words, stream))
         t_c = timed(lambda: call("h3v_conv3d_i8", p(qx), p(xs), p(qw), p(ws), p(bias), p(y), 1, 128, 11, 66, 66, 128,
                                  3, 3, 3, 1, 1, 1, 1, stream))
         useful = 2 * 36864 * 128 * 3456 * 8 // 9
@@ -535,6 +537,20 @@ def cpu_baseline(budget_s: float):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "stage0_conv_traffic_pmc.md"
+GEMM_TRAFFIC_PROFILE = ROOT / "profiles" / "int8_gemm_k2048_traffic_pmc.md"
+GEMM_K2048_KERNEL = ("gemm_i8_mfma<256,256,128,2,4,2,2,Gemm,Dequant> (decoder INT8 GEMMs with K = 2048: QKV, "
+                     "attention-out, FFN-up; 256x256 tiles, two-slot LDS ring)")
+
+
+def _profile_number(path, key):
+    """The integer after `key:` in a committed profile summary, or None."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith(key + ":"):
+                return int(line.split(":", 1)[1].strip())
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def stage0_conv_traffic():
@@ -543,13 +559,13 @@ def stage0_conv_traffic():
     The summary holds one line `traffic_bytes_per_launch: N`, derived from two rocprofv3 --pmc runs of
     `bench.py --traffic-sample`, each scaled by the counter's reading for a copy of known size.
     """
-    try:
-        for line in TRAFFIC_PROFILE.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1].strip())
-    except OSError:
-        pass
-    return None
+    return _profile_number(TRAFFIC_PROFILE, "traffic_bytes_per_launch")
+
+
+def gemm_k2048_traffic():
+    """HBM bytes per launch of the K = 2048 GEMM family (mean over the QKV, attention-out and FFN-up launches of
+    a decoder block), from the committed FETCH_SIZE/WRITE_SIZE summary of `bench.py --traffic-sample`."""
+    return _profile_number(GEMM_TRAFFIC_PROFILE, "traffic_bytes_per_launch")
 
 
 def build_runtime(torch, pkg, args):
@@ -567,19 +583,72 @@ def build_runtime(torch, pkg, args):
     return runtime
 
 
+PMC_SAMPLE_ORDER = [
+    # (label, entry point, shape) in dispatch order; each runs 3 times (the first one warms L2 and the clock)
+    ("copy_1GiB", "torch.neg fp16 [2^29]", None),
+    ("stage0_conv", "h3v_conv3d_i8", "[1,128,19,258,258] -> 128, causal, after the fused producer"),
+    ("stage1_conv_c256", "h3v_conv3d_i8", "[1,256,19,130,130] -> 256, causal"),
+    ("stage1_conv_c128_256", "h3v_conv3d_i8", "[1,128,19,130,130] -> 256, causal"),
+    ("h3_qkv", "h3v_gemm_i8_dequant", "7188 x 6144 x 2048"),
+    ("h3_attn_out", "h3v_gemm_i8_dequant", "7188 x 2048 x 2048"),
+    ("h3_ffn_up", "h3v_gemm_i8_dequant", "7188 x 16384 x 2048"),
+    ("h3_ffn_down", "h3v_gemm_i8_dequant", "7188 x 2048 x 8192"),
+    ("cfg2_qkv", "h3v_gemm_i8_dequant", "16384 x 3072 x 1024"),
+    ("cfg3_up", "h3v_gemm_i8_dequant", "16384 x 8192 x 1024"),
+    ("cfg3_down", "h3v_gemm_i8_dequant", "16384 x 1024 x 4096"),
+    ("cfg4_out", "h3v_gemm_i8_dequant", "16384 x 1024 x 1024"),
+    ("cfg1_conv", "h3v_conv3d_i8", "[1,128,11,66,66] -> 128, causal"),
+]
+
+
 def traffic_sample(torch, pkg):
-    """Counter calibration + the dominant kernel in pipeline context for rocprofv3 --pmc: a 1 GiB
-    elementwise copy (FETCH_SIZE / WRITE_SIZE scale), then three stage-0 fused layers (producer + conv)."""
+    """The INT8 matrix kernels of the step and of configs 1-4, each launched 3 times in PMC_SAMPLE_ORDER, for
+    rocprofv3 --pmc passes (HBM bytes, MFMA busy cycles): a 1 GiB elementwise copy first (FETCH_SIZE / WRITE_SIZE
+    scale), then the stage-0 fused layer (producer + conv) and the other convs and GEMMs on their step shapes with
+    the step's data distributions (row-quantized N(0, 1) activations, N(0, 0.02) weights; fused-producer int8
+    activations and kaiming-like weights for the convs)."""
     import importlib
     integ = importlib.import_module(f"{pkg.__name__}.opt.encoder_int8_integration")
     enc = importlib.import_module(f"{pkg.__name__}.opt.encoder_int8")
+    kitchen = importlib.import_module(f"{pkg.__name__}.opt.kitchen_int8")
+    hip = importlib.import_module(f"{pkg.__name__}._hip")
     dev = torch.device("cuda:0")
+    stream = hip.stream(dev)
+    call, p = hip.call, hip.ptr
     g = torch.Generator(device=dev).manual_seed(20261002)
+
+    def randn(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * scale).half()
+
+    def conv(cin, cout, d, h, w):
+        x = randn(1, cin, d, h, w).contiguous(memory_format=torch.channels_last_3d)
+        qx, xs = enc.quantize_activation_tensor(F.pad(x, (1, 1, 1, 1, 2, 0)))
+        qw, ws, _ = enc.prepare_int8_weight(randn(cout, cin, 3, 3, 3, scale=(27 * cin) ** -0.5))
+        bias = randn(cout, scale=0.1)
+        y = torch.empty((d, h, w, cout), device=dev, dtype=torch.float16)
+        for _ in range(3):
+            call("h3v_conv3d_i8", p(qx), p(xs), p(qw), p(ws), p(bias), p(y), 1, cin, d + 2, h + 2, w + 2, cout,
+                 3, 3, 3, 1, 1, 1, 1, stream)
+
+    def gemm(m, n, k):
+        xa = randn(m, k)
+        qa = torch.empty((m, k), device=dev, dtype=torch.int8)
+        sa = torch.empty(m, device=dev, dtype=torch.float32)
+        call("h3v_row_quant", p(xa), m, k, p(qa), p(sa), stream)
+        wb, wbs = kitchen.quantize_int8_rowwise(randn(n, k, scale=0.02))
+        wbs = wbs.reshape(-1).contiguous()
+        bb = randn(n, scale=0.02)
+        yb = torch.empty((m, n), device=dev, dtype=torch.float16)
+        for _ in range(3):
+            call("h3v_gemm_i8_dequant", p(qa), p(sa), p(wb), p(wbs), p(bb), p(yb), m, n, k, stream)
+
+    import torch.nn.functional as F
     with torch.inference_mode():
         src = torch.ones(1 << 29, device=dev, dtype=torch.float16)
         dst = torch.empty_like(src)
         for _ in range(3):
             torch.neg(src, out=dst)
+        del src, dst
         x = torch.randn((1, 128, 17, 256, 256), generator=g, device=dev).half().contiguous(
             memory_format=torch.channels_last_3d)
         gamma, beta = torch.ones(128, device=dev, dtype=torch.float16), torch.zeros(128, device=dev, dtype=torch.float16)
@@ -587,8 +656,17 @@ def traffic_sample(torch, pkg):
         bias = torch.zeros(128, device=dev, dtype=torch.float16)
         for _ in range(3):
             integ.int8_norm_conv3d(x, gamma, beta, None, 1e-6, qw, ws, bias)
+        del x
+        conv(256, 256, 17, 128, 128)
+        conv(128, 256, 17, 128, 128)
+        for m, n, k in [(DEC_M, 3 * DEC_D, DEC_D), (DEC_M, DEC_D, DEC_D), (DEC_M, 16384, DEC_D), (DEC_M, DEC_D, 8192),
+                        (16384, 3072, 1024), (16384, 8192, 1024), (16384, 1024, 4096), (16384, 1024, 1024)]:
+            gemm(m, n, k)
+        conv(128, 128, 9, 64, 64)
         torch.cuda.synchronize()
-    print("[bench] traffic sample done: 3 x neg(1 GiB fp16), 3 x stage-0 producer + conv", file=sys.stderr)
+    print("[bench] traffic / PMC sample done: " + "; ".join(f"{label}: {entry} {shape or ''}".strip()
+                                                              for label, entry, shape in PMC_SAMPLE_ORDER),
+          file=sys.stderr)
 
 
 def mfma_ceiling(torch, hip, runtime, clip):
@@ -665,10 +743,14 @@ def main():
         traffic_sample(torch, pkg)
         return
 
-    # stage-0 conv (C128 -> 128 on the padded [19, 258, 258] int8 input, no residual) and the FFN-up GEMM
+    # the decoder's INT8 GEMMs (h3v_gemm_i8_dequant args: ..., m, n, k, stream) and the stage-0 conv (C128 -> 128
+    # on the padded [19, 258, 258] int8 input, no residual)
     timer = LaunchTimer(torch, hip, {
+        "qkv": ("h3v_gemm_i8_dequant", lambda a: a[7] == 3 * DEC_D and a[8] == DEC_D),
+        "attn_out": ("h3v_gemm_i8_dequant", lambda a: a[7] == DEC_D and a[8] == DEC_D),
+        "ffn_up": ("h3v_gemm_i8_dequant", lambda a: a[7] == 16384 and a[8] == DEC_D),
+        "ffn_down": ("h3v_gemm_i8_dequant", lambda a: a[7] == DEC_D and a[8] == 8192),
         "stage0_conv": ("h3v_conv3d_i8", lambda a: a[7] == 128 and a[11] == 128 and a[9] == 258 and a[8] == 19),
-        "ffn_up_gemm": ("h3v_gemm_i8_dequant", lambda a: a[7] == 16384 and a[8] == 2048),
     })
     log("building the reconstructed H3 VAE (random init) and the runtime")
     runtime = build_runtime(torch, pkg, args)
@@ -714,10 +796,22 @@ def main():
     dec_calls = 7 * 28 // 4 if args.frames == 124 else None
     useful, _ = enc_ops_per_call()
     conv_us, conv_n = timer.mean_us("stage0_conv")
-    up_us, up_n = timer.mean_us("ffn_up_gemm")
     conv_ops = stage0_conv_useful_ops()
-    up_ops = 2 * DEC_M * 16384 * DEC_D
     achieved = conv_ops / conv_us / 1e6
+    # the dominant kernel by step time: the K = 2048 GEMM instantiation behind QKV, attention-out and FFN-up
+    gemm_n = {"qkv": 3 * DEC_D, "attn_out": DEC_D, "ffn_up": 16384, "ffn_down": DEC_D}
+    gemm_k = {"qkv": DEC_D, "attn_out": DEC_D, "ffn_up": DEC_D, "ffn_down": 8192}
+    per_gemm = {}
+    for key in gemm_n:
+        us, n = timer.mean_us(key)
+        ops = 2 * DEC_M * gemm_n[key] * gemm_k[key]
+        per_gemm[key] = {"avg_us": round(us, 2), "launches_timed": n, "ops_per_launch": ops,
+                         "tops": round(ops / us / 1e6, 1), "frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)}
+    fam = ("qkv", "attn_out", "ffn_up")
+    fam_n = sum(per_gemm[k]["launches_timed"] for k in fam)
+    fam_us = sum(per_gemm[k]["avg_us"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
+    fam_ops = sum(per_gemm[k]["ops_per_launch"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
+    gemm_achieved = fam_ops / fam_us / 1e6
     ref_s = REF_ENCODE_S + REF_DECODE_S
     result = {
         "metric": "H3 VAE encode/decode s @768x1344x124 tile256; INT8 MFMA % of peak",
@@ -747,6 +841,21 @@ def main():
                                    "source": "reference README.md:43,53-54"},
         "outputs_finite": finite,
         "roofline": {
+            "kernel": GEMM_K2048_KERNEL,
+            "bound": "mfma",
+            "achieved": round(gemm_achieved, 1),
+            "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_achieved / INT8_PEAK_TOPS, 4),
+            "traffic": gemm_k2048_traffic(),
+            "launches_timed": fam_n,
+            "avg_us": round(fam_us, 2),
+            "algorithmic_ops_per_launch": round(fam_ops),
+            "launch_mix": "per decoder block: QKV 7188x6144x2048, attention-out 7188x2048x2048, FFN-up "
+                          "7188x16384x2048 (one of each); achieved = mean ops per launch / mean launch time",
+            "per_gemm": per_gemm,
+        },
+        "roofline_stage0_conv": {
             "kernel": "conv3_halo_i8<256,Dequant,SP,64> (stage-0 conv C128->128, strided pixels on 64-pixel column blocks, "
                       "[1,128,19,258,258] int8, no residual)",
             "bound": "mfma",
@@ -759,22 +868,12 @@ def main():
             "avg_us": round(conv_us, 1),
             "algorithmic_ops_per_launch": conv_ops,
         },
-        "roofline_ffn_up": {
-            "kernel": "gemm_i8_mfma<...,Dequant> FFN-up [7188 x 2048] x [16384 x 2048]^T",
-            "bound": "mfma",
-            "achieved": round(up_ops / up_us / 1e6, 1),
-            "peak": INT8_PEAK_TOPS,
-            "unit": "TFLOP/s",
-            "frac": round(up_ops / up_us / 1e6 / INT8_PEAK_TOPS, 4),
-            "launches_timed": up_n,
-            "avg_us": round(up_us, 1),
-            "algorithmic_ops_per_launch": up_ops,
-        },
     }
     log("measuring the MFMA ceiling for the stage-0 conv operands")
     with torch.inference_mode():
         ceiling = mfma_ceiling(torch, hip, runtime, clip)
     ceiling["conv_frac_of_ceiling"] = round(achieved / ceiling["tops"], 4)
+    ceiling["gemm_k2048_frac_of_ceiling"] = round(gemm_achieved / ceiling["tops"], 4)
     result["mfma_ceiling"] = ceiling
     del runtime, clip, out
     torch.cuda.empty_cache()

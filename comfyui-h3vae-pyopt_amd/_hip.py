@@ -39,7 +39,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_conv3d_i8_residual_padded": [_P] * 8 + [_I] * 12 + [_P],
     "h3v_conv3d_i8": [_P, _P, _P, _P, _P, _P] + [_I] * 13 + [_P],
     "h3v_conv3d_i8_i32": [_P, _P, _P] + [_I] * 13 + [_P],
-    "h3v_tensor_quant_i8": [_P, _I64, _P, _P, _P, _P],
+    "h3v_tensor_quant_i8": [_P, _I64, _P, _P, _P, _I64, _P],
     "h3v_gn_norm_pack_i8": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "h3v_gn_norm_pack_i8_noalloc": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P],
     "h3v_residual_norm1_quant": [_P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P, _P],

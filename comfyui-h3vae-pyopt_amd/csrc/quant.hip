@@ -320,10 +320,13 @@ int h3v_selftest_fast_div(uint32_t* counts, hipStream_t stream) {
 int64_t h3v_tensor_quant_scratch_words(void) { return kTensorPartials; }
 
 int h3v_tensor_quant_i8(const uint16_t* x, int64_t n, int8_t* q, float* scale, uint32_t* scratch,
-                        hipStream_t stream) {
+                        int64_t scratch_words, hipStream_t stream) {
     const char* what = "h3v_tensor_quant_i8";
     H3V_REQUIRE(x && q && scale && scratch, "%s: null pointer argument", what);
     H3V_REQUIRE(n > 0, "%s: activation quantization requires a nonempty tensor", what);
+    H3V_REQUIRE(scratch_words >= kTensorPartials,
+                "%s: scratch holds %lld words; h3v_tensor_quant_scratch_words() = %d are required", what,
+                (long long)scratch_words, kTensorPartials);
     const bool vec = aligned(x, 16) && aligned(q, 8);
     const int64_t nvec = vec ? n / 8 : n / 8 + 1;
     // pass 1: at least 8 vectors per lane; pass 2: at least 4 (it also writes)

@@ -365,23 +365,28 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         downsample) with INT8 convolutions under int8_encode; the clip-batched native suffix."""
         from .opt.encoder_fused_batched_norm import fused_suffix
         from .opt.encoder_fused_norm_next import next_fused_prefix
-        from .opt.encoder_internal_padding import replace_selected
+        from .opt.encoder_internal_padding import replace_selected, restore_selected
         from .opt.encoder_staged_batch import encode_staged
         self._encode_staged = encode_staged
         encoder = core.encoder.to(memory_format=torch.channels_last_3d)
         quant = core.quant_conv.to(memory_format=torch.channels_last_3d)
-        replace_selected(encoder, ["down.0.downsample.conv", "conv_in"])
-        prefix = next_fused_prefix(encoder, "extend_bias_pack")
-        suffix = fused_suffix(encoder, quant, all_stages=True)
-        self.int8_encoder_metadata = None
-        if self.int8_encode:
-            from .opt.encoder_int8_integration import install_int8_encoder_prefix
-            try:
-                self.int8_encoder_metadata = install_int8_encoder_prefix(prefix, require_cuda=True,
-                                                                         tile_variant="auto")
-            except Exception as exc:  # noqa: BLE001 - an explicit option has no fallback
-                raise RuntimeError("int8_encode installation failed; no fallback was applied") from exc
-            logger.info("[H3VAE-PyOpt] INT8 encoder convolutions: %d", self.int8_encoder_metadata["count"])
+        # checked as a whole before anything is swapped; a later failure puts the model's convs back
+        swaps = replace_selected(encoder, ["down.0.downsample.conv", "conv_in"])
+        try:
+            prefix = next_fused_prefix(encoder, "extend_bias_pack")
+            suffix = fused_suffix(encoder, quant, all_stages=True)
+            self.int8_encoder_metadata = None
+            if self.int8_encode:
+                from .opt.encoder_int8_integration import install_int8_encoder_prefix
+                try:
+                    self.int8_encoder_metadata = install_int8_encoder_prefix(prefix, require_cuda=True,
+                                                                             tile_variant="auto")
+                except Exception as exc:  # noqa: BLE001 - an explicit option has no fallback
+                    raise RuntimeError("int8_encode installation failed; no fallback was applied") from exc
+                logger.info("[H3VAE-PyOpt] INT8 encoder convolutions: %d", self.int8_encoder_metadata["count"])
+        except BaseException:
+            restore_selected(swaps)
+            raise
         self.prefix, self.suffix = prefix, suffix
 
     @staticmethod

@@ -10,8 +10,12 @@ The attention between the fused QK-RoPE and the output projection, which the
 reference hands to the model's ``perform_attention`` (:66-74), runs as
 ``h3v_attention_d64`` (``attention_d64`` below): q and k straight from the
 QK-RoPE outputs and v as the strided slice of the QKV projection, no copies.
-Calls that carry ``pack_info`` (packed-sequence masks of the model code) keep
-the model's own attention.
+The kernel computes unmasked attention over each (batch, head).  A call that
+carries a non-empty ``pack_info`` (the model code's packed-sequence metadata,
+whose layout the reference leaves to the external model) or no rotary table
+raises ``ValueError`` rather than running a different path; a wrapper built
+with ``native_attention=False`` keeps the model's ``perform_attention`` for
+every call, as the reference does.
 """
 from __future__ import annotations
 
@@ -106,17 +110,30 @@ class FusedQKAttention(torch.nn.Module):
 
     def forward(self, x, rotary_pos_emb=None, pack_info=None):
         if rotary_pos_emb is None:
+            if self.native_attention:
+                raise ValueError("FusedQKAttention with native attention needs the rotary table (cos, sin); "
+                                 "build it with native_attention=False to run the model's own attention")
             return self.original(x, rotary_pos_emb, pack_info or {})
         b, n, _ = x.shape
         a = self.original
         qkv = a.to_qkv(x)
         q, k = qk_rope(qkv, *rotary_pos_emb, a.heads, a.norm_q.eps, self.rows)
         v = qkv.view(b, n, a.heads, 3 * a.dim_head)[..., 2 * a.dim_head:]
-        if self.native_attention and not pack_info:
-            y = attention_d64(q, k, v, a.dim_head ** -0.5)
-        else:
-            y = a.perform_attention(q, k, v, pack_info or {})
-        return a.to_out(y.reshape(b, n, -1))
+        return a.to_out(run_attention(self, q, k, v, pack_info).reshape(b, n, -1))
+
+
+def run_attention(wrapper, q, k, v, pack_info):
+    """The attention of a FusedQKAttention ``wrapper`` on q, k, v [B, N, H, 64]: ``attention_d64`` (unmasked)
+    when the wrapper is native, else the model's ``perform_attention``.  A native wrapper refuses a non-empty
+    ``pack_info``: the kernel has no packed-sequence masking, and the call must not silently change path."""
+    a = wrapper.original
+    if not getattr(wrapper, "native_attention", False):
+        return a.perform_attention(q, k, v, pack_info or {})
+    if pack_info:
+        raise ValueError("attention_d64 computes unmasked attention and cannot apply pack_info "
+                         f"(keys {sorted(map(str, pack_info))}); build the decoder with "
+                         "clone_with_qk_fusion(..., native_attention=False) to use the model's perform_attention")
+    return attention_d64(q, k, v, a.dim_head ** -0.5)
 
 
 def clone_with_qk_fusion(raw, rows=8, native_attention=True):
@@ -125,7 +142,8 @@ def clone_with_qk_fusion(raw, rows=8, native_attention=True):
     Weights are shared read-only and the original decoder is left intact
     (reference opt/decoder_fused_qk_rope.py:76-89).  ``native_attention=False``
     keeps the model's ``perform_attention`` for every call (the reference's
-    behaviour); the default runs ``attention_d64`` when no ``pack_info`` is given.
+    behaviour); the default runs ``attention_d64`` and refuses calls with a
+    non-empty ``pack_info`` or without a rotary table.
     """
     if raw.training or os.environ.get("MINIMAX_H3_VAE_DECODER_VIT_FP32_NORM", "1").lower() in ("0", "false", "no",
                                                                                                "off"):

@@ -21,10 +21,16 @@ wiring functions in those files build it.
   quant, FFN-up + SwiGLU + requant, FFN-down) on gfx950; elsewhere
   ``residual_rms_linear`` then ``swiglu_int8_linear``.
 * the hand-over.  ``carry`` off: ``h + out * scale2``.  ``carry`` on: the
-  tuple ``(h, out, scale2)`` while the rows stay eligible (contiguous fp16
-  ``[B, N, width]`` on a gfx950 GPU with a rotary table); the last block hands
-  it to ``CarryLayerNorm`` (``h3vae_final_ln::residual_ln_w8``) through the
-  decoder's unpad hook, which lets a carry through only with zero padding.
+  tuple ``(h, out, scale2)``; the last block hands it to ``CarryLayerNorm``
+  (``h3vae_final_ln::residual_ln_w8``) through the decoder's unpad hook, which
+  lets a carry through only with zero padding.
+
+A ``carry`` block runs only the fused kernels.  Rows the carry kernels cannot
+take (not contiguous fp16 ``[B, N, width]`` on a gfx950 GPU, or no rotary
+table), a plain tensor reaching a block after the first, or a carry reaching
+block 0 raise ``ValueError``.  The reference drops to eager torch for those
+calls (opt/int8_norm1_quant.py:218-252, non-B4 shapes); here the decode-fusion
+mode never changes path silently.
 """
 from __future__ import annotations
 
@@ -120,38 +126,47 @@ class Int8Block(nn.Module):
         return self.norm1(h.float()).to(h.dtype)
 
     def _attention_from_qkv(self, qkv, rotary, pack_info):
+        from .decoder_fused_qk_rope import run_attention
         wrapper, a = self.attn, self.attn.original
         b, n, _ = qkv.shape
         q, k = self._rope(qkv, *rotary, a.heads, a.norm_q.eps, wrapper.rows)
         v = qkv.view(b, n, a.heads, 3 * a.dim_head)[..., 2 * a.dim_head:]
-        if getattr(wrapper, "native_attention", False) and not pack_info:
-            from .decoder_fused_qk_rope import attention_d64
-            y = attention_d64(q, k, v, a.dim_head ** -0.5)
-        else:
-            y = a.perform_attention(q, k, v, pack_info)
-        return a.to_out(y.reshape(b, n, -1))
+        return a.to_out(run_attention(wrapper, q, k, v, pack_info).reshape(b, n, -1))
+
+    def _require_rows(self, h, rotary):
+        """Refuse rows the carry kernels cannot take (no eager fallback in the decode-fusion mode)."""
+        if not self._eligible(h):
+            got = (f"{tuple(h.shape)} {h.dtype} on {h.device}, contiguous={h.is_contiguous()}"
+                   if isinstance(h, torch.Tensor) else type(h).__name__)
+            platform = "" if self.fuse_norm1 else " (the block's parameters are not on a gfx950 GPU)"
+            raise ValueError(f"fused INT8 decoder block: the carry kernels take contiguous fp16 [B, N, "
+                             f"{self.scale1.shape[0]}] rows on a gfx950 GPU{platform}; got {got}")
+        if rotary is None:
+            raise ValueError("fused INT8 decoder block: the carry path needs the rotary table (cos, sin)")
 
     def _enter(self, states, rotary, pack_info):
-        """-> (residual stream, attention output, whether the block may hand on a carry)."""
+        """-> (residual stream, attention output)."""
         if isinstance(states, tuple):
+            if not self.carry or self.first:
+                raise ValueError("a residual carry (h, out, scale2) reached a block that does not take one "
+                                 f"(carry={self.carry}, first={self.first})")
             h, prev_out, prev_scale2 = states
-            fusable = (not self.first and self._eligible(h) and rotary is not None and prev_out.shape == h.shape
-                       and prev_out.dtype == torch.float16 and prev_out.is_contiguous())
-            if fusable:
-                from .int8_norm1_quant import residual_qkv
-                lin = self.attn.original.to_qkv
-                qkv = residual_qkv(h, prev_out, prev_scale2, self.norm1.weight, lin.qweight, lin.weight_scale,
-                                   lin.bias)
-                return h, self._attention_from_qkv(qkv, rotary, pack_info), True
-            h = h + prev_out * prev_scale2
-            return h, self.attn(self._model_norm1(h), rotary, pack_info), False
-        if self.carry and self.first and self._eligible(states):
+            self._require_rows(h, rotary)
+            if not (isinstance(prev_out, torch.Tensor) and prev_out.shape == h.shape
+                    and prev_out.dtype == torch.float16 and prev_out.is_contiguous()):
+                raise ValueError("the carried block output must be contiguous fp16 of the residual's shape")
+            from .int8_norm1_quant import residual_qkv
+            lin = self.attn.original.to_qkv
+            qkv = residual_qkv(h, prev_out, prev_scale2, self.norm1.weight, lin.qweight, lin.weight_scale, lin.bias)
+            return h, self._attention_from_qkv(qkv, rotary, pack_info)
+        if self.carry:
+            if not self.first:
+                raise ValueError("a fused INT8 decoder block after the first needs the previous block's residual "
+                                 "carry (h, out, scale2), got a plain tensor")
+            self._require_rows(states, rotary)
             from .decoder_block0_norm import rms_fp16_x2_w16
-            normed = rms_fp16_x2_w16(states, self.norm1.weight)
-        else:
-            normed = self._model_norm1(states)
-        attn = self.attn(normed, rotary, pack_info)
-        return states, attn, self.carry and self._eligible(states) and rotary is not None
+            return states, self.attn(rms_fp16_x2_w16(states, self.norm1.weight), rotary, pack_info)
+        return states, self.attn(self._model_norm1(states), rotary, pack_info)
 
     def _ffn(self, h, attn):
         w1, w2 = self.ff.w1, self.ff.w2
@@ -168,16 +183,18 @@ class Int8Block(nn.Module):
     def forward(self, states, rotary_pos_emb=None, pack_info=None):
         require_inference(self)
         pack_info = {} if pack_info is None else pack_info
-        h, attn, chained = self._enter(states, rotary_pos_emb, pack_info)
+        h, attn = self._enter(states, rotary_pos_emb, pack_info)
         h, out = self._ffn(h, attn)
-        hand_on = self._eligible(h) if self.last else chained
-        if self.carry and hand_on:
+        if self.carry:
             return h, out, self.scale2
         return h + out * self.scale2
 
 
 class CarryLayerNorm(nn.Module):
-    """The decoder's final LayerNorm, also taking the last block's carry (reference opt/int8_norm1_quant.py:31-46)."""
+    """The decoder's final LayerNorm, also taking the last block's carry (reference opt/int8_norm1_quant.py:31-46).
+
+    In a carry decoder the last ``Int8Block`` always hands over the tuple (or has raised), so the tensor branch
+    is the standalone adapter's contract only: the model's own LayerNorm of a plain tensor, as in the reference."""
 
     def __init__(self, original):
         super().__init__()

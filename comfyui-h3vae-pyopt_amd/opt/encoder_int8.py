@@ -139,8 +139,9 @@ def quantize_activation_tensor(x, *, check_finite: bool = False):
     x = x.contiguous(memory_format=_CL3D)
     qx = torch.empty(x.shape, dtype=torch.int8, device=x.device, memory_format=_CL3D)
     scale = torch.empty((), dtype=torch.float32, device=x.device)
-    partials = torch.empty((int(_hip.lib().h3v_tensor_quant_scratch_words()),), dtype=torch.int32, device=x.device)
-    _hip.call("h3v_tensor_quant_i8", _hip.ptr(x), x.numel(), _hip.ptr(qx), _hip.ptr(scale), _hip.ptr(partials),
+    words = int(_hip.lib().h3v_tensor_quant_scratch_words())
+    partials = torch.empty((words,), dtype=torch.int32, device=x.device)
+    _hip.call("h3v_tensor_quant_i8", _hip.ptr(x), x.numel(), _hip.ptr(qx), _hip.ptr(scale), _hip.ptr(partials), words,
               _hip.stream(x.device))
     return qx, scale
 

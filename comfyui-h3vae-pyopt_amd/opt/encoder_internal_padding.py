@@ -74,14 +74,26 @@ class _Swap:
 
 
 def replace_selected(encoder, names):
-    """Wrap the named convs of ``encoder`` in place; -> handles for ``restore_selected``."""
-    swaps = []
+    """Wrap the named convs of ``encoder`` in place; -> handles for ``restore_selected``.
+
+    Every named conv is checked and wrapped before any is swapped in, so a conv the wrapper refuses (for
+    instance a ``conv_in`` whose spatial padding is not reflect) raises ``ValueError`` naming it and leaves
+    the encoder untouched."""
+    planned = []
     for path in names:
         *owner_path, leaf = path.split(".")
         owner = encoder.get_submodule(".".join(owner_path))
-        swaps.append(_Swap(owner, leaf, owner._modules[leaf]))
-        owner._modules[leaf] = ImplicitTemporalPadConv3d(swaps[-1].original)
-    return swaps
+        original = owner._modules[leaf]
+        try:
+            wrapper = ImplicitTemporalPadConv3d(original)
+        except ValueError as exc:
+            raise ValueError(f"{path}: {exc} (causal={getattr(original, 'causal', None)!r}, "
+                             f"pad_mode={getattr(original, 'pad_mode', None)!r}, "
+                             f"pad_mode_t={getattr(original, 'pad_mode_t', None)!r}); no conv was replaced") from exc
+        planned.append((_Swap(owner, leaf, original), wrapper))
+    for swap, wrapper in planned:
+        swap.owner._modules[swap.name] = wrapper
+    return [swap for swap, _ in planned]
 
 
 def restore_selected(replacements):

@@ -238,12 +238,13 @@ int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batc
 
 /* Per-tensor dynamic activation quant of a contiguous fp16 tensor of n
  * elements: scale = amax * fp32(1/127) (0 -> 1), q = clamp(half-away(x/scale),
- * +-127).  scratch: h3v_tensor_quant_scratch_words() 32-bit words of device
- * scratch (partial maxima; nothing needs clearing between calls).
+ * +-127).  scratch: scratch_words 32-bit words of device scratch (partial
+ * maxima; nothing needs clearing between calls), at least
+ * h3v_tensor_quant_scratch_words(); a shorter one is rejected (H3V_EINVAL).
  * Replaces quantize_activation_tensor (opt/encoder_int8.py:384-426). */
 int64_t h3v_tensor_quant_scratch_words(void);
 int h3v_tensor_quant_i8(const uint16_t* x, int64_t n, int8_t* q, float* scale, uint32_t* scratch,
-                        hipStream_t stream);
+                        int64_t scratch_words, hipStream_t stream);
 
 /* Float count of the workspace h3v_gn_norm_pack_i8 needs for a [d, h, w] input. */
 int64_t h3v_gn_norm_pack_workspace_floats(int d, int h, int w);

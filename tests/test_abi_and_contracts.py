@@ -67,7 +67,9 @@ def test_entry_points_reject_bad_arguments_before_any_launch(ops):
     with pytest.raises(ValueError, match="too small"):
         ops.hip.call("h3v_conv3d_i8", 16, 16, 16, 16, None, 16, 1, 8, 2, 4, 4, 8, 3, 3, 3, 1, 1, 1, 0, None)
     with pytest.raises(ValueError, match="nonempty"):
-        ops.hip.call("h3v_tensor_quant_i8", 16, 0, 16, 16, 16, None)
+        ops.hip.call("h3v_tensor_quant_i8", 16, 0, 16, 16, 16, 1024, None)
+    with pytest.raises(ValueError, match="scratch holds 1 words"):   # the one-word amax buffer of an older contract
+        ops.hip.call("h3v_tensor_quant_i8", 16, 64, 16, 16, 16, 1, None)
     with pytest.raises(ValueError, match="blocks in"):
         ops.hip.call("h3v_probe_mfma_rate", 16, 16, 16, 16, 0, 1, 16, 16, None)
     pad = ("h3v_conv3d_i8_residual_padded", 16, 32, 48, 64, None)

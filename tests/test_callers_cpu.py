@@ -171,6 +171,50 @@ def test_qk_fusion_clone_wraps_every_attention(mods):
         int8_block(dec.transformer_blocks[0], carry=True)
 
 
+# -- no silent eager fallback in the decode-fusion mode ----------------------------------------------------
+
+def test_native_attention_refuses_pack_info_and_missing_rotary(mods):
+    qk = mods["decoder_fused_qk_rope"]
+    dec = h3_arch.H3Decoder(dim=1024, hidden=512, depth=1).eval()
+    native = qk.clone_with_qk_fusion(dec, rows=8).transformer_blocks[0].attn
+    q = k = v = torch.zeros(1, 4, 16, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="cannot apply pack_info"):
+        qk.run_attention(native, q, k, v, {"cu_seqlens": torch.tensor([0, 4])})
+    with torch.inference_mode(), pytest.raises(ValueError, match="rotary table"):
+        native(torch.zeros(1, 4, 1024), None, {})
+    # the model's attention only on explicit request (the reference's behaviour), pack_info passed through
+    model = qk.clone_with_qk_fusion(dec, rows=8, native_attention=False).transformer_blocks[0].attn
+    with patch.object(model.original, "perform_attention", return_value="model") as perform:
+        assert qk.run_attention(model, q, k, v, {"cu_seqlens": 1}) == "model"
+    perform.assert_called_once_with(q, k, v, {"cu_seqlens": 1})
+
+
+def test_carry_blocks_raise_instead_of_eager_fallback(mods):
+    qk, d8 = mods["decoder_fused_qk_rope"], mods["decoder_int8"]
+    fused = qk.clone_with_qk_fusion(h3_arch.H3Decoder(dim=1024, hidden=512, depth=2).eval(), rows=8)
+    first = d8.Int8Block(fused.transformer_blocks[0], carry=True, first=True).eval()
+    second = d8.Int8Block(fused.transformer_blocks[1], carry=True, last=True).eval()
+    plain = d8.Int8Block(fused.transformer_blocks[1]).eval()
+    h = torch.zeros(1, 4, 1024, dtype=torch.float16)
+    rotary = (torch.zeros(1, 4, 1, 48, dtype=torch.float16),) * 2
+    with torch.inference_mode():
+        # rows the carry kernels cannot take (here: CPU tensors; the block is not on a gfx950 GPU)
+        with pytest.raises(ValueError, match="carry kernels take contiguous fp16"):
+            first(h, rotary, {})
+        with pytest.raises(ValueError, match="carry kernels take contiguous fp16"):
+            second((h, h, h[0, 0]), rotary, {})
+        # a plain tensor after block 0, a carry into block 0 or into a block built without carry
+        with pytest.raises(ValueError, match="previous block's residual carry"):
+            second(h, rotary, {})
+        with pytest.raises(ValueError, match="does not take one"):
+            first((h, h, h[0, 0]), rotary, {})
+        with pytest.raises(ValueError, match="does not take one"):
+            plain((h, h, h[0, 0]), rotary, {})
+    # rows the kernels take, but no rotary table
+    with patch.object(second, "_eligible", return_value=True), pytest.raises(ValueError, match="rotary table"):
+        second._require_rows(h, None)
+
+
 # -- E9 / C1 encoder wiring ---------------------------------------------------------------------------------
 
 def test_prefix_structure_and_int8_policy(mods):
@@ -222,6 +266,16 @@ def test_implicit_temporal_pad_geometry_and_no_cpu_fallback(mods):
     assert type(parent.child.conv).__name__ == "ImplicitTemporalPadConv3d"
     ip.restore_selected(rep)
     assert parent.child.conv is conv
+
+
+def test_non_reflect_conv_in_is_refused_before_any_swap(mods):
+    ip = mods["encoder_internal_padding"]
+    enc = h3_arch.H3Encoder()
+    down, conv_in = enc.down[0].downsample.conv, enc.conv_in
+    conv_in.pad_mode = "replicate"
+    with pytest.raises(ValueError, match="conv_in: .*pad_mode='replicate'.*no conv was replaced"):
+        ip.replace_selected(enc, ["down.0.downsample.conv", "conv_in"])
+    assert enc.down[0].downsample.conv is down and enc.conv_in is conv_in
 
 
 def test_encode_staged_clips_batches_and_token_drop(mods):

@@ -305,9 +305,10 @@ def _tensor_quant_gpu(ops, x):
     xd = x.to(DEV).contiguous()
     q = torch.empty(x.shape, dtype=torch.int8, device=DEV)
     s = torch.empty((), dtype=torch.float32, device=DEV)
-    scratch = torch.full((int(ops.hip.lib().h3v_tensor_quant_scratch_words()),), -1, dtype=torch.int32, device=DEV)
+    words = int(ops.hip.lib().h3v_tensor_quant_scratch_words())
+    scratch = torch.full((words,), -1, dtype=torch.int32, device=DEV)
     ops.hip.call("h3v_tensor_quant_i8", ops.hip.ptr(xd), x.numel(), ops.hip.ptr(q), ops.hip.ptr(s),
-                 ops.hip.ptr(scratch), ops.hip.stream(DEV))
+                 ops.hip.ptr(scratch), words, ops.hip.stream(DEV))
     torch.cuda.synchronize()
     return np_(q), np.float32(s.item())
 

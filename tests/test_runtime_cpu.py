@@ -385,6 +385,13 @@ def test_encoder_wiring_on_a_reconstructed_core(rt, pkg):
             raise AssertionError("not called")
 
     config = {"latents_mean": [0.0] * 24, "latents_std": [1.0] * 24}
+    # a conv_in without a reflect border is refused before any conv of the caller's core is swapped
+    bad = _Core().eval()
+    bad.encoder.conv_in.pad_mode = "constant"
+    down, conv_in = bad.encoder.down[0].downsample.conv, bad.encoder.conv_in
+    with pytest.raises(ValueError, match="conv_in: .*pad_mode='constant'"):
+        rt.H3VAEPyOptRuntime(device="cpu", dtype=torch.float32, log_calls=False, core=bad, config=config)
+    assert bad.encoder.down[0].downsample.conv is down and bad.encoder.conv_in is conv_in
     runtime = rt.H3VAEPyOptRuntime(device="cpu", dtype=torch.float32, log_calls=False, core=_Core().eval(),
                                    config=config)
     assert type(runtime.prefix.conv_in).__name__ == "ImplicitTemporalPadConv3d"
