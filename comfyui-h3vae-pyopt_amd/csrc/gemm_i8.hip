@@ -793,6 +793,237 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_i8_mfma(GemmParams p) {
     write_tile<BM, BN, WGM, WGN, RING, EP>(p, acc, smem, m0, n0, tn);
 }
 
+// Ping-pong INT8 GEMM (AMode::Gemm, Dequant or Int32 epilogue): 256 x 256 x 128 tiles, 8 waves in two
+// groups of four (one wave of each group per SIMD: wave w runs on SIMD w % 4).  Group g owns output rows
+// 128 g .. 128 g + 127 of the tile, and wave s of a group the 64 columns 64 s .. 64 s + 63: a 128 x 64 block
+// of v_mfma_i32_32x32x32_i8 accumulators, as in gemm_i8_mfma.  Instead of interleaving fragment reads with
+// MFMAs inside every wave, the two waves of a SIMD alternate whole phases, one workgroup barrier apart:
+//
+//   phase 2k     group 0 reads all fragments of K step k from LDS (24 x 16 bytes per lane) and issues
+//                the weight DMA of step k + 1; group 1 runs its 32 MFMAs of step k - 1;
+//   phase 2k + 1 group 0 runs its 32 MFMAs of step k; group 1 reads its fragments of step k and issues
+//                the activation DMA of step k + 2.
+//
+// So on every SIMD one wave issues nothing but MFMAs for a whole phase while its partner does the LDS reads,
+// the LDS-DMA issue and the waits, and the matrix pipe never waits on a fragment read of its own wave.
+// Ring: three activation slots and two weight slots of 32 KB (160 KB).  Stage k is read in phases 2k and
+// 2k + 1; its slots are refilled (A k + 3, B k + 2) from phase 2k + 2 on, and every issuing wave waits for
+// its own loads of stage k + 1 before the barrier that ends phase 2k + 1.  Group 1 starts one phase late
+// (an extra barrier up front) and skips the barrier after its last MFMA phase, so both groups pass the same
+// number of barriers.  Epilogue: each wave converts its own block into a private 16 KB LDS region and stores
+// it as whole 128-byte row segments (no workgroup barrier), so group 0's epilogue runs while group 1 still
+// issues its last MFMAs.
+template <Epi EP>
+__global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
+    static_assert(EP == Epi::Dequant || EP == Epi::Int32, "ping-pong GEMM epilogues");
+    constexpr int BM = 256, BN = 256, BK = 128;
+    constexpr int SLOT = 256 * BK;                        // 32 KB per operand slot
+    constexpr int NSA = 3;                                // activation slots; weights have 2
+    constexpr int PW = 8;                                 // DMA instructions per issuing wave and stage
+    extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, sw4 = wave & 3;
+
+    int tm, tn;
+    grouped_tile(xcd_remap(blockIdx.x, gridDim.x), p.tiles_m, p.tiles_n, 8, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int nk = p.K / BK;
+
+    // DMA: group 1 moves the activation rows, group 0 the weight rows; wave s of a group the 64 tile rows
+    // 64 s .. 64 s + 63, eight rows of 128 bytes per instruction (lane: row lane / 8, chunk lane % 8 of it,
+    // fetched from k-chunk (lane % 8) ^ swz(row))
+    const int lrow = lane >> 3, lslot = lane & 7;
+    const __amdgpu_buffer_rsrc_t rsrc =
+        grp ? __builtin_amdgcn_make_buffer_rsrc((void*)p.a, 0, (int)p.a_bytes, kRsrcWord3)
+            : __builtin_amdgcn_make_buffer_rsrc((void*)p.b, 0, (int)p.b_bytes, kRsrcWord3);
+    uint32_t doff[PW];
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+        const int r = (sw4 * PW + j) * 8 + lrow;
+        int64_t base;
+        if (grp) {
+            const int m = m0 + r < p.M ? m0 + r : p.M - 1;
+            base = (int64_t)m * p.lda;
+        } else {
+            const int n = n0 + r < p.N ? n0 + r : p.N - 1;
+            base = (int64_t)n * p.K;
+        }
+        doff[j] = (uint32_t)(base + ((lslot ^ swz<BK>(r)) << 4));
+    }
+    int8_t* const ring = grp ? smem : smem + NSA * SLOT;
+    auto issue = [&](int k) {
+        int8_t* dst = ring + (grp ? k % NSA : k & 1) * SLOT + sw4 * PW * 1024;
+#pragma unroll
+        for (int j = 0; j < PW; ++j) lds_dma16(rsrc, doff[j], (uint32_t)(k * BK), dst + j * 1024);
+    };
+
+    v16i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+
+    // fragments of one K step: lane reads row (lane & 31) of a 32-row block, k-chunk (lane >> 5) + 2 ks
+    const int frow = lane & 31, fhi = lane >> 5;
+    v4i fa[4][4], fb[4][2];   // [ks][block]
+    auto load_frags = [&](int k) {
+        const int8_t* sa = smem + (k % NSA) * SLOT;
+        const int8_t* sb = smem + NSA * SLOT + (k & 1) * SLOT;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int kc = fhi + 2 * ks;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = grp * 128 + i * 32 + frow;
+                fa[ks][i] = *reinterpret_cast<const v4i*>(sa + r * BK + ((kc ^ swz<BK>(r)) << 4));
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int r = sw4 * 64 + j * 32 + frow;
+                fb[ks][j] = *reinterpret_cast<const v4i*>(sb + r * BK + ((kc ^ swz<BK>(r)) << 4));
+            }
+        }
+    };
+    auto mfma_step = [&]() {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
+    };
+
+    // prologue: weights 0, 1 by group 0; activations 0, 1, 2 by group 1; stage 0 lands before the first barrier
+    if (grp == 0) {
+        issue(0);
+        if (nk > 1) { issue(1); wait_vmcnt<PW>(); } else { wait_vmcnt<0>(); }
+    } else {
+        issue(0);
+        if (nk > 1) issue(1);
+        if (nk > 2) { issue(2); wait_vmcnt<2 * PW>(); }
+        else if (nk > 1) wait_vmcnt<PW>();
+        else wait_vmcnt<0>();
+    }
+    lds_barrier();
+    if (grp == 1) lds_barrier();                      // group 1 runs one phase behind
+    __builtin_amdgcn_sched_barrier(0);
+    for (int k = 0; k < nk; ++k) {
+        // load phase of step k
+        load_frags(k);
+        if (k >= 1) {
+            if (grp == 0) { if (k + 1 < nk) issue(k + 1); }
+            else { if (k + 2 < nk) issue(k + 2); }
+        }
+        if (grp == 1 && k + 1 < nk) {                 // activations of step k + 1 land before group 0 reads them
+            if (k + 2 < nk) wait_vmcnt<PW>();
+            else wait_vmcnt<0>();
+        }
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        // MFMA phase of step k
+        mfma_step();
+        __builtin_amdgcn_sched_barrier(0);
+        if (grp == 0) {
+            if (k + 1 < nk) wait_vmcnt<0>();          // weights of step k + 1
+            lds_barrier();
+        } else if (k + 1 < nk) {
+            lds_barrier();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // epilogue: lane holds rows m0 + 128 grp + 32 i + (lane & 31) and, in register r of block j, column
+    // n0 + 64 s + 32 j + (r / 4) * 8 + (lane >> 5) * 4 + r % 4
+    const int rbase = m0 + grp * 128;
+    const int cbase = n0 + sw4 * 64;
+    if constexpr (EP == Epi::Int32) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const int c0 = cbase + j * 32 + q4 * 8 + fhi * 4;
+                if (c0 >= p.N) continue;
+                const bool full = c0 + 4 <= p.N && (p.ldo & 3) == 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = rbase + i * 32 + frow;
+                    if (row >= p.M) continue;
+                    int32_t* dst = static_cast<int32_t*>(p.out) + (int64_t)row * p.ldo + c0;
+                    if (full) {
+                        *reinterpret_cast<v4i*>(dst) =
+                            v4i{acc[i][j][q4 * 4], acc[i][j][q4 * 4 + 1], acc[i][j][q4 * 4 + 2], acc[i][j][q4 * 4 + 3]};
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (c0 + e < p.N) dst[e] = acc[i][j][q4 * 4 + e];
+                    }
+                }
+            }
+    } else {
+        // the wave's 128 x 64 fp16 block in its own 16 KB of LDS: row r at 128 r, 16-byte chunk c (8 columns)
+        // at slot c ^ ((r >> 1) & 7), so the 8-byte writes of 32 rows and the 16-byte row reads stay at the
+        // minimum of two passes per 256 bytes
+        int8_t* stage = smem + wave * (128 * 128);
+        float sx[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = rbase + i * 32 + frow;
+            sx[i] = row < p.M ? p.sx[(int64_t)row * p.sx_stride] : 0.0f;
+        }
+        int qc[8], ql[8];
+        f32x4 qsw[8] = {};
+        u16x4 qb[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            qc[q] = cbase + (q >> 2) * 32 + (q & 3) * 8 + fhi * 4;
+            ql[q] = p.N;
+        }
+        auto convert = [&](auto hb) {
+            constexpr bool HB = decltype(hb)::value;
+            load_cols<8, HB>(p, qc, ql, qsw, qb);
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const int q = j * 4 + q4;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        u16x4 v;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sx[i], qsw[q][e], qb[q][e]));
+                        const int r = i * 32 + frow;
+                        *reinterpret_cast<u16x4*>(stage + r * 128 + ((q ^ ((r >> 1) & 7)) << 4) + fhi * 8) = v;
+                    }
+                }
+        };
+        if (p.bias) convert(std::true_type{});
+        else convert(std::false_type{});
+        __builtin_amdgcn_s_waitcnt((15 << 4) | (0 << 8) | 0xC00F);   // this wave's LDS writes are done
+        uint16_t* out = static_cast<uint16_t*>(p.out);
+        const int c8 = lane & 7;
+        const int gcol = cbase + c8 * 8;
+#pragma unroll 4
+        for (int t = 0; t < 16; ++t) {
+            const int r = t * 8 + (lane >> 3);
+            const int grow = rbase + r;
+            const u16x8 v = *reinterpret_cast<const u16x8*>(stage + r * 128 + ((c8 ^ ((r >> 1) & 7)) << 4));
+            if (grow >= p.M || gcol >= p.N) continue;
+            uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+            if (p.vec_out && gcol + 8 <= p.N) {
+                *reinterpret_cast<u16x8*>(dst) = v;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    if (gcol + e < p.N) dst[e] = v[e];
+            }
+        }
+    }
+}
+
 // Window row pitch in pixels of conv3_halo_i8 for tiles TW pixels wide: TW + 2 rounded up to 16 (the
 // plain swizzle works on 16-pixel groups) or, in the strided-pixel variant, to 8 (whole 256-byte lines).
 constexpr int halo_hpl(int tw, bool sp) { return sp ? (tw + 2 + 7) / 8 * 8 : (tw + 2 + 15) / 16 * 16; }
@@ -1395,6 +1626,30 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     return launch_status(what);
 }
 
+template <Epi EP>
+int launch_pingpong(GemmParams p, hipStream_t stream, const char* what) {
+    p.tiles_m = (p.M + 255) / 256;
+    p.tiles_n = (p.N + 255) / 256;
+    p.vec_epi = (p.sw == nullptr || aligned(p.sw, 16)) && (p.bias == nullptr || aligned(p.bias, 8)) && p.N % 4 == 0;
+    p.vec_out = aligned(p.out, 16) && p.ldo % 8 == 0;
+    const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+    if (tiles > 0x7fffffff) return fail(H3V_EINVAL, "%s: too many tiles", what);
+    const int64_t a_bytes = (int64_t)p.M * p.lda, b_bytes = (int64_t)p.N * p.K;
+    if (a_bytes >= ((int64_t)1 << 32) || b_bytes >= ((int64_t)1 << 32))
+        return fail(H3V_EINVAL, "%s: an operand exceeds 4 GiB (%lld, %lld bytes)", what, (long long)a_bytes,
+                    (long long)b_bytes);
+    p.a_bytes = (uint32_t)a_bytes;
+    p.b_bytes = (uint32_t)b_bytes;
+    constexpr size_t lds = 5 * 256 * 128;   // three activation and two weight slots: 160 KB
+    auto kernel = &gemm_i8_pingpong<EP>;
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, lds,
+                                        hipGetErrorString(attr));
+    hipLaunchKernelGGL(kernel, dim3((unsigned)tiles), dim3(512), lds, stream, p);
+    return launch_status(what);
+}
+
 template <AMode AM, Epi EP>
 int launch_generic(GemmParams p, hipStream_t stream, const char* what) {
     int64_t total = (int64_t)p.M * p.N;
@@ -1410,6 +1665,8 @@ int run_gemm(GemmParams p, hipStream_t stream, const char* what) {
     // K <= 4096: the two-stage ring (one barrier-to-use step of prefetch) measured faster
     // than three A stages (FFN-up 7188 x 16384 x 2048: 285 vs 305 us); long K keeps the
     // deeper A ring (FFN-down 7188 x 2048 x 8192: 116 vs 132 us).
+    if constexpr (EP == Epi::Dequant || EP == Epi::Int32)
+        if (al && p.K % 128 == 0) return launch_pingpong<EP>(p, stream, what);
     if (al && p.K % 128 == 0 && p.K <= 4096) return launch_tiled<256, 256, 128, 2, 4, 2, 2, AMode::Gemm, EP>(p, stream, what);
     if (al && p.K % 128 == 0) return launch_tiled<256, 256, 128, 2, 4, 3, 2, AMode::Gemm, EP>(p, stream, what);
     if (al && p.K % 64 == 0) return launch_tiled<256, 256, 64, 2, 4, 4, 4, AMode::Gemm, EP>(p, stream, what);

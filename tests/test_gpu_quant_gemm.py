@@ -132,7 +132,9 @@ def _i32_gpu(ops, a, w):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 256, 2048), (17, 6144, 2048), (129, 512, 1024), (300, 200, 192),
-                                   (256, 256, 64), (5, 7, 33), (2, 3, 5)])
+                                   (256, 256, 64), (5, 7, 33), (2, 3, 5),
+                                   # one, two, three and many K steps of 128, ragged M and N (13: scalar stores)
+                                   (257, 300, 128), (70, 13, 256), (300, 520, 384), (515, 264, 8192)])
 def test_gemm_int32_accumulators_exact(ops, oracle, m, n, k):
     gen = _gen(m + n + k)
     a = torch.randint(-128, 128, (m, k), generator=gen, dtype=torch.int8)
@@ -158,7 +160,8 @@ def test_gemm_int32_full_size_sampled_rows(ops):
 
 
 @pytest.mark.parametrize("m,n,k,with_bias", [(1, 6144, 2048, True), (17, 2048, 2048, False), (129, 1024, 4096, True),
-                                             (300, 200, 192, True), (5, 7, 33, False)])
+                                             (300, 200, 192, True), (5, 7, 33, False), (257, 300, 128, True),
+                                             (70, 13, 256, True), (300, 520, 384, False), (515, 264, 8192, True)])
 def test_gemm_dequant_matches_oracle(ops, oracle, m, n, k, with_bias):
     gen = _gen(m * 3 + n)
     a = torch.randint(-128, 128, (m, k), generator=gen, dtype=torch.int8)
