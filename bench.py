@@ -471,8 +471,182 @@ def cpu_configs(rng, threads):
     return out
 
 
+def _cpu_row_quant(x):
+    """Q1 per-row quant on the CPU (CK quantize_int8_rowwise): s = max|x| / 127 per row (1 for a zero row),
+    q = round(x / s) clamped to +-127."""
+    import torch
+    xf = x.float()
+    s = xf.abs().amax(dim=-1, keepdim=True) / 127.0
+    s = torch.where(s > 0, s, torch.ones_like(s))
+    return torch.round(xf / s).clamp_(-127, 127).to(torch.int8), s
+
+
+def _cpu_tensor_quant(x):
+    """E3 per-tensor quant on the CPU (reference opt/encoder_int8.py:591-610): half-away rounding."""
+    import torch
+    xf = x.float()
+    s = xf.abs().amax() / 127.0
+    s = torch.where(s > 0, s, torch.ones_like(s))
+    y = xf / s
+    q = torch.where(y >= 0, torch.floor(y + 0.5), -torch.floor(-y + 0.5))
+    return q.clamp_(-127, 127).to(torch.int8), s
+
+
+def _cpu_int8_linear(q, s, w_t, ws, bias):
+    """int8 [M, K] x int8 [K, N] -> exact int32 (torch._int_mm) -> fp16(acc * sx * sw + b)."""
+    import torch
+    acc = torch._int_mm(q, w_t)
+    return (acc.float() * s * ws + bias.float()).half()
+
+
+def _cpu_conv3x3x3(qx, qw_t, d, h, w):
+    """Valid 3x3x3 conv of an int8 NDHWC [d + 2, h + 2, w + 2, C] input as im2col + torch._int_mm (exact int32),
+    one output frame per GEMM: -> int32 [d, h * w, Cout]."""
+    import torch
+    out = []
+    for t in range(d):
+        cols = torch.cat([qx[t + kd, kh:kh + h, kw:kw + w] for kd in range(3) for kh in range(3) for kw in range(3)],
+                         dim=-1).reshape(h * w, -1)
+        out.append(torch._int_mm(cols, qw_t))
+    return torch.stack(out)
+
+
+def torch_cpu_configs(threads):
+    """BASELINE.json configs 1-4 in full through a PyTorch CPU restatement of the reference arithmetic (exact int32
+    GEMMs with torch._int_mm, convs as im2col + _int_mm, quantizers and norms in fp32): median of 5 runs after a
+    warm-up each."""
+    import torch
+    g = torch.Generator().manual_seed(20261002)
+    randn = lambda *shape, scale=1.0: (torch.randn(*shape, generator=g) * scale).half()
+    qweight = lambda n, k: torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    out = {}
+    # cfg1: per-tensor quant of the padded input, causal 3x3x3 conv C128 -> 128 (dense reduction), dequant
+    xp = torch.zeros(11, 66, 66, 128, dtype=torch.float16)
+    xp[2:] = randn(9, 66, 66, 128)
+    w1 = qweight(128, 3456).t()
+    ws1, b1 = torch.full((128,), 1e-4), torch.zeros(128, dtype=torch.float16)
+
+    def cfg1():
+        q, s = _cpu_tensor_quant(xp)
+        acc = _cpu_conv3x3x3(q, w1, 9, 64, 64)
+        return (acc.float() * s * ws1 + b1.float()).half()
+
+    m, d = 16384, 1024
+    h, o = randn(m, d), randn(m, d)
+    gate, gam, beta = randn(d, scale=0.1), (1 + 0.1 * torch.randn(d, generator=g)).half(), randn(d, scale=0.02)
+    wq, sq, bq = qweight(3072, d).t(), torch.full((3072,), 1e-3), randn(3072, scale=0.02)
+
+    def cfg2():   # residual + RMSNorm (fp32) + row quant, QKV GEMM 1024 -> 3072
+        hn = (h.float() + o.float() * gate.float()).half()
+        n = (hn.float() * torch.rsqrt(hn.float().pow(2).mean(-1, keepdim=True) + 1e-5) * gam.float()).half()
+        q, s = _cpu_row_quant(n)
+        return _cpu_int8_linear(q, s, wq, sq, bq)
+
+    x3 = randn(m, d)
+    wu, su, bu = qweight(8192, d).t(), torch.full((8192,), 1e-3), randn(8192, scale=0.02)
+    wd, sd, bd = qweight(d, 4096).t(), torch.full((d,), 1e-3), randn(d, scale=0.02)
+
+    def cfg3():   # row quant, FFN-up 1024 -> 2 x 4096, SwiGLU (fp32) + row quant, down 4096 -> 1024
+        q, s = _cpu_row_quant(x3)
+        gu = _cpu_int8_linear(q, s, wu, su, bu).float()
+        act = (torch.nn.functional.silu(gu[:, :4096]) * gu[:, 4096:]).half()
+        q2, s2 = _cpu_row_quant(act)
+        return _cpu_int8_linear(q2, s2, wd, sd, bd)
+
+    heads = 16
+    qkv = randn(1, m, heads, 192)
+    ang = torch.rand(m, 1, 24, generator=g) * 6.283
+    cos, sin = torch.cat([ang.cos()] * 2, -1), torch.cat([ang.sin()] * 2, -1)
+    wo, so, bo = qweight(d, d).t(), torch.full((d,), 1e-3), randn(d, scale=0.02)
+
+    def rope(t):   # RMS (fp32, no affine) then rotate-half on the first 48 dims
+        t = t.float()
+        t = (t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 1e-6)).half().float()
+        r = t[..., :48]
+        rot = torch.cat([-r[..., 24:], r[..., :24]], -1)
+        return torch.cat([r * cos + rot * sin, t[..., 48:]], -1)
+
+    def cfg4():   # QK-RMSNorm-RoPE, SDPA over 16384 tokens (fp32 on the CPU), out row quant + GEMM 1024 -> 1024
+        qh, kh, vh = rope(qkv[..., :64]), rope(qkv[..., 64:128]), qkv[..., 128:].float()
+        y = torch.nn.functional.scaled_dot_product_attention(qh.transpose(1, 2), kh.transpose(1, 2),
+                                                             vh.transpose(1, 2), scale=0.125)
+        q, s = _cpu_row_quant(y.transpose(1, 2).reshape(m, d).half())
+        return _cpu_int8_linear(q, s, wo, so, bo)
+
+    for key, fn in (("cfg1_causal_conv3d_c128_9x64x64", cfg1), ("cfg2_norm1_qkv_m16384_d1024", cfg2),
+                    ("cfg3_ffn_m16384_d1024_h4096", cfg3), ("cfg4_qk_rope_sdpa_out_proj_16384tok_16x64", cfg4)):
+        out[key] = {"s": round(_median_s(fn), 4), "sample": "full"}
+    return out
+
+
+def torch_cpu_step_sample():
+    """The INT8 hot path of the step on the CPU, sampled: one output frame of a stage-0 fused layer (GroupNorm
+    statistics, SiLU, pad, per-tensor quant, dense 3x3x3 conv C128 -> 128 on 256 x 256 pixels as im2col +
+    _int_mm, dequant) and one decoder block at the B4 shape M = 7188 (norm1 + row quant + QKV GEMM, QK-RMSNorm-
+    RoPE, SDPA fp32 over 4 x 32 heads x 1797 tokens, out GEMM, norm2 + row quant, FFN-up, SwiGLU + row quant,
+    FFN-down).  -> (encoder seconds per dense op, decoder seconds per block)."""
+    import torch
+    g = torch.Generator().manual_seed(20261002)
+    randn = lambda *shape, scale=1.0: (torch.randn(*shape, generator=g) * scale).half()
+    qweight = lambda n, k: torch.randint(-127, 128, (n, k), generator=g, dtype=torch.int8)
+    # encoder: the producer over the 3 input frames one output frame reads, then that frame's conv
+    x = randn(3, 256, 256, 128)
+    w0 = qweight(128, 3456).t()
+    ws0, b0 = torch.full((128,), 1e-4), torch.zeros(128, dtype=torch.float16)
+
+    def enc():
+        xf = x.float().view(3, 256 * 256, 32, 4)
+        mean = xf.mean(dim=(1, 3), keepdim=True)
+        var = xf.var(dim=(1, 3), keepdim=True, unbiased=False)
+        y = torch.nn.functional.silu((xf - mean) * torch.rsqrt(var + 1e-6)).view(3, 256, 256, 128).half()
+        yp = torch.nn.functional.pad(y.permute(0, 3, 1, 2).float(), (1, 1, 1, 1), mode="reflect").permute(0, 2, 3, 1)
+        q, s = _cpu_tensor_quant(yp.half())
+        acc = _cpu_conv3x3x3(q, w0, 1, 256, 256)
+        return (acc.float() * s * ws0 + b0.float()).half()
+
+    enc_s = _median_s(enc, runs=3)
+    enc_ops = 2 * 256 * 256 * 128 * 3456
+    # decoder block at M = 7188 (4 x 1797 tokens), width 2048, 32 heads
+    m, dd, heads = DEC_M, DEC_D, DEC_HEADS
+    h = randn(m, dd)
+    gam = (1 + 0.1 * torch.randn(dd, generator=g)).half()
+    w_qkv, w_o, w_u, w_d = qweight(3 * dd, dd).t(), qweight(dd, dd).t(), qweight(16384, dd).t(), qweight(dd, 8192).t()
+    sc = lambda n: torch.full((n,), 1e-3)
+    zb = lambda n: torch.zeros(n, dtype=torch.float16)
+    ang = torch.rand(m, 1, 24, generator=g) * 6.283
+    cos, sin = torch.cat([ang.cos()] * 2, -1), torch.cat([ang.sin()] * 2, -1)
+
+    def rms(t, w):
+        return (t.float() * torch.rsqrt(t.float().pow(2).mean(-1, keepdim=True) + 1e-5) * w.float()).half()
+
+    def rope(t):
+        t = t.float()
+        t = (t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 1e-6)).half().float()
+        r = t[..., :48]
+        rot = torch.cat([-r[..., 24:], r[..., :24]], -1)
+        return torch.cat([r * cos + rot * sin, t[..., 48:]], -1)
+
+    def dec():
+        q, s = _cpu_row_quant(rms(h, gam))
+        qkv = _cpu_int8_linear(q, s, w_qkv, sc(3 * dd), zb(3 * dd)).view(m, heads, 192)
+        qh, kh, vh = rope(qkv[..., :64]), rope(qkv[..., 64:128]), qkv[..., 128:].float()
+        split = lambda t: t.view(4, 1797, heads, 64).transpose(1, 2)
+        y = torch.nn.functional.scaled_dot_product_attention(split(qh), split(kh), split(vh), scale=0.125)
+        q, s = _cpu_row_quant(y.transpose(1, 2).reshape(m, dd).half())
+        h2 = (h.float() + _cpu_int8_linear(q, s, w_o, sc(dd), zb(dd)).float()).half()
+        q, s = _cpu_row_quant(rms(h2, gam))
+        gu = _cpu_int8_linear(q, s, w_u, sc(16384), zb(16384)).float()
+        q, s = _cpu_row_quant((torch.nn.functional.silu(gu[:, :8192]) * gu[:, 8192:]).half())
+        return _cpu_int8_linear(q, s, w_d, sc(dd), zb(dd))
+
+    dec_s = _median_s(dec, runs=3)
+    return enc_s / enc_ops, dec_s
+
+
 def cpu_baseline(budget_s: float):
-    """The CPU oracle on a bounded sample of the full step, extrapolated by op count; configs 1-4 per entry."""
+    """The reference arithmetic on the host CPU: BASELINE.json configs 1-4 in full through PyTorch (torch._int_mm,
+    median of 5), the full step extrapolated from one stage-0 conv frame and one decoder block; the scalar C oracle
+    beside it (configs 1-4 on row samples, labelled)."""
     import numpy as np
     import oracle
     import torch
@@ -480,59 +654,28 @@ def cpu_baseline(budget_s: float):
     threads = len(os.sched_getaffinity(0))
     oracle.set_threads(threads)
     torch.set_num_threads(threads)
+    configs = torch_cpu_configs(threads)
+    enc_s_per_op, dec_block_s = torch_cpu_step_sample()
+    _, dense = enc_ops_per_call()
+    enc_s = enc_s_per_op * ENC_CALLS * dense
+    dec_s = dec_block_s * DEC_BLOCKS * DEC_CALLS
     rng = np.random.default_rng(20261002)
-    configs = cpu_configs(rng, threads)
-    # sample 1: a stage-0 fused layer (norm producer + conv) on 3 frames of 64x256 pixels
-    x = rng.standard_normal((3, 64, 256, 128)).astype(np.float16)
-    gamma = np.ones(128, np.float16)
-    beta = np.zeros(128, np.float16)
-    qw = rng.integers(-127, 128, (128, 3456)).astype(np.int8)
-    ws = np.full(128, 1e-4, np.float32)
-    bias = np.zeros(128, np.float16)
-    # sample 2: one decoder block's GEMM work on 64 of 7188 rows
-    mrow = 64
-    a = rng.integers(-127, 128, (mrow, DEC_D)).astype(np.int8)
-    wq = rng.integers(-127, 128, (6144, DEC_D)).astype(np.int8)
-    wu = rng.integers(-127, 128, (16384, DEC_D)).astype(np.int8)
-    wd = rng.integers(-127, 128, (DEC_D, 8192)).astype(np.int8)
-    wo = rng.integers(-127, 128, (DEC_D, DEC_D)).astype(np.int8)
-    sx = np.full(mrow, 1e-2, np.float32)
-    t_enc = t_dec = 0.0
-    n_enc = n_dec = 0
-    start = time.perf_counter()
-    while time.perf_counter() - start < budget_s or n_enc == 0 or n_dec == 0:
-        t0 = time.perf_counter()
-        oracle.norm_conv3d(x, gamma, beta, 1e-6, qw, ws, bias)      # out: [3, 64, 256, 128]
-        t_enc += time.perf_counter() - t0
-        n_enc += 1
-        t0 = time.perf_counter()
-        qkv = oracle.gemm_dequant(oracle.gemm_acc(a, wq), sx, np.full(6144, 1e-3, np.float32))
-        oracle.gemm_dequant(oracle.gemm_acc(a, wo), sx, np.full(DEC_D, 1e-3, np.float32))
-        act = oracle.gemm_swiglu(oracle.gemm_acc(a, wu), sx, np.full(16384, 1e-3, np.float32))
-        q2, s2 = oracle.row_quant(act)
-        oracle.gemm_dequant(oracle.gemm_acc(q2, wd), s2, np.full(DEC_D, 1e-3, np.float32))
-        del qkv
-        t_dec += time.perf_counter() - t0
-        n_dec += 1
-    enc_sample_ops = 3 * 64 * 256 * 2 * 128 * 3456          # dense conv ops of the sample (3 frames)
-    dec_sample_ops = 2 * mrow * (6144 * DEC_D + DEC_D * DEC_D + 16384 * DEC_D + DEC_D * 8192)
-    useful, dense = enc_ops_per_call()
-    enc_total = ENC_CALLS * dense
-    dec_total = DEC_CALLS * dec_ops_per_call()
-    enc_s = (t_enc / n_enc) * enc_total / enc_sample_ops
-    dec_s = (t_dec / n_dec) * dec_total / dec_sample_ops
     return {
         "value": round(enc_s + dec_s, 1),
         "unit": "s (extrapolated)",
-        "cores": threads,
+        "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"CPU oracle (C, OpenMP {threads} threads): {n_enc}x one fused stage-0 norm+conv on a "
-                   f"3x64x256x128 input ({enc_sample_ops / 1e9:.1f} GOP) and {n_dec}x one decoder block's four "
-                   f"INT8 GEMMs + SwiGLU + requant on {mrow} of 7188 rows ({dec_sample_ops / 1e9:.1f} GOP); "
-                   f"extrapolated by op count to the INT8 work of the full step (encode {enc_s:.0f} s + decode "
-                   f"{dec_s:.0f} s; the FP16 layers are not included, so this is a lower bound)"),
+        "sample": (f"PyTorch CPU restatement of the reference arithmetic ({torch.get_num_threads()} threads; exact int32 "
+                   f"GEMMs with torch._int_mm, convs as im2col + _int_mm, quantizers and norms in fp32): one output "
+                   f"frame of a stage-0 fused layer (producer + dense 3x3x3 conv on 256x256x128) and one decoder block "
+                   f"at M = 7188 (GEMMs, row quants, norms, QK-RoPE, fp32 SDPA), median of 3 each, extrapolated by "
+                   f"dense conv op count to the {ENC_CALLS} prefix calls and x{DEC_BLOCKS} blocks x{DEC_CALLS} calls: "
+                   f"encode {enc_s:.0f} s + decode {dec_s:.0f} s (the encoder's FP16 layers are not included, so this "
+                   f"is a lower bound)"),
         "host": _host_cpu(),
+        "torch_threads": torch.get_num_threads(),
         "configs": configs,
+        "c_oracle_configs": {"kind": "port (scalar C oracle, OpenMP)", **cpu_configs(rng, threads)},
     }
 
 
