@@ -680,9 +680,9 @@ def cpu_baseline(budget_s: float):
 
 
 TRAFFIC_PROFILE = ROOT / "profiles" / "stage0_conv_traffic_pmc.md"
-GEMM_TRAFFIC_PROFILE = ROOT / "profiles" / "int8_gemm_k2048_traffic_pmc.md"
-GEMM_K2048_KERNEL = ("gemm_i8_mfma<256,256,128,2,4,2,2,Gemm,Dequant> (decoder INT8 GEMMs with K = 2048: QKV, "
-                     "attention-out, FFN-up; 256x256 tiles, two-slot LDS ring)")
+GEMM_TRAFFIC_PROFILE = ROOT / "profiles" / "int8_gemm_decoder_traffic_pmc.md"
+GEMM_KERNEL = ("gemm_i8_pingpong<Dequant> (every decoder INT8 GEMM: QKV, attention-out and FFN-up with K = 2048, "
+               "FFN-down with K = 8192; 256x256x128 tiles, two wave groups alternating MFMA and fragment-read phases)")
 
 
 def _profile_number(path, key):
@@ -705,9 +705,9 @@ def stage0_conv_traffic():
     return _profile_number(TRAFFIC_PROFILE, "traffic_bytes_per_launch")
 
 
-def gemm_k2048_traffic():
-    """HBM bytes per launch of the K = 2048 GEMM family (mean over the QKV, attention-out and FFN-up launches of
-    a decoder block), from the committed FETCH_SIZE/WRITE_SIZE summary of `bench.py --traffic-sample`."""
+def gemm_traffic():
+    """HBM (L2-miss) bytes per launch of the decoder GEMM kernel (mean over the QKV, attention-out, FFN-up and
+    FFN-down launches of a block), from the committed FETCH_SIZE/WRITE_SIZE summary of `bench.py --traffic-sample`."""
     return _profile_number(GEMM_TRAFFIC_PROFILE, "traffic_bytes_per_launch")
 
 
@@ -941,7 +941,8 @@ def main():
     conv_us, conv_n = timer.mean_us("stage0_conv")
     conv_ops = stage0_conv_useful_ops()
     achieved = conv_ops / conv_us / 1e6
-    # the dominant kernel by step time: the K = 2048 GEMM instantiation behind QKV, attention-out and FFN-up
+    # the dominant kernel by step time: the INT8 GEMM kernel behind every decoder linear (QKV, attention-out,
+    # FFN-up, FFN-down), one launch of each per block
     gemm_n = {"qkv": 3 * DEC_D, "attn_out": DEC_D, "ffn_up": 16384, "ffn_down": DEC_D}
     gemm_k = {"qkv": DEC_D, "attn_out": DEC_D, "ffn_up": DEC_D, "ffn_down": 8192}
     per_gemm = {}
@@ -950,7 +951,7 @@ def main():
         ops = 2 * DEC_M * gemm_n[key] * gemm_k[key]
         per_gemm[key] = {"avg_us": round(us, 2), "launches_timed": n, "ops_per_launch": ops,
                          "tops": round(ops / us / 1e6, 1), "frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)}
-    fam = ("qkv", "attn_out", "ffn_up")
+    fam = ("qkv", "attn_out", "ffn_up", "ffn_down")
     fam_n = sum(per_gemm[k]["launches_timed"] for k in fam)
     fam_us = sum(per_gemm[k]["avg_us"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
     fam_ops = sum(per_gemm[k]["ops_per_launch"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
@@ -984,18 +985,19 @@ def main():
                                    "source": "reference README.md:43,53-54"},
         "outputs_finite": finite,
         "roofline": {
-            "kernel": GEMM_K2048_KERNEL,
+            "kernel": GEMM_KERNEL,
             "bound": "mfma",
             "achieved": round(gemm_achieved, 1),
             "peak": INT8_PEAK_TOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_achieved / INT8_PEAK_TOPS, 4),
-            "traffic": gemm_k2048_traffic(),
+            "traffic": gemm_traffic(),
             "launches_timed": fam_n,
             "avg_us": round(fam_us, 2),
             "algorithmic_ops_per_launch": round(fam_ops),
             "launch_mix": "per decoder block: QKV 7188x6144x2048, attention-out 7188x2048x2048, FFN-up "
-                          "7188x16384x2048 (one of each); achieved = mean ops per launch / mean launch time",
+                          "7188x16384x2048, FFN-down 7188x2048x8192 (one of each); achieved = mean ops per launch / "
+                          "mean launch time",
             "per_gemm": per_gemm,
         },
         "roofline_stage0_conv": {
@@ -1016,7 +1018,7 @@ def main():
     with torch.inference_mode():
         ceiling = mfma_ceiling(torch, hip, runtime, clip)
     ceiling["conv_frac_of_ceiling"] = round(achieved / ceiling["tops"], 4)
-    ceiling["gemm_k2048_frac_of_ceiling"] = round(gemm_achieved / ceiling["tops"], 4)
+    ceiling["gemm_frac_of_ceiling"] = round(gemm_achieved / ceiling["tops"], 4)
     result["mfma_ceiling"] = ceiling
     del runtime, clip, out
     torch.cuda.empty_cache()

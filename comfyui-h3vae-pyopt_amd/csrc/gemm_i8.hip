@@ -827,8 +827,18 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave >> 2, sw4 = wave & 3;
 
+    // Tiles of the partial last row block (when M % 256 != 0) take the last workgroup ids, so they form the
+    // final round of the launch, where their skipped MFMAs shorten the kernel; the full tiles are mapped as
+    // in the other GEMMs (per-XCD contiguous ranges, grouped by 8 row blocks).
     int tm, tn;
-    grouped_tile(xcd_remap(blockIdx.x, gridDim.x), p.tiles_m, p.tiles_n, 8, tm, tn);
+    const int ntail = p.M % BM ? p.tiles_n : 0;
+    const int nfull = p.tiles_m * p.tiles_n - ntail;
+    if ((int)blockIdx.x < nfull) {
+        grouped_tile(xcd_remap(blockIdx.x, nfull), p.tiles_m - (ntail ? 1 : 0), p.tiles_n, 8, tm, tn);
+    } else {
+        tm = p.tiles_m - 1;
+        tn = blockIdx.x - nfull;
+    }
     const int m0 = tm * BM, n0 = tn * BN;
     const int nk = p.K / BK;
 
@@ -866,6 +876,12 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
 
+    // 32-row accumulator blocks of this wave that hold rows below M (4 except in the last row of tiles: the
+    // H3 decoder's M = 7188 leaves 20 rows in it); the MFMAs of the others are skipped, so a tail tile costs a
+    // fraction of a full one
+    const int vrows = p.M - m0 - grp * 128;
+    const int vblk = __builtin_amdgcn_readfirstlane(vrows >= 128 ? 4 : (vrows <= 0 ? 0 : (vrows + 31) / 32));
+
     // fragments of one K step: lane reads row (lane & 31) of a 32-row block, k-chunk (lane >> 5) + 2 ks
     const int frow = lane & 31, fhi = lane >> 5;
     v4i fa[4][4], fb[4][2];   // [ks][block]
@@ -887,16 +903,19 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
             }
         }
     };
-    auto mfma_step = [&]() {
+    auto mfma_blocks = [&](auto nb) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < decltype(nb)::value; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fb[ks][j], fa[ks][i], acc[i][j], 0, 0, 0);
     };
 
+    // the K loop for NB valid accumulator blocks (one instantiation per count, so no branch sits between the
+    // MFMAs of a phase)
+    auto kloop = [&](auto nb) {
     // prologue: weights 0, 1 by group 0; activations 0, 1, 2 by group 1; stage 0 lands before the first barrier
     if (grp == 0) {
         issue(0);
@@ -925,7 +944,7 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
         // MFMA phase of step k
-        mfma_step();
+        mfma_blocks(nb);
         __builtin_amdgcn_sched_barrier(0);
         if (grp == 0) {
             if (k + 1 < nk) wait_vmcnt<0>();          // weights of step k + 1
@@ -935,6 +954,12 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    };
+    if (vblk == 4) kloop(std::integral_constant<int, 4>{});
+    else if (vblk == 3) kloop(std::integral_constant<int, 3>{});
+    else if (vblk == 2) kloop(std::integral_constant<int, 2>{});
+    else if (vblk == 1) kloop(std::integral_constant<int, 1>{});
+    else kloop(std::integral_constant<int, 0>{});
 
     // epilogue: lane holds rows m0 + 128 grp + 32 i + (lane & 31) and, in register r of block j, column
     // n0 + 64 s + 32 j + (r / 4) * 8 + (lane >> 5) * 4 + r % 4
@@ -1110,7 +1135,6 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int WM = BM / WGM, WN = BN / WGN;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int RO = BM / TW;                               // output rows per tile
-    constexpr int NCB = WO / TW;                              // column blocks per output row
     constexpr int HR = RO + 2;                                // window rows
     constexpr int HPL = halo_hpl(TW, SP);                     // LDS pixels per window row
     constexpr int ROWB = HPL * 32;                            // LDS bytes per window row
@@ -1131,16 +1155,18 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
     const int wm = wave / WGN, wn = wave % WGN;
 
-    // tile -> (row block, column block, frame, weight tile); the weight tiles of one window are
-    // adjacent, then the frames of one row and column block (they share input rows in L2)
+    // tile -> (column block, row block, frame, weight tile); the weight tiles of one window are
+    // adjacent, then the frames of one row and column block (they share input frames in L2), then the
+    // row blocks of one column block (consecutive row blocks share two window rows)
     int id = xcd_remap(blockIdx.x, gridDim.x);
     const int tn = id % p.tiles_n;
     id /= p.tiles_n;
     const int nfr = p.M / (p.Ho * WO);                        // batch * Do
     const int fr = id % nfr;
     id /= nfr;
-    const int cb = id % NCB;
-    const int rb = id / NCB;
+    const int nrb = p.Ho / RO;
+    const int rb = id % nrb;
+    const int cb = id / nrb;
     const int od = fr % p.Do;
     const int bi = fr / p.Do;
     const int oh0 = rb * RO;
