@@ -20,7 +20,7 @@ import torch
 
 LIB_NAME = "libh3vae_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 2
+ABI_VERSION = 3
 EINVAL = 1
 
 _P = ctypes.c_void_p

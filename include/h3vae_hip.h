@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define H3V_ABI_VERSION 2
+#define H3V_ABI_VERSION 3
 
 #define H3V_OK 0
 #define H3V_EINVAL 1   /* shape / dtype / alignment / contract violation */
