@@ -20,7 +20,7 @@ import torch
 
 LIB_NAME = "libh3vae_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 3
+ABI_VERSION = 4
 EINVAL = 1
 
 _P = ctypes.c_void_p
@@ -37,11 +37,13 @@ SIGNATURES: dict[str, list] = {
     "h3v_gemm_i8_i32": [_P, _P, _P, _I64, _I64, _I64, _P],
     "h3v_conv3d_i8_residual": [_P] * 7 + [_I] * 13 + [_P],
     "h3v_conv3d_i8_residual_padded": [_P] * 8 + [_I] * 12 + [_P],
+    "h3v_conv3d_i8_gn": [_P] * 7 + [_I] * 6 + [_P, _P, _P],
     "h3v_conv3d_i8": [_P, _P, _P, _P, _P, _P] + [_I] * 13 + [_P],
     "h3v_conv3d_i8_i32": [_P, _P, _P] + [_I] * 13 + [_P],
     "h3v_tensor_quant_i8": [_P, _I64, _P, _P, _P, _I64, _P],
     "h3v_gn_norm_pack_i8": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "h3v_gn_norm_pack_i8_noalloc": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P],
+    "h3v_gn_norm_pack_i8_partials": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "h3v_residual_norm1_quant": [_P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P, _P],
     "h3v_residual_rms_quant": [_P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P, _P],
     "h3v_rms_fp16": [_P, _P, _F, _I64, _I64, _P, _P],

@@ -72,6 +72,13 @@ struct GemmParams {
     uint32_t a_bytes;  // extents of A and W in bytes (buffer resource ranges, < 4 GiB)
     uint32_t b_bytes;
     int k_splits;      // tiled kernels: K blocks split evenly over gridDim.y = k_splits workgroups (0 or 1: none)
+    // statistics epilogue of the window conv (h3v_conv3d_i8_gn; null gn_avg: off): the GroupNorm(32)
+    // partial statistics of each 512-pixel output tile, in the producer workspace layout (GnWorkspace)
+    float* gn_avg;
+    float* gn_m2;
+    uint32_t* gn_ext;
+    const uint16_t* gn_bias;   // fp16 per output channel, nullable: statistics of fp16(out + gn_bias)
+    int gn_nchunk;             // tiles per output frame
 };
 
 // Buffer resource word 3 for raw byte addressing (no swizzle, 32-bit format).
@@ -488,6 +495,153 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 }
             }
         };
+        // Statistics epilogue (window conv, whole 512 x 128 tiles of one frame, batch one): the stores of
+        // the plain path, then the GroupNorm(32) partial statistics of the tile as the encoder producer's
+        // statistics pass would form them for a 512-pixel chunk, on the stored values (with the residual)
+        // plus gn_bias (fp16 sum, one rounding).  Thread tid keeps tile columns 8 (tid % 16) .. + 7 of
+        // tile pixels pl + 32 s (pl = tid / 16, s = 0 .. 15, tile pixel = tile row * TILEW + column):
+        // per pixel a group's channels are summed left to right and added to the thread's running sum;
+        // the 32 pixel lanes combine as the adjacent tree (pl, pl + 1), then pairs of pairs, ..., whose
+        // first two levels are the shuffles to lanes ^ 16 and ^ 32 and the last three the sum over the
+        // eight waves ((w0 + w1) + (w2 + w3)) + ((w4 + w5) + (w6 + w7)).  avg = sum / (512 cg); M2 is
+        // the same sum of (v - avg)^2 per channel.  Max and min per channel are exact in any order.
+        if constexpr (EP == Epi::Dequant && SROWS && TILEW > 0 && PADWO == 0) {
+            if (p.gn_avg != nullptr) {
+                static_assert(BM == 512 && RCH == 16 && NW == 8 && LDS_BYTES >= BM * OUTW * 2 + 9472,
+                              "statistics epilogue: 512 x 128 tiles of 8 waves, 9.25 KB of LDS past the tile");
+                constexpr int NT = NW * 64, PER = BM * RCH / NT;
+                const int ch = tid & 15;
+                const int gcol = gcol0 + ch * 8;
+                float* const gred = reinterpret_cast<float*>(smem + BM * OUTW * 2);   // [wave][32]
+                float* const gavg = gred + NW * 32;                                     // [32]
+                // per wave and channel the (max, min) pair as two floats: the values are fp16, but kept as
+                // fp32 here, since the compiler narrows a maximum of fp16 values to v_max3_f16 and then packs
+                // two such results with a v_or_b32 that assumes the upper half of the register is zero,
+                // which v_max3_f16 on gfx950 does not clear (the packed minima came out corrupted)
+                float* const gext = gavg + 32;                                           // [wave][128][2]
+                u16x8 v[PER];
+                if (p.res != nullptr) {
+#pragma unroll
+                    for (int k = 0; k < PER; ++k)
+                        v[k] = *reinterpret_cast<const u16x8*>(p.res + (int64_t)gidx((tid >> 4) + 32 * k) * p.ldo + gcol);
+                }
+                u16x8 gb{};
+                if (p.gn_bias) gb = *reinterpret_cast<const u16x8*>(p.gn_bias + gcol);
+                lds_barrier();   // the output tile is complete in LDS
+#pragma unroll
+                for (int k = 0; k < PER; ++k) {
+                    const int r = (tid >> 4) + 32 * k;
+                    u16x8 y = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
+                    if (p.res != nullptr) y = add_f16x8(v[k], y);   // fp16(res + y), one rounding
+                    *reinterpret_cast<u16x8*>(out + (int64_t)gidx(r) * p.ldo + gcol) = y;
+                    v[k] = p.gn_bias ? add_f16x8(y, gb) : y;
+                }
+                const int fpix = p.Ho * p.Wo;
+                const int fr = m0 / fpix, rem = m0 - fr * fpix;
+                const int oh0 = rem / p.Wo, owb = rem - oh0 * p.Wo;
+                const int chunk = (oh0 / (BM / TILEW)) * (p.Wo / TILEW) + owb / TILEW;
+                const int64_t cbase = (int64_t)fr * kGnGroups * p.gn_nchunk + chunk;   // + group * nchunk
+                auto stats = [&](auto cg_c) {
+                    constexpr int CG = decltype(cg_c)::value;
+                    constexpr int GPT = 8 / CG, NG = 128 / CG;
+                    float ls[GPT], vmx[8], vmn[8];
+#pragma unroll
+                    for (int gi = 0; gi < GPT; ++gi) ls[gi] = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) { vmx[e] = -__builtin_inff(); vmn[e] = __builtin_inff(); }
+#pragma unroll
+                    for (int k = 0; k < PER; ++k) {
+                        float f[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            f[e] = h2f(v[k][e]);
+                            vmx[e] = __builtin_fmaxf(vmx[e], f[e]);
+                            vmn[e] = __builtin_fminf(vmn[e], f[e]);
+                        }
+#pragma unroll
+                        for (int gi = 0; gi < GPT; ++gi) {
+                            float ps = f[gi * CG];
+#pragma unroll
+                            for (int i = 1; i < CG; ++i) ps = ps + f[gi * CG + i];
+                            ls[gi] = ls[gi] + ps;
+                        }
+                    }
+                    // the tree over the 32 pixel lanes; lanes 0-15 of each wave hold its part
+                    auto lane_tree = [&](float (&x)[GPT]) {
+#pragma unroll
+                        for (int gi = 0; gi < GPT; ++gi) {
+                            x[gi] = x[gi] + __shfl_xor(x[gi], 16, 64);
+                            x[gi] = x[gi] + __shfl_xor(x[gi], 32, 64);
+                        }
+                        if (lane < 16) {
+#pragma unroll
+                            for (int gi = 0; gi < GPT; ++gi) gred[wave * 32 + ch * GPT + gi] = x[gi];
+                        }
+                    };
+                    auto wave_tree = [&](int g) {
+                        const float* r = gred + g;
+                        return ((r[0] + r[32]) + (r[64] + r[96])) + ((r[128] + r[160]) + (r[192] + r[224]));
+                    };
+                    lane_tree(ls);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        vmx[e] = __builtin_fmaxf(vmx[e], __shfl_xor(vmx[e], 16, 64));
+                        vmx[e] = __builtin_fmaxf(vmx[e], __shfl_xor(vmx[e], 32, 64));
+                        vmn[e] = __builtin_fminf(vmn[e], __shfl_xor(vmn[e], 16, 64));
+                        vmn[e] = __builtin_fminf(vmn[e], __shfl_xor(vmn[e], 32, 64));
+                    }
+                    if (lane < 16) {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            gext[2 * (wave * 128 + ch * 8 + e)] = vmx[e];
+                            gext[2 * (wave * 128 + ch * 8 + e) + 1] = vmn[e];
+                        }
+                    }
+                    lds_barrier();
+                    if (tid < NG) gavg[tid] = wave_tree(tid) / (float)(BM * CG);
+                    if (tid >= 256 && tid < 384) {
+                        const int c = tid - 256;
+                        float mx = gext[2 * c], mn = gext[2 * c + 1];
+#pragma unroll
+                        for (int w = 1; w < NW; ++w) {
+                            mx = __builtin_fmaxf(mx, gext[2 * (w * 128 + c)]);
+                            mn = __builtin_fminf(mn, gext[2 * (w * 128 + c) + 1]);
+                        }
+                        // the extremes are stored values: exact as fp16
+                        p.gn_ext[((int64_t)fr * p.gn_nchunk + chunk) * p.N + n0 + c] =
+                            (uint32_t)f2h(mx) | ((uint32_t)f2h(mn) << 16);
+                    }
+                    lds_barrier();
+                    float a[GPT], lm[GPT];
+#pragma unroll
+                    for (int gi = 0; gi < GPT; ++gi) { a[gi] = gavg[ch * GPT + gi]; lm[gi] = 0.0f; }
+#pragma unroll
+                    for (int k = 0; k < PER; ++k) {
+#pragma unroll
+                        for (int gi = 0; gi < GPT; ++gi) {
+                            float dv = h2f(v[k][gi * CG]) - a[gi];
+                            float pm = dv * dv;
+#pragma unroll
+                            for (int i = 1; i < CG; ++i) {
+                                dv = h2f(v[k][gi * CG + i]) - a[gi];
+                                pm = pm + dv * dv;
+                            }
+                            lm[gi] = lm[gi] + pm;
+                        }
+                    }
+                    lane_tree(lm);
+                    lds_barrier();
+                    if (tid < NG) {
+                        const int64_t dst = cbase + (int64_t)(n0 / CG + tid) * p.gn_nchunk;
+                        p.gn_avg[dst] = gavg[tid];
+                        p.gn_m2[dst] = wave_tree(tid);
+                    }
+                };
+                if (p.N == 128) stats(std::integral_constant<int, 4>{});
+                else stats(std::integral_constant<int, 8>{});
+                return;
+            }
+        }
         if (p.res == nullptr) {
             lds_barrier();   // the output tile is complete in LDS
 #pragma unroll 4
@@ -1054,11 +1208,12 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
 constexpr int halo_hpl(int tw, bool sp) { return sp ? (tw + 2 + 7) / 8 * 8 : (tw + 2 + 15) / 16 * 16; }
 
 // LDS of conv3_halo_i8 with TW-pixel tile rows: two stages of window + weights, or the fp16 output
-// tile if larger.
+// tile if larger; the strided-pixel variant adds the statistics epilogue's reduction space.
+constexpr int kGnLdsBytes = 12288;
 constexpr int halo_lds_bytes(int tw, bool sp) {
     const int hb = ((512 / tw + 2) * halo_hpl(tw, sp) * 32 + 4095) / 4096 * 4096;
     const int ring = 2 * (hb + 9 * 128 * 32);
-    return ring > 512 * 128 * 2 ? ring : 512 * 128 * 2;
+    return (ring > 512 * 128 * 2 ? ring : 512 * 128 * 2) + (sp ? kGnLdsBytes : 0);
 }
 
 // Compile-time loop: f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}).
@@ -1142,7 +1297,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     constexpr int WB = 9 * BN * 32;                           // weight bytes of a stage
     constexpr int STAGE = HB + WB;
     constexpr int NH = HB / 1024 / NWD, NWT = WB / 1024 / NWD; // DMA instructions per issuing wave and stage
-    constexpr int LDS = 2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2;
+    constexpr int LDS = (2 * STAGE > BM * BN * 2 ? 2 * STAGE : BM * BN * 2) + (SP ? kGnLdsBytes : 0);
     static_assert(WO == 32 || WO == 64 || WO == 128 || WO == 256, "output width");
     static_assert(LDS <= 163840, "LDS");
     static_assert(LDS == halo_lds_bytes(TW, SP), "host and kernel LDS sizes");
@@ -1639,6 +1794,7 @@ int launch_halo(GemmParams p, hipStream_t stream, const char* what) {
     constexpr int lds = halo_lds_bytes(WO, false), lds_sp = halo_lds_bytes(kTw, true);
     static_assert(lds <= 163840 && lds_sp <= 163840, "LDS exceeds 160 KB");
     const bool sp = kSp && (p.C * ES) % 128 == 0 && p.Ho % (512 / kTw) == 0;   // whole 8-row tiles of the column blocks
+    if (p.gn_avg && !sp) return fail(H3V_EINVAL, "%s: the statistics epilogue needs the strided-pixel kernel", what);
     auto kernel = sp ? &conv3_halo_i8<WO, EP, ES, PAD, kSp, kTw> : &conv3_halo_i8<WO, EP, ES, PAD, false>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv3_halo_i8<WO, EP, ES, PAD, false>),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds);
@@ -1834,6 +1990,34 @@ int h3v_conv3d_i8_residual(const int8_t* qx, const float* x_scale, const int8_t*
     p.res = residual;
     p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
     return run_conv<Epi::Dequant>(p, stream, what);
+}
+
+int h3v_conv3d_i8_gn(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                     const uint16_t* bias, const uint16_t* residual, uint16_t* out, int cin, int d, int h, int w,
+                     int cout, int causal_skip, const uint16_t* gn_bias, float* workspace, hipStream_t stream) {
+    const char* what = "h3v_conv3d_i8_gn";
+    H3V_REQUIRE(qx && x_scale && qw && w_scale && out && workspace, "%s: null pointer argument", what);
+    H3V_REQUIRE(residual != out, "%s: the residual must not alias the output", what);
+    GemmParams p{};
+    int rc = fill_conv(p, what, 1, cin, d, h, w, cout, 3, 3, 3, 1, 1, 1);
+    if (rc) return rc;
+    p.a = qx; p.b = qw; p.sx = x_scale; p.sx_stride = 0; p.sw = w_scale; p.bias = bias; p.out = out;
+    p.res = residual;
+    p.causal_skip = causal_skip ? 1 : 0;
+    H3V_REQUIRE(halo_conv_fits(p) && cin % 128 == 0 && (cout == 128 || cout == 256) && (p.Wo == 128 || p.Wo == 256) &&
+                    p.Ho % 8 == 0,
+                "%s: needs Cin %% 128 == 0, Cout 128 or 256, output width 128 or 256 and output height a multiple of 8 "
+                "(got Cin %d, Cout %d, output %d x %d)", what, cin, cout, p.Ho, p.Wo);
+    H3V_REQUIRE(aligned(out, 16) && (!residual || aligned(residual, 16)) && (!gn_bias || aligned(gn_bias, 16)) &&
+                    aligned(workspace, 16),
+                "%s: out, residual, gn_bias and workspace need 16-byte alignment", what);
+    const GnWorkspace g = gn_workspace(workspace, p.Do, p.Ho * p.Wo, kGnTileChunk);
+    p.gn_avg = g.avg;
+    p.gn_m2 = g.m2;
+    p.gn_ext = g.ext;
+    p.gn_bias = gn_bias;
+    p.gn_nchunk = g.nchunk;
+    return p.Wo == 256 ? launch_halo<256, Epi::Dequant>(p, stream, what) : launch_halo<128, Epi::Dequant>(p, stream, what);
 }
 
 int h3v_conv3d_i8_residual_padded(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,

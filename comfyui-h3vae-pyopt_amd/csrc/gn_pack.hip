@@ -79,8 +79,7 @@ __device__ __forceinline__ void load8(const uint16_t* p, float* v) {
 template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
                                                   int hw, int nchunk, float* __restrict__ part_avg,
-                                                  float* __restrict__ part_m2, uint32_t* __restrict__ ext,
-                                                  uint32_t* __restrict__ done) {
+                                                  float* __restrict__ part_m2, uint32_t* __restrict__ ext) {
     constexpr int CG = C / kGroups;
     constexpr int TPP = C / 8;
     constexpr int PL = kNT / TPP;
@@ -160,10 +159,6 @@ __global__ __launch_bounds__(kNT) void gn_partial(const uint16_t* __restrict__ x
         }
         // the extremes are input values (fp16, or fp16-rounded with the pre-bias): exact as fp16
         ext[((int64_t)t * nchunk + j) * C + tid] = (uint32_t)f2h(a) | ((uint32_t)f2h(b) << 16);
-    }
-    if (j == 0 && t == 0 && tid == 0) {   // for absmax_lut, which runs after this kernel
-        done[0] = 0u;
-        done[1] = 0u;
     }
     __syncthreads();
 
@@ -305,12 +300,17 @@ __device__ void gn_merge_group(const float* __restrict__ pa, const float* __rest
 __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_avg, const float* __restrict__ part_m2,
                                                const uint32_t* __restrict__ ext,
                                                const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ beta,
-                                               int hw, int nchunk, int c, float eps, float* __restrict__ stats,
-                                               uint32_t* __restrict__ cands) {
+                                               int hw, int nchunk, int chunk, int c, float eps,
+                                               float* __restrict__ stats, uint32_t* __restrict__ cands,
+                                               uint32_t* __restrict__ done) {
     __shared__ float sa[kMergeBatch];
     __shared__ float sm[kMergeBatch];
     __shared__ float ms[2];
     const int g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    if (g == 0 && t == 0 && tid == 0) {   // absmax_lut's counters (it runs after this kernel)
+        done[0] = 0u;
+        done[1] = 0u;
+    }
     const int cg = c / kGroups;
     const float* pa = part_avg + ((int64_t)t * kGroups + g) * nchunk;
     const float* pm = part_m2 + ((int64_t)t * kGroups + g) * nchunk;
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(64) void gn_merge(const float* __restrict__ part_av
     constexpr int kExtRegs = 64 * kMergeRegs / 8;             // chunks per lane at cg = 8
     const bool held = nchunk <= 64 * kMergeRegs;
     uint32_t ek[kExtRegs];
-    gn_merge_group(pa, pm, hw, nchunk, kChunk, cg, eps, sa, sm, ms, [&] {
+    gn_merge_group(pa, pm, hw, nchunk, chunk, cg, eps, sa, sm, ms, [&] {
         if (held) {
 #pragma unroll
             for (int r = 0; r < kExtRegs; ++r)   // a clamped index re-reads the last chunk: max / min unchanged
@@ -470,14 +470,9 @@ __global__ __launch_bounds__(kNT) void absmax_lut(const uint16_t* __restrict__ x
     if (last) build_lut_range(fin, lut, 0, 65536);
 }
 
-constexpr int kLutFloats = 65536 / 4;    // the int8 quantize table
+static_assert(kGnGroups == kGroups && kGnMaxC == kMaxC && kGnSizingChunk == kChunk, "producer workspace layout");
 
-int64_t workspace_floats(int d, int h, int w) {
-    int64_t nchunk = ((int64_t)h * w + kChunk - 1) / kChunk;
-    // (avg, M2) per chunk and group; per chunk and channel the packed fp16 (max, min); the quantize table;
-    // 64 floats whose first words are absmax_lut's counters; the absmax candidate of every (frame, group)
-    return 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC + kLutFloats + 64 + (int64_t)d * kGroups;
-}
+int64_t workspace_floats(int d, int h, int w) { return gn_workspace_floats(d, h, w); }
 
 // PASS 1 through the table.  Each block walks whole padded output rows
 // (frame, padded row): the source row follows from the row index alone, so the
@@ -561,34 +556,30 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
     }
 }
 
+// chunk = kChunk: the statistics pass runs here; chunk = kGnTileChunk: the workspace already holds the
+// partial statistics of 512-pixel tiles, written by the window conv that produced x (h3v_conv3d_i8_gn).
 template <int C, bool PB>
 void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta, float eps,
-                int d, int h, int w, int8_t* q, float* scale, float* stats, float* ws, uint32_t* amax_bits,
+                int d, int h, int w, int chunk, int8_t* q, float* scale, float* stats, float* ws, uint32_t* amax_bits,
                 hipStream_t stream) {
     const int hw = h * w;
-    const int nchunk = (hw + kChunk - 1) / kChunk;
-    float* part_avg = ws;
-    float* part_m2 = ws + (int64_t)d * nchunk * kGroups;
-    uint32_t* ext = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups);
-    int8_t* lut = reinterpret_cast<int8_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC);
-    uint32_t* done = reinterpret_cast<uint32_t*>(ws + 2 * (int64_t)d * nchunk * kGroups + (int64_t)d * nchunk * kMaxC +
-                                                 kLutFloats);
-    uint32_t* cands = done + 64;
-    // block (0, 0) zeroes absmax_lut's counters; gn_merge writes every candidate word
-    hipLaunchKernelGGL((gn_partial<C, PB>), dim3(nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, nchunk, part_avg,
-                       part_m2, ext, done);
-    hipLaunchKernelGGL(gn_merge, dim3(kGroups, d), dim3(64), 0, stream, part_avg, part_m2, ext, gamma, beta, hw,
-                       nchunk, C, eps, stats, cands);
+    const GnWorkspace g = gn_workspace(ws, d, hw, chunk);
+    if (chunk == kChunk)
+        hipLaunchKernelGGL((gn_partial<C, PB>), dim3(g.nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, g.nchunk,
+                           g.avg, g.m2, g.ext);
+    // block (0, 0) zeroes absmax_lut's counters; every candidate word is written
+    hipLaunchKernelGGL(gn_merge, dim3(kGroups, d), dim3(64), 0, stream, g.avg, g.m2, g.ext, gamma, beta, hw,
+                       g.nchunk, chunk, C, eps, stats, g.cands, g.done);
     const int64_t nvec = (int64_t)(d + 2) * (h + 2) * (w + 2) * (C / 8);
     int64_t want = (nvec + kNT - 1) / kNT;
     // grid-strided full pass (rarely run) with at least one block per 256 table entries
     unsigned blocks = (unsigned)(want > 1024 ? 1024 : (want < 256 ? 256 : want));
     hipLaunchKernelGGL((absmax_lut<C, PB>), dim3(blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats, d, h,
-                       w, cands, amax_bits, done, lut);
+                       w, g.cands, amax_bits, g.done, g.lut);
     // 64 KB of LDS per block: two blocks per CU; each block walks many vectors
     unsigned lut_blocks = (unsigned)(want > 512 ? 512 : want);
     hipLaunchKernelGGL((norm_pack_lut<C, PB>), dim3(lut_blocks), dim3(kNT), 0, stream, x, pre_bias, gamma, beta, stats,
-                       d, h, w, amax_bits, lut, q, scale);
+                       d, h, w, amax_bits, g.lut, q, scale);
 }
 
 // ---------------------------------------------------------------------------
@@ -810,7 +801,7 @@ void launch_f16(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
 // ---------------------------------------------------------------------------
 // Checks and launch shared by h3v_gn_norm_pack_i8 and its no-allocation variant.
 int run_norm_pack_i8(const char* what, const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
-                     const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
+                     const uint16_t* beta, float eps, int c, int d, int h, int w, int chunk, int8_t* q, float* scale,
                      float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
     H3V_REQUIRE(x && gamma && beta && q && scale && stats, "%s: null pointer argument", what);
     H3V_REQUIRE(c == 128 || c == 256, "%s: C must be 128 or 256 (got %d)", what, c);
@@ -822,11 +813,11 @@ int run_norm_pack_i8(const char* what, const uint16_t* x, const uint16_t* pre_bi
                     aligned(q, 8),
                 "%s: x, gamma, beta, pre_bias need 16-byte and q 8-byte alignment", what);
     if (c == 128) {
-        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
-        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
     } else {
-        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
-        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, q, scale, stats, workspace, amax_scratch, stream);
+        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
     }
     return launch_status(what);
 }
@@ -871,8 +862,21 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
     const char* what = "h3v_gn_norm_pack_i8";
     H3V_REQUIRE(workspace && amax_scratch, "%s: null pointer argument", what);
     H3V_REQUIRE(aligned(workspace, 16), "%s: workspace needs 16-byte alignment", what);
-    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, q, scale, stats, workspace, amax_scratch,
-                            stream);
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kChunk, q, scale, stats, workspace,
+                            amax_scratch, stream);
+}
+
+int h3v_gn_norm_pack_i8_partials(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
+                                 const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
+                                 float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
+    const char* what = "h3v_gn_norm_pack_i8_partials";
+    H3V_REQUIRE(workspace && amax_scratch, "%s: null pointer argument", what);
+    H3V_REQUIRE(aligned(workspace, 16), "%s: workspace needs 16-byte alignment", what);
+    H3V_REQUIRE(h >= 8 && ((int64_t)h * w) % kGnTileChunk == 0,
+                "%s: the partial statistics are those of %d-pixel conv tiles: H * W must be a multiple of %d and "
+                "H at least 8 (got %d x %d)", what, kGnTileChunk, kGnTileChunk, h, w);
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kGnTileChunk, q, scale, stats, workspace,
+                            amax_scratch, stream);
 }
 
 int h3v_gn_norm_pack_i8_noalloc(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
@@ -889,7 +893,7 @@ int h3v_gn_norm_pack_i8_noalloc(const uint16_t* x, const uint16_t* pre_bias, con
     const int rc = scratch_for_current_device(what, &base);
     if (rc != H3V_OK) return rc;
     // word 0: the absmax key; the workspace starts 256 bytes in (16-byte alignment kept)
-    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, q, scale, stats,
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kChunk, q, scale, stats,
                             base + kScratchHeadFloats, reinterpret_cast<uint32_t*>(base), stream);
 }
 

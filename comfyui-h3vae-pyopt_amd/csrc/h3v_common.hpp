@@ -198,4 +198,48 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Workspace of the INT8 encoder producer (h3v_gn_norm_pack_i8) for an fp16 [D, H, W, C] input whose
+// GroupNorm(32) statistics are summed over chunks of `chunk` pixels of a frame: the average and M2 of
+// every (frame, group, chunk) ([D][32][nchunk] each), the packed fp16 (max, min) of every (frame, chunk,
+// channel) ([D][nchunk][C], with room for C = 256), the int8 quantize table (64 KB), 64 words whose first
+// two are absmax_lut's counters, and the absmax candidate of every (frame, group).  The producer's own
+// statistics pass uses 256-pixel chunks, which sizes the workspace (h3v_gn_norm_pack_workspace_floats);
+// the window conv's statistics epilogue uses its 512-pixel tiles, whose layout fits inside.
+constexpr int kGnGroups = 32;
+constexpr int kGnMaxC = 256;
+constexpr int kGnSizingChunk = 256;
+constexpr int kGnTileChunk = 512;   // pixels of a window-conv output tile (8 rows of a 64-pixel column block)
+constexpr int kGnLutFloats = 65536 / 4;
+
+struct GnWorkspace {
+    float* avg;
+    float* m2;
+    uint32_t* ext;
+    int8_t* lut;
+    uint32_t* done;
+    uint32_t* cands;
+    int nchunk;
+};
+
+__host__ __device__ inline GnWorkspace gn_workspace(float* ws, int d, int hw, int chunk) {
+    GnWorkspace g;
+    g.nchunk = (hw + chunk - 1) / chunk;
+    const int64_t stat = (int64_t)d * g.nchunk * kGnGroups;
+    g.avg = ws;
+    g.m2 = ws + stat;
+    g.ext = reinterpret_cast<uint32_t*>(ws + 2 * stat);
+    float* const tail = ws + 2 * stat + (int64_t)d * g.nchunk * kGnMaxC;
+    g.lut = reinterpret_cast<int8_t*>(tail);
+    g.done = reinterpret_cast<uint32_t*>(tail + kGnLutFloats);
+    g.cands = g.done + 64;
+    return g;
+}
+
+// floats of the producer workspace for [D, H, W] (the 256-pixel layout, the larger one)
+inline int64_t gn_workspace_floats(int d, int h, int w) {
+    const int64_t nchunk = ((int64_t)h * w + kGnSizingChunk - 1) / kGnSizingChunk;
+    return 2 * (int64_t)d * nchunk * kGnGroups + (int64_t)d * nchunk * kGnMaxC + kGnLutFloats + 64 +
+           (int64_t)d * kGnGroups;
+}
+
 }  // namespace h3v

@@ -173,21 +173,33 @@ class BiasFusedResidualBlock(torch.nn.Module):
         kernel of this package (bit-identical to the separate fp16 add of the reference, :141)."""
         if zq is not None:
             raise ValueError("Unconditional inference only")
+        return self.forward_partials(x)[0]
+
+    def forward_partials(self, x, x_partials=None):
+        """``(forward(x), partials)``.  In INT8 mode the first conv writes the GroupNorm tile statistics of
+        its output (plus the first bias, the second norm's pre-bias) for the second norm, and the second
+        conv those of the block's output for the norm that reads it next (the next block's first norm),
+        returned as ``partials``; None where the convs' geometry has no statistics epilogue or the block
+        writes the padded form.  ``x_partials``: the statistics of ``x`` that the previous block's second
+        conv wrote (no bias), read by the first norm instead of its own statistics pass."""
         residual = self.shortcut_conv(x) if self.shortcut_conv is not None else x
         if self.int8_first is not None and self.int8_first.fuse_norm:
-            h = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
+            h, hp = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps,
+                                                 x_partials=x_partials, emit_partials=True,
+                                                 partials_bias=self.first.bias)
             form = self._padded_form(residual)
             if form is not None:
                 from .encoder_fp16_conv import tag_padded_input
                 padded = self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias,
                                                        self.second.eps, pre_bias=self.first.bias, residual=residual,
-                                                       pad_front=form[0], pad_border=form[1])
-                return tag_padded_input(padded, *form)
+                                                       pad_front=form[0], pad_border=form[1], x_partials=hp)
+                return tag_padded_input(padded, *form), None
             return self.int8_second.forward_norm(h, self.second.norm_weight, self.second.norm_bias, self.second.eps,
-                                                 pre_bias=self.first.bias, residual=residual)
+                                                 pre_bias=self.first.bias, residual=residual, x_partials=hp,
+                                                 emit_partials=True)
         if self.int8_first is None:
             h = self.first.conv(self.first(x), with_bias=False, causal_skip=True)
             second_input = bias_temporal_norm_pack(h, self.first.bias, self.second.norm_weight,
                                                    self.second.norm_bias, self.second.eps)
-            return self.second.conv(second_input, causal_skip=True, residual=residual)
-        return residual + self._residual_body(x, self.second.bias)
+            return self.second.conv(second_input, causal_skip=True, residual=residual), None
+        return residual + self._residual_body(x, self.second.bias), None

@@ -70,6 +70,11 @@ class ResidualDownsampleBlock(BiasFusedResidualBlock):
     def forward(self, x, zq=None):
         if zq is not None:
             raise ValueError("Unconditional inference only")
+        return self.forward_partials(x)[0]
+
+    def forward_partials(self, x, x_partials=None):
+        """``(forward(x), None)``; ``x_partials`` as in ``BiasFusedResidualBlock.forward_partials`` (read by the
+        first norm in INT8 mode).  The first conv hands its tile statistics to the second norm."""
         if self.int8_first is not None and self.int8_first.fuse_norm and self.int8_second.fuse_norm:
             from .encoder_int8 import padded_output_fits
             h, w = x.shape[3:]
@@ -77,13 +82,15 @@ class ResidualDownsampleBlock(BiasFusedResidualBlock):
                 # The second conv writes the pack's output itself: fp16(x + (conv + second.bias)) into the
                 # downsample's padded input (two zero frames, bottom / right reflect); bit-identical to the
                 # conv followed by residual_downsample_pack, without re-reading the conv output.
-                h1 = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias, self.first.eps)
+                h1, hp = self.int8_first.forward_norm(x, self.first.norm_weight, self.first.norm_bias,
+                                                      self.first.eps, x_partials=x_partials, emit_partials=True,
+                                                      partials_bias=self.first.bias)
                 padded = self.int8_second.forward_norm(h1, self.second.norm_weight, self.second.norm_bias,
                                                        self.second.eps, pre_bias=self.first.bias, residual=x,
                                                        residual_bias=self.second.bias, pad_front=2,
-                                                       pad_border=(0, 1, 0, 1))
-                return self.down(padded)
+                                                       pad_border=(0, 1, 0, 1), x_partials=hp)
+                return self.down(padded), None
         # second.bias is added by the pack, not by the second convolution
         h = self._residual_body(x, None)
         h = residual_downsample_pack(h, x, self.second.bias)
-        return self.down(h)
+        return self.down(h), None

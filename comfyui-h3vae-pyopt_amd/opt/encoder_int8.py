@@ -182,12 +182,16 @@ def int8_valid_conv3d(x, qweight, weight_scale, *, config: Int8Conv3DConfig, bia
 
 
 def _conv3d_from_quantized(qx, activation_scale, qweight, weight_scale, *, config: Int8Conv3DConfig, bias,
-                           tile_variant: str, causal_prefix_zero: bool = False, residual=None):
+                           tile_variant: str, causal_prefix_zero: bool = False, residual=None, gn_workspace=None,
+                           gn_bias=None):
     """The implicit-GEMM conv of an int8 NDHWC input.
 
     ``causal_prefix_zero`` may be set only by a producer that writes exactly two zero leading frames:
     the taps it skips multiply those zeros, so the result equals the full reduction.  ``residual``
-    (fp16, the output's shape) is added in the epilogue as a following fp16 ``residual + out`` would."""
+    (fp16, the output's shape) is added in the epilogue as a following fp16 ``residual + out`` would.
+    ``gn_workspace`` (fp32, ``gn_workspace_floats`` of the output's D, H, W; geometry of ``gn_stats_fits``):
+    the conv also writes the GroupNorm(32) tile statistics of its output (plus ``gn_bias``, fp16 per
+    output channel, when given) for ``quantized_temporal_norm_pad(..., partials=gn_workspace)``."""
     if tile_variant not in _TILE_VARIANTS:
         raise ValueError(f"unknown tile variant {tile_variant!r}")
     _hip.require_gfx950(qx.device, "INT8 implicit conv")
@@ -196,14 +200,53 @@ def _conv3d_from_quantized(qx, activation_scale, qweight, weight_scale, *, confi
     out = torch.empty(out_shape, dtype=torch.float16, device=qx.device, memory_format=_CL3D)
     geometry = (*qx.shape, config.out_channels, *config.kernel_size, *config.stride, int(bool(causal_prefix_zero)))
     head = (_hip.ptr(qx), _hip.ptr(activation_scale), _hip.ptr(qweight), _hip.ptr(weight_scale), _hip.ptr(bias))
+    if residual is not None:
+        if tuple(residual.shape) != out_shape or residual.dtype != torch.float16 or residual.device != out.device:
+            raise ValueError("residual must be an fp16 tensor of the convolution output's shape on its device")
+        residual = residual.contiguous(memory_format=_CL3D)
+    if gn_workspace is not None:
+        b, c, d, h, w = qx.shape
+        if (config.kernel_size != (3, 3, 3) or config.stride != (1, 1, 1)
+                or not gn_stats_fits(c, config.out_channels, *out_shape[2:], batch=b)):
+            raise ValueError(f"the statistics epilogue does not take this conv: input {tuple(qx.shape)}, output "
+                             f"{out_shape}, kernel {config.kernel_size}, stride {config.stride}")
+        need = gn_workspace_floats(*out_shape[2:])
+        if (gn_workspace.dtype != torch.float32 or gn_workspace.device != out.device
+                or not gn_workspace.is_contiguous() or gn_workspace.numel() < need):
+            raise ValueError(f"gn_workspace must be a contiguous fp32 tensor of at least {need} elements on the "
+                             "output's device")
+        if gn_bias is not None and (gn_bias.shape != (config.out_channels,) or gn_bias.dtype != torch.float16
+                                    or gn_bias.device != out.device):
+            raise ValueError("gn_bias must be an fp16 vector of the output channels on the output's device")
+        _hip.call("h3v_conv3d_i8_gn", *head, _hip.ptr(residual), _hip.ptr(out), c, d, h, w, config.out_channels,
+                  int(bool(causal_prefix_zero)), _hip.ptr(None if gn_bias is None else gn_bias.contiguous()),
+                  _hip.ptr(gn_workspace), _hip.stream(qx.device))
+        return out
+    if gn_bias is not None:
+        raise ValueError("gn_bias is only taken with gn_workspace")
     if residual is None:
         _hip.call("h3v_conv3d_i8", *head, _hip.ptr(out), *geometry, _hip.stream(qx.device))
         return out
-    if tuple(residual.shape) != out_shape or residual.dtype != torch.float16 or residual.device != out.device:
-        raise ValueError("residual must be an fp16 tensor of the convolution output's shape on its device")
-    residual = residual.contiguous(memory_format=_CL3D)
     _hip.call("h3v_conv3d_i8_residual", *head, _hip.ptr(residual), _hip.ptr(out), *geometry, _hip.stream(qx.device))
     return out
+
+
+def gn_stats_fits(in_channels: int, out_channels: int, out_d: int, out_h: int, out_w: int, *, batch: int = 1) -> bool:
+    """Whether ``h3v_conv3d_i8_gn`` takes a stride-1 3x3x3 conv of this geometry and whether it is the
+    kernel the plain conv would run anyway: the window conv's strided-pixel form (batch one, Cin % 128 == 0,
+    Cout 128 or 256, output width 128 or 256, output height a multiple of 8), at 128 or more 512 x 128
+    output tiles (fewer run as the implicit GEMM, which fills the GPU better)."""
+    tiles = out_d * (out_h * out_w // 512) * (out_channels // 128)
+    return (batch == 1 and in_channels % 128 == 0 and out_channels in (128, 256) and out_w in (128, 256)
+            and out_d >= 1 and out_h >= 8 and out_h % 8 == 0 and tiles >= 128)
+
+
+def gn_workspace_floats(d: int, h: int, w: int) -> int:
+    """fp32 elements of the INT8 producer's workspace for an fp16 [1, C, d, h, w] input."""
+    n = int(_hip.lib().h3v_gn_norm_pack_workspace_floats(int(d), int(h), int(w)))
+    if n <= 0:
+        raise ValueError(f"no producer workspace for [D, H, W] = [{d}, {h}, {w}]")
+    return n
 
 
 def padded_output_fits(in_channels: int, out_channels: int, out_h: int, out_w: int) -> bool:

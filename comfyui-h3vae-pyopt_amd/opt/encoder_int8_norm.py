@@ -28,8 +28,13 @@ def _validate(x, weight, bias, pre_bias):
             raise ValueError("Expected contiguous FP16 channel vectors on input device")
 
 
-def quantized_temporal_norm_pad(x, weight, bias, eps, *, pre_bias=None, return_stats=False):
-    """-> (q int8 [1, C, D+2, H+2, W+2] channels-last-3d, scale fp32 scalar)."""
+def quantized_temporal_norm_pad(x, weight, bias, eps, *, pre_bias=None, return_stats=False, partials=None):
+    """-> (q int8 [1, C, D+2, H+2, W+2] channels-last-3d, scale fp32 scalar).
+
+    ``partials``: the producer workspace that the INT8 window conv which wrote ``x`` filled with the
+    GroupNorm tile statistics of ``x`` (plus ``pre_bias``, which must be the bias that conv was given as
+    its statistics bias); the statistics pass is then skipped (``h3v_gn_norm_pack_i8_partials``).  The
+    workspace is reused for the rest of the call."""
     _validate(x, weight, bias, pre_bias)
     _hip.require_gfx950(x.device, "INT8 norm producer")
     _, c, d, h, w = x.shape
@@ -39,9 +44,17 @@ def quantized_temporal_norm_pad(x, weight, bias, eps, *, pre_bias=None, return_s
     scale = torch.empty((), device=x.device, dtype=torch.float32)
     stats = torch.empty((d, 32, 2), device=x.device, dtype=torch.float32)
     nws = int(_hip.lib().h3v_gn_norm_pack_workspace_floats(d, h, w))
-    workspace = torch.empty((nws,), device=x.device, dtype=torch.float32)
+    if partials is None:
+        workspace, entry = torch.empty((nws,), device=x.device, dtype=torch.float32), "h3v_gn_norm_pack_i8"
+    else:
+        if (partials.dtype != torch.float32 or partials.device != x.device or not partials.is_contiguous()
+                or partials.numel() < nws):
+            raise ValueError(f"partials must be a contiguous fp32 workspace of at least {nws} elements on x's device")
+        if h % 8 or w % 64:
+            raise ValueError(f"tile statistics need H % 8 == 0 and W % 64 == 0 (got {h} x {w})")
+        workspace, entry = partials, "h3v_gn_norm_pack_i8_partials"
     scratch = torch.empty((1,), device=x.device, dtype=torch.int32)
-    _hip.call("h3v_gn_norm_pack_i8", _hip.ptr(x), _hip.ptr(pre_bias), _hip.ptr(weight), _hip.ptr(bias), float(eps),
+    _hip.call(entry, _hip.ptr(x), _hip.ptr(pre_bias), _hip.ptr(weight), _hip.ptr(bias), float(eps),
               c, d, h, w, _hip.ptr(qy), _hip.ptr(scale), _hip.ptr(stats), _hip.ptr(workspace), _hip.ptr(scratch),
               _hip.stream(x.device))
     if return_stats:

@@ -23,10 +23,17 @@ _CL3D = torch.channels_last_3d
 
 
 def _run_stages(stages, h):
-    """Every residual block of each stage in order, then the stage's downsample if it has one."""
+    """Every residual block of each stage in order, then the stage's downsample if it has one.  Blocks with
+    ``forward_partials`` (the INT8 prefix blocks) hand the GroupNorm tile statistics of their output,
+    written by their last conv, to the next block's first norm."""
     for stage in stages:
+        partials = None
         for block in stage.block:
-            h = block(h)
+            step = getattr(block, "forward_partials", None)
+            if step is not None:
+                h, partials = step(h, partials)
+            else:
+                h, partials = block(h), None
         downsample = getattr(stage, "downsample", None)
         if downsample is not None:
             h = downsample(h)

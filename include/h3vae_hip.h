@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define H3V_ABI_VERSION 3
+#define H3V_ABI_VERSION 4
 
 #define H3V_OK 0
 #define H3V_EINVAL 1   /* shape / dtype / alignment / contract violation */
@@ -231,6 +231,26 @@ int h3v_conv3d_i8_residual_padded(const int8_t* qx, const float* x_scale, const 
                                   uint16_t* out, int batch, int cin, int d, int h, int w, int cout, int causal_skip,
                                   int front, int top, int bottom, int left, int right, hipStream_t stream);
 
+/* h3v_conv3d_i8 / h3v_conv3d_i8_residual (batch one, stride-1 3x3x3) that also
+ * writes the GroupNorm(32) statistics the next INT8 producer needs of its
+ * output, so that producer skips its own statistics pass over it.  Replaces,
+ * for the convolution that feeds a norm, the `_partial` / `_partial_bias`
+ * launches of _norm_statistics (opt/encoder_int8_norm.py:16-50, kernels of
+ * opt/encoder_fused_temporal_norm.py and opt/encoder_fused_norm_bias.py:14-39)
+ * that follow _conv3d_from_quantized (opt/encoder_int8.py:509).
+ * out (and residual, nullable): fp16 NDHWC [1, do, ho, wo, cout] as in those
+ * entry points; gn_bias: fp16 [cout] or NULL, the next producer's pre_bias
+ * (statistics of fp16(out + gn_bias)).  workspace: the next producer's
+ * workspace (h3v_gn_norm_pack_workspace_floats(do, ho, wo) floats), filled
+ * with the partial statistics of every 8-row x 64-column output tile (512
+ * pixels: per tile and group the average and M2, per tile and channel the
+ * fp16 max and min); hand it to h3v_gn_norm_pack_i8_partials with the same
+ * pre_bias.  Requires cin % 128 == 0, cout 128 or 256, wo 128 or 256, ho a
+ * multiple of 8, 16-byte aligned out, residual, gn_bias and workspace. */
+int h3v_conv3d_i8_gn(const int8_t* qx, const float* x_scale, const int8_t* qw, const float* w_scale,
+                     const uint16_t* bias, const uint16_t* residual, uint16_t* out, int cin, int d, int h, int w,
+                     int cout, int causal_skip, const uint16_t* gn_bias, float* workspace, hipStream_t stream);
+
 /* Raw int32 accumulators of the same convolution (exactness checks). */
 int h3v_conv3d_i8_i32(const int8_t* qx, const int8_t* qw, int32_t* acc, int batch, int cin, int d, int h,
                       int w, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
@@ -260,6 +280,17 @@ int64_t h3v_gn_norm_pack_workspace_floats(int d, int h, int w);
 int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta,
                         float eps, int c, int d, int h, int w, int8_t* q, float* scale, float* stats,
                         float* workspace, uint32_t* amax_scratch, hipStream_t stream);
+
+/* h3v_gn_norm_pack_i8 on an input written by h3v_conv3d_i8_gn: `workspace`
+ * holds the partial statistics of x's 512-pixel tiles (h * w a multiple of
+ * 512, h >= 8), summed over x + pre_bias with the same pre_bias; the
+ * statistics pass is skipped and the tiles merge in order (8-row bands of
+ * 64-column blocks).  Same outputs as h3v_gn_norm_pack_i8 up to the
+ * summation order of the statistics.  Replaces quantized_temporal_norm_pad
+ * (opt/encoder_int8_norm.py:77-110) after the fused conv. */
+int h3v_gn_norm_pack_i8_partials(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
+                                 const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
+                                 float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream);
 
 /* h3v_gn_norm_pack_i8 without a workspace argument and without allocating:
  * no counterpart in the reference.  It is for callers that cannot allocate

@@ -48,6 +48,8 @@ _SIGNATURES = {
     "ora_tensor_quant": (None, [_P, _I64, _F, _P]),
     "ora_conv3d_acc": (None, [_P, _P, _P] + [_I] * 12),
     "ora_gn_stats": (None, [_P, _P, _I, _I, _I, _I, _F, _P]),
+    "ora_gn_partials_tiled": (None, [_P, _P, _I, _I, _I, _I, _P, _P, _P]),
+    "ora_gn_merge_equal": (None, [_P, _P, _I, _I, _I, _I, _F, _P]),
     "ora_norm_pack": (_F, [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _F]),
     "ora_residual_rms_quant": (None, [_P, _P, _P, _P, _F, _I64, _I, _I, _P, _P, _P]),
     "ora_rms_fp16": (None, [_P, _P, _F, _I64, _I, _P]),
@@ -252,6 +254,41 @@ def gn_stats(x_ndhwc, eps, pre_bias=None):
     return stats
 
 
+GN_TILE = (8, 64)   # rows x columns of the window conv's output tiles (512 pixels)
+
+
+def gn_partials_tiled(x_ndhwc, pre_bias=None):
+    """GroupNorm(32) partial statistics of fp16 NDHWC [D,H,W,C] over the window conv's 8 x 64 output
+    tiles -> (avg [D,32,nchunk] fp32, m2 [D,32,nchunk] fp32, ext [D,nchunk,C] uint32 = fp16 max | min << 16),
+    the producer workspace layout of h3v_conv3d_i8_gn.  H % 8 == 0, W % 64 == 0."""
+    x = _f16(x_ndhwc)
+    d, h, w, c = x.shape
+    if h % GN_TILE[0] or w % GN_TILE[1]:
+        raise ValueError("tiled statistics need H % 8 == 0 and W % 64 == 0")
+    nchunk = (h // GN_TILE[0]) * (w // GN_TILE[1])
+    avg = np.empty((d, 32, nchunk), np.float32)
+    m2 = np.empty((d, 32, nchunk), np.float32)
+    ext = np.empty((d, nchunk, c), np.uint32)
+    lib().ora_gn_partials_tiled(_ptr(x), _ptr(_opt16(pre_bias)), d, h, w, c, _ptr(avg), _ptr(m2), _ptr(ext))
+    return avg, m2, ext
+
+
+def gn_merge_equal(avg, m2, chunk_pixels, c, eps):
+    """Sequential Chan merge of equal chunks (ora_gn_stats' merge) -> fp32 [D,32,2] (mean, rstd)."""
+    avg = np.ascontiguousarray(avg, np.float32)
+    m2 = np.ascontiguousarray(m2, np.float32)
+    d, _, nchunk = avg.shape
+    stats = np.empty((d, 32, 2), np.float32)
+    lib().ora_gn_merge_equal(_ptr(avg), _ptr(m2), d, nchunk, int(chunk_pixels), int(c), float(eps), _ptr(stats))
+    return stats
+
+
+def gn_stats_tiled(x_ndhwc, eps, pre_bias=None):
+    """Per-frame GroupNorm(32) (mean, rstd) summed over the window conv's 512-pixel tiles."""
+    avg, m2, _ = gn_partials_tiled(x_ndhwc, pre_bias)
+    return gn_merge_equal(avg, m2, GN_TILE[0] * GN_TILE[1], np.asarray(x_ndhwc).shape[-1], eps)
+
+
 def norm_pack(x_ndhwc, gamma, beta, stats, pre_bias=None, scale=None, want_fp16=True):
     """GroupNorm/SiLU/causal+reflect pack -> (fp16 y or None, int8 q or None, amax)."""
     x = _f16(x_ndhwc)
@@ -266,9 +303,10 @@ def norm_pack(x_ndhwc, gamma, beta, stats, pre_bias=None, scale=None, want_fp16=
     return y, q, np.float32(amax)
 
 
-def norm_conv3d(x_ndhwc, gamma, beta, eps, qw, ws, bias=None, pre_bias=None):
-    """E7: GN stats -> pack (absmax) -> scale -> INT8 pack -> conv -> fp16 NDHWC."""
-    stats = gn_stats(x_ndhwc, eps, pre_bias)
+def norm_conv3d(x_ndhwc, gamma, beta, eps, qw, ws, bias=None, pre_bias=None, tiled=False):
+    """E7: GN stats -> pack (absmax) -> scale -> INT8 pack -> conv -> fp16 NDHWC.  ``tiled``: the
+    statistics summed over the window conv's 8 x 64 output tiles (an input written by h3v_conv3d_i8_gn)."""
+    stats = gn_stats_tiled(x_ndhwc, eps, pre_bias) if tiled else gn_stats(x_ndhwc, eps, pre_bias)
     _, _, amax = norm_pack(x_ndhwc, gamma, beta, stats, pre_bias, want_fp16=False)
     s = scale_from_amax(amax)
     _, q, _ = norm_pack(x_ndhwc, gamma, beta, stats, pre_bias, scale=s, want_fp16=False)

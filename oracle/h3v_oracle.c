@@ -485,6 +485,108 @@ API void ora_gn_stats(const uint16_t* x, const uint16_t* pre_bias, int d, int h,
 }
 
 /*
+ * E6b: the same statistics over 512-pixel conv tiles (the window conv's statistics epilogue in
+ * csrc/gemm_i8.hip `write_tile`, read back by h3v_gn_norm_pack_i8_partials).  Chunk j of a frame
+ * is the tile of rows 8 rb .. 8 rb + 7 and columns 64 cb .. 64 cb + 63, j = rb * (W / 64) + cb;
+ * tile pixel r = (row - 8 rb) * 64 + (column - 64 cb).  Per group (cg channels), pixel lane
+ * pl = 0..31 takes tile pixels pl + 32 s, s = 0..15: the group's channels of a pixel summed left
+ * to right, added to the lane's running sum.  The lanes combine as the adjacent tree: for
+ * off = 1, 2, 4, 8, 16, lane i (a multiple of 2 off) adds lane i + off.  avg = S / (512 cg); M2
+ * the same with (v - avg)^2 terms.  Outputs in the producer workspace layout:
+ * avg, m2 [D][32][nchunk]; ext [D][nchunk][C] = fp16 max | fp16 min << 16 per channel.
+ * Requires H % 8 == 0 and W % 64 == 0.
+ */
+#define GN_TILE_ROWS 8
+#define GN_TILE_COLS 64
+#define GN_TILE_LANES 32
+
+API void ora_gn_partials_tiled(const uint16_t* x, const uint16_t* pre_bias, int d, int h, int w, int c,
+                               float* avg, float* m2, uint32_t* ext) {
+    int cg = c / GN_GROUPS;
+    int ncb = w / GN_TILE_COLS;
+    int nchunk = (h / GN_TILE_ROWS) * ncb;
+    int tpix = GN_TILE_ROWS * GN_TILE_COLS;
+    int steps = tpix / GN_TILE_LANES;
+    #pragma omp parallel for schedule(static)
+    for (int tj = 0; tj < d * nchunk; ++tj) {
+        int t = tj / nchunk, j = tj % nchunk;
+        int rb = j / ncb, cb = j % ncb;
+        float lanes[GN_TILE_LANES];
+        /* image index of tile pixel r */
+        #define TILE_PIX(r) (((int64_t)t * h + rb * GN_TILE_ROWS + (r) / GN_TILE_COLS) * w + \
+                             cb * GN_TILE_COLS + (r) % GN_TILE_COLS)
+        for (int g = 0; g < GN_GROUPS; ++g) {
+            for (int pl = 0; pl < GN_TILE_LANES; ++pl) {
+                float ls = 0.0f;
+                for (int st = 0; st < steps; ++st) {
+                    int64_t base = TILE_PIX(pl + GN_TILE_LANES * st) * c + g * cg;
+                    float ps = gn_load(x, pre_bias, base, g * cg);
+                    for (int i = 1; i < cg; ++i) ps = ps + gn_load(x, pre_bias, base + i, g * cg + i);
+                    ls = ls + ps;
+                }
+                lanes[pl] = ls;
+            }
+            for (int off = 1; off < GN_TILE_LANES; off <<= 1)
+                for (int i = 0; i < GN_TILE_LANES; i += 2 * off) lanes[i] = lanes[i] + lanes[i + off];
+            float a = lanes[0] / (float)(tpix * cg);
+            for (int pl = 0; pl < GN_TILE_LANES; ++pl) {
+                float lm = 0.0f;
+                for (int st = 0; st < steps; ++st) {
+                    int64_t base = TILE_PIX(pl + GN_TILE_LANES * st) * c + g * cg;
+                    float dv = gn_load(x, pre_bias, base, g * cg) - a;
+                    float pm = dv * dv;
+                    for (int i = 1; i < cg; ++i) {
+                        dv = gn_load(x, pre_bias, base + i, g * cg + i) - a;
+                        pm = pm + dv * dv;
+                    }
+                    lm = lm + pm;
+                }
+                lanes[pl] = lm;
+            }
+            for (int off = 1; off < GN_TILE_LANES; off <<= 1)
+                for (int i = 0; i < GN_TILE_LANES; i += 2 * off) lanes[i] = lanes[i] + lanes[i + off];
+            avg[((int64_t)t * GN_GROUPS + g) * nchunk + j] = a;
+            m2[((int64_t)t * GN_GROUPS + g) * nchunk + j] = lanes[0];
+        }
+        for (int ch = 0; ch < c; ++ch) {
+            float mx = -INFINITY, mn = INFINITY;
+            for (int r = 0; r < tpix; ++r) {
+                float v = gn_load(x, pre_bias, TILE_PIX(r) * c + ch, ch);
+                mx = fmaxf(mx, v);
+                mn = fminf(mn, v);
+            }
+            ext[((int64_t)t * nchunk + j) * c + ch] = (uint32_t)ora_f2h(mx) | ((uint32_t)ora_f2h(mn) << 16);
+        }
+        #undef TILE_PIX
+    }
+}
+
+/* Chan merge of equal chunks (as in ora_gn_stats) -> stats [D, 32, 2] = (mean, rstd). */
+API void ora_gn_merge_equal(const float* avg, const float* m2, int d, int nchunk, int chunk_pixels, int c,
+                            float eps, float* stats) {
+    int cg = c / GN_GROUPS;
+    for (int t = 0; t < d; ++t)
+        for (int g = 0; g < GN_GROUPS; ++g) {
+            const float* a = avg + ((int64_t)t * GN_GROUPS + g) * nchunk;
+            const float* m = m2 + ((int64_t)t * GN_GROUPS + g) * nchunk;
+            float nj = (float)(chunk_pixels * cg);
+            float total = (float)(nchunk * chunk_pixels * cg);
+            float san = 0.0f;
+            for (int j = 0; j < nchunk; ++j) san = san + a[j] * nj;
+            float mean = san / total;
+            float sv = 0.0f;
+            for (int j = 0; j < nchunk; ++j) {
+                float dl = a[j] - mean;
+                sv = sv + (m[j] + (nj * dl) * dl);
+            }
+            float var = sv / total;
+            if (var < 0.0f) var = 0.0f;
+            stats[(t * GN_GROUPS + g) * 2] = mean;
+            stats[(t * GN_GROUPS + g) * 2 + 1] = rsqrt_rn(var + eps);
+        }
+}
+
+/*
  * Norm / SiLU / causal + reflect pad producer
  * (opt/encoder_int8_norm_recompute.py:18-48):
  *   z = fp16(((v - mean) * rstd) * gamma + beta); z = fp16(z / (1 + exp(-z)))

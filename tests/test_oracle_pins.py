@@ -252,6 +252,56 @@ def test_gn_stats_against_float64(oracle, c, d, h, w, pre):
     assert np.allclose(st[..., 1], 1 / np.sqrt(var + 1e-6), rtol=1e-5)
 
 
+@pytest.mark.parametrize("c,d,h,w,pre", [(128, 2, 16, 128, False), (256, 1, 24, 64, True), (128, 1, 8, 192, True)])
+def test_gn_tiled_partials_against_float64(oracle, c, d, h, w, pre):
+    """Tile statistics of the window conv's 8 x 64 output tiles: per (frame, tile, channel) max / min
+    exactly numpy's over that tile's pixels (pins the tile geometry and the chunk numbering
+    rb * (W / 64) + cb), per (frame, group, tile) avg and M2 within float32 rounding of float64."""
+    x = (RNG.standard_normal((d, h, w, c)) * 2 + 0.3).astype(np.float16)
+    pb = RNG.standard_normal(c).astype(np.float16) if pre else None
+    avg, m2, ext = oracle.gn_partials_tiled(x, pb)
+    v = x.astype(np.float32)
+    if pre:
+        v = (v + pb.astype(np.float32)).astype(np.float16)
+    v = v.astype(np.float64)
+    ncb = w // 64
+    nchunk = (h // 8) * ncb
+    assert avg.shape == m2.shape == (d, 32, nchunk) and ext.shape == (d, nchunk, c)
+    # tiles[t, j, pixel, channel] with j = rb * ncb + cb
+    tiles = v.reshape(d, h // 8, 8, ncb, 64, c).transpose(0, 1, 3, 2, 4, 5).reshape(d, nchunk, 512, c)
+    mx = tiles.max(axis=2).astype(np.float16).view(np.uint16).astype(np.uint32)
+    mn = tiles.min(axis=2).astype(np.float16).view(np.uint16).astype(np.uint32)
+    assert np.array_equal(ext, mx | (mn << 16))
+    g = tiles.reshape(d, nchunk, 512, 32, c // 32)
+    mean = g.mean(axis=(2, 4)).transpose(0, 2, 1)                         # [d, 32, nchunk]
+    assert np.allclose(avg, mean, rtol=1e-5, atol=2e-6)
+    dev = g - avg.transpose(0, 2, 1)[:, :, None, :, None].astype(np.float64)
+    ss = (dev ** 2).sum(axis=(2, 4)).transpose(0, 2, 1)
+    assert np.allclose(m2, ss, rtol=1e-5)
+    st = oracle.gn_stats_tiled(x, 1e-6, pb)
+    gf = v.reshape(d, h * w, 32, c // 32)
+    assert np.allclose(st[..., 0], gf.mean(axis=(1, 3)), rtol=1e-5, atol=1e-6)
+    assert np.allclose(st[..., 1], 1 / np.sqrt(gf.var(axis=(1, 3)) + 1e-6), rtol=1e-5)
+    # the 256-pixel row chunks of the producer's own pass sum the same values in another order
+    assert np.allclose(st, oracle.gn_stats(x, 1e-6, pb), rtol=2e-6, atol=1e-7)
+
+
+def test_gn_tiled_lane_order(oracle):
+    """The documented order inside a tile, on values where the fp32 addition order shows.  One 8 x 64
+    tile, group 0 (channels 0-3): tile pixel 0 sums to B = 4 x 2048 = 2^13 (ulp 2^-10), tile pixels 16
+    and 17 hold d = 2^-11 in channel 0, half an ulp of B.  Documented: lanes pl = pixel % 32, so the
+    two d sit in lanes 16 and 17, whose adjacent-tree sum 2^-10 reaches lane 0 at the last level:
+    S = B + 2^-10 exactly, avg = S / 2048 = 4 + 2^-21.  Adding the pixels in raster order, a halving
+    tree (lane 0 + lane 16 first) or 16 pixel lanes (pixel 16 in lane 0 after B) each meets B + d
+    alone, a tie that rounds to B: avg = 4."""
+    x = np.zeros((1, 8, 64, 128), np.float16)
+    x[0, 0, 0, 0:4] = np.float16(2048.0)
+    x[0, 0, 16, 0] = x[0, 0, 17, 0] = np.float16(2.0 ** -11)
+    avg, m2, _ = oracle.gn_partials_tiled(x)
+    assert avg[0, 0, 0] == np.float32(4.0 + 2.0 ** -21)
+    assert (avg[0, 1:, 0] == 0).all() and (m2[0, 1:, 0] == 0).all()
+
+
 def test_norm_pack_structure_and_float64(oracle):
     d, h, w, c = 3, 6, 7, 128
     x = RNG.standard_normal((d, h, w, c)).astype(np.float16)
