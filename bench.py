@@ -887,13 +887,15 @@ def main():
         return
 
     # the decoder's INT8 GEMMs (h3v_gemm_i8_dequant args: ..., m, n, k, stream) and the stage-0 conv (C128 -> 128
-    # on the padded [19, 258, 258] int8 input, no residual)
+    # on the padded [19, 258, 258] int8 input, no residual; h3v_conv3d_i8_gn args: qx, xs, qw, ws, bias, residual,
+    # out, cin, d, h, w, cout, ...: the blocks' first convs, which also write the next norm's tile statistics)
     timer = LaunchTimer(torch, hip, {
         "qkv": ("h3v_gemm_i8_dequant", lambda a: a[7] == 3 * DEC_D and a[8] == DEC_D),
         "attn_out": ("h3v_gemm_i8_dequant", lambda a: a[7] == DEC_D and a[8] == DEC_D),
         "ffn_up": ("h3v_gemm_i8_dequant", lambda a: a[7] == 16384 and a[8] == DEC_D),
         "ffn_down": ("h3v_gemm_i8_dequant", lambda a: a[7] == DEC_D and a[8] == 8192),
-        "stage0_conv": ("h3v_conv3d_i8", lambda a: a[7] == 128 and a[11] == 128 and a[9] == 258 and a[8] == 19),
+        "stage0_conv": ("h3v_conv3d_i8_gn",
+                        lambda a: a[5] is None and a[7] == 128 and a[11] == 128 and a[10] == 258 and a[8] == 19),
     })
     log("building the reconstructed H3 VAE (random init) and the runtime")
     runtime = build_runtime(torch, pkg, args)
@@ -1002,7 +1004,7 @@ def main():
         },
         "roofline_stage0_conv": {
             "kernel": "conv3_halo_i8<256,Dequant,SP,64> (stage-0 conv C128->128, strided pixels on 64-pixel column blocks, "
-                      "[1,128,19,258,258] int8, no residual)",
+                      "[1,128,19,258,258] int8, no residual, with the GroupNorm tile statistics of its output)",
             "bound": "mfma",
             "achieved": round(achieved, 1),
             "peak": INT8_PEAK_TOPS,
