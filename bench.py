@@ -83,14 +83,42 @@ def synthetic_clip(torch, dev, seed=20261002, shape=(1, 3, 124, 768, 1344)):
 
 class LaunchTimer:
     """HIP events around selected C-ABI launches, recorded on torch's current stream (the stream every op
-    of the package launches on).  Wraps ``_hip.call``; off unless ``armed``."""
+    of the package launches on: one of the runtime's tile streams inside a step).  Wraps ``_hip.call``;
+    off until ``arm()``, which also records a reference event that dates every launch on one clock."""
 
     def __init__(self, torch, hip, selectors):
         self.torch, self.hip, self.selectors = torch, hip, selectors
         self.events = {name: [] for name in selectors}
         self.armed = False
+        self.ref = None
         self._call = hip.call
         hip.call = self
+
+    def reset(self):
+        self.events = {name: [] for name in self.selectors}
+
+    def arm(self):
+        self.ref = self.torch.cuda.Event(enable_timing=True)
+        self.ref.record()
+        self.armed = True
+
+    def union_us(self, keys):
+        """Length of the union of the selected launches' [start, end] intervals: the time in which at least
+        one of them ran.  Launches on different tile streams overlap; without overlap this is the sum of
+        their durations."""
+        spans = sorted((self.ref.elapsed_time(e0), self.ref.elapsed_time(e1))
+                       for key in keys for e0, e1 in self.events[key])
+        total, cur0, cur1 = 0.0, None, None
+        for a, b in spans:
+            if cur1 is None or a > cur1:
+                if cur1 is not None:
+                    total += cur1 - cur0
+                cur0, cur1 = a, b
+            else:
+                cur1 = max(cur1, b)
+        if cur1 is not None:
+            total += cur1 - cur0
+        return total * 1e3
 
     def __call__(self, name, *args):
         if self.armed:
@@ -722,7 +750,8 @@ def build_runtime(torch, pkg, args):
         core, config = rec.build_core(depth=args.depth)
     runtime = rt.H3VAEPyOptRuntime(device="cuda", dtype=torch.float16, decoder_tile_size=256, tile_batch=4,
                                    encoder_staged_batch=4, encoder_tile_size=0, int8_encode=True, int8_decode=True,
-                                   decode_fusions=True, log_calls=False, core=core, config=config)
+                                   decode_fusions=True, log_calls=False, core=core, config=config,
+                                   tile_streams=2)
     return runtime
 
 
@@ -859,6 +888,52 @@ def mfma_ceiling(torch, hip, runtime, clip):
     }
 
 
+GEMM_SHAPES = {"qkv": (3 * DEC_D, DEC_D), "attn_out": (DEC_D, DEC_D), "ffn_up": (16384, DEC_D),
+               "ffn_down": (DEC_D, 8192)}   # (N, K) of the decoder linears, M = DEC_M
+
+
+def launch_stats(timer):
+    """Roofline figures of the timed launches: the decoder GEMM family per shape and together, and the
+    stage-0 conv.  avg_us = the union of the launches' HIP-event intervals per launch (the time in which at
+    least one of them ran; the plain mean duration when no two overlap), launch_avg_us_shared = the mean of
+    the individual durations; achieved = algorithmic ops over the union."""
+    per_gemm = {}
+    for key, (n_, k_) in GEMM_SHAPES.items():
+        shared, n = timer.mean_us(key)
+        us = timer.union_us([key]) / n
+        ops = 2 * DEC_M * n_ * k_
+        per_gemm[key] = {"avg_us": round(us, 2), "launch_avg_us_shared": round(shared, 2), "launches_timed": n,
+                         "ops_per_launch": ops, "tops": round(ops / us / 1e6, 1),
+                         "frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)}
+    fam = tuple(GEMM_SHAPES)
+    fam_n = sum(per_gemm[k]["launches_timed"] for k in fam)
+    fam_us = timer.union_us(fam) / fam_n
+    fam_shared = sum(per_gemm[k]["launch_avg_us_shared"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
+    fam_ops = sum(per_gemm[k]["ops_per_launch"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
+    conv_shared, conv_n = timer.mean_us("stage0_conv")
+    conv_us = timer.union_us(["stage0_conv"]) / conv_n
+    conv_ops = stage0_conv_useful_ops()
+    return {"per_gemm": per_gemm, "fam_n": fam_n, "fam_us": fam_us, "fam_shared": fam_shared, "fam_ops": fam_ops,
+            "gemm_achieved": fam_ops / fam_us / 1e6, "conv_n": conv_n, "conv_us": conv_us, "conv_shared": conv_shared,
+            "conv_ops": conv_ops, "conv_achieved": conv_ops / conv_us / 1e6}
+
+
+def in_step_summary(st, which):
+    """The timed steps' figures of one roofline kernel (two tile streams: launches overlap)."""
+    if which == "gemm":
+        us, shared, n, achieved = st["fam_us"], st["fam_shared"], st["fam_n"], st["gemm_achieved"]
+    else:
+        us, shared, n, achieved = st["conv_us"], st["conv_shared"], st["conv_n"], st["conv_achieved"]
+    out = {"launches_timed": n, "avg_us": round(us, 2), "launch_avg_us_shared": round(shared, 2),
+           "achieved": round(achieved, 1), "frac": round(achieved / INT8_PEAK_TOPS, 4),
+           "timing": "timed steps, two tile streams: avg_us = the union of the launches' HIP-event intervals per "
+                     "launch (time in which at least one ran), launch_avg_us_shared = the mean individual duration "
+                     "(includes time shared with the other stream's kernels); achieved = ops / union"}
+    if which == "gemm":
+        out["per_gemm"] = st["per_gemm"]
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -925,8 +1000,8 @@ def main():
         latents = step(split)               # one extra untimed step for the encode/decode split
         log(f"split step: encode {split['enc']:.3f} s, decode {split['dec']:.3f} s; latents {tuple(latents.shape)}")
         finite = bool(torch.isfinite(latents).all()) and bool(torch.isfinite(out).all())
-        timer.armed = True
         torch.cuda.synchronize()
+        timer.arm()
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
@@ -936,28 +1011,31 @@ def main():
         log(f"timed {args.steps} steps: {elapsed / args.steps:.3f} s/step")
 
     sec_per_step = elapsed / args.steps
+    in_step = launch_stats(timer)
+
+    # The timed steps run encoder tiles and decoder tile groups on two streams at once, so a launch shares
+    # the GPU with the other stream's kernels for part of its time and its duration no longer describes the
+    # kernel.  One more step with a single tile stream times the same launches alone: `roofline` and
+    # `roofline_stage0_conv` come from it, their `in_step` objects from the timed steps.
+    with torch.inference_mode():
+        streams = runtime.tile_streams.count
+        runtime.tile_streams.count = 1
+        timer.reset()
+        torch.cuda.synchronize()
+        timer.arm()
+        t0 = time.perf_counter()
+        step()
+        torch.cuda.synchronize()
+        one_stream_s = time.perf_counter() - t0
+        timer.armed = False
+        runtime.tile_streams.count = streams
+    alone = launch_stats(timer)
+    log(f"one-stream step for the launch timings: {one_stream_s:.3f} s")
     clips = -(-args.frames // 17)
     enc_calls = 28 * clips
     dec_calls = 7 * 28 // 4 if args.frames == 124 else None
-    useful, _ = enc_ops_per_call()
-    conv_us, conv_n = timer.mean_us("stage0_conv")
-    conv_ops = stage0_conv_useful_ops()
-    achieved = conv_ops / conv_us / 1e6
-    # the dominant kernel by step time: the INT8 GEMM kernel behind every decoder linear (QKV, attention-out,
-    # FFN-up, FFN-down), one launch of each per block
-    gemm_n = {"qkv": 3 * DEC_D, "attn_out": DEC_D, "ffn_up": 16384, "ffn_down": DEC_D}
-    gemm_k = {"qkv": DEC_D, "attn_out": DEC_D, "ffn_up": DEC_D, "ffn_down": 8192}
-    per_gemm = {}
-    for key in gemm_n:
-        us, n = timer.mean_us(key)
-        ops = 2 * DEC_M * gemm_n[key] * gemm_k[key]
-        per_gemm[key] = {"avg_us": round(us, 2), "launches_timed": n, "ops_per_launch": ops,
-                         "tops": round(ops / us / 1e6, 1), "frac": round(ops / us / 1e6 / INT8_PEAK_TOPS, 4)}
-    fam = ("qkv", "attn_out", "ffn_up", "ffn_down")
-    fam_n = sum(per_gemm[k]["launches_timed"] for k in fam)
-    fam_us = sum(per_gemm[k]["avg_us"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
-    fam_ops = sum(per_gemm[k]["ops_per_launch"] * per_gemm[k]["launches_timed"] for k in fam) / fam_n
-    gemm_achieved = fam_ops / fam_us / 1e6
+    conv_ops, fam_ops = alone["conv_ops"], alone["fam_ops"]
+    achieved, gemm_achieved = alone["conv_achieved"], alone["gemm_achieved"]
     ref_s = REF_ENCODE_S + REF_DECODE_S
     result = {
         "metric": "H3 VAE encode/decode s @768x1344x124 tile256; INT8 MFMA % of peak",
@@ -977,7 +1055,8 @@ def main():
         "config": {
             "workload": f"cfg5_full_vae_encode_decode_1x3x{args.frames}x768x1344_tile256_batch4",
             "step": "runtime.encode(clip) then runtime.decode(latents, output_buffer) through H3VAEPyOptRuntime, "
-                    "int8_encode + int8_decode + decode_fusions, staged batch 4, tile batch 4",
+                    "int8_encode + int8_decode + decode_fusions, staged batch 4, tile batch 4, two tile streams "
+                    "(encoder tiles and decoder tile groups run two at a time)",
             "encode_tiles": 28, "clips": clips, "encode_prefix_calls": enc_calls,
             "decode_calls": dec_calls, "decode_blocks": args.depth, "decode_tokens_per_call": DEC_M,
         },
@@ -994,13 +1073,16 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(gemm_achieved / INT8_PEAK_TOPS, 4),
             "traffic": gemm_traffic(),
-            "launches_timed": fam_n,
-            "avg_us": round(fam_us, 2),
+            "launches_timed": alone["fam_n"],
+            "avg_us": round(alone["fam_us"], 2),
+            "timing": f"HIP events around every launch of one extra step run with a single tile stream "
+                      f"({one_stream_s:.3f} s), so that no launch shares the GPU; achieved = mean ops per launch / "
+                      "mean launch time",
             "algorithmic_ops_per_launch": round(fam_ops),
             "launch_mix": "per decoder block: QKV 7188x6144x2048, attention-out 7188x2048x2048, FFN-up "
-                          "7188x16384x2048, FFN-down 7188x2048x8192 (one of each); achieved = mean ops per launch / "
-                          "mean launch time",
-            "per_gemm": per_gemm,
+                          "7188x16384x2048, FFN-down 7188x2048x8192 (one of each)",
+            "per_gemm": alone["per_gemm"],
+            "in_step": in_step_summary(in_step, "gemm"),
         },
         "roofline_stage0_conv": {
             "kernel": "conv3_halo_i8<256,Dequant,SP,64> (stage-0 conv C128->128, strided pixels on 64-pixel column blocks, "
@@ -1011,9 +1093,11 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(achieved / INT8_PEAK_TOPS, 4),
             "traffic": stage0_conv_traffic(),
-            "launches_timed": conv_n,
-            "avg_us": round(conv_us, 1),
+            "launches_timed": alone["conv_n"],
+            "avg_us": round(alone["conv_us"], 1),
+            "timing": "as roofline: the one-stream step",
             "algorithmic_ops_per_launch": conv_ops,
+            "in_step": in_step_summary(in_step, "conv"),
         },
     }
     log("measuring the MFMA ceiling for the stage-0 conv operands")

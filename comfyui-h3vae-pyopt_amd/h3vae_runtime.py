@@ -227,6 +227,39 @@ def stitch_tiles(grid, y_overlaps, x_overlaps, blend):
     return canvas
 
 
+class _TileStreams:
+    """Runs independent tile jobs on ``count`` side streams in turn (default priority), so that one tile's
+    memory-bound kernels and the partial last rounds of its matrix kernels overlap another tile's work.
+    Each side stream first waits for the caller's stream; the caller's stream waits for every side stream
+    before it goes on, and each result is marked as used on the caller's stream (``record_stream``), so
+    the caching allocator never hands its memory out while a later kernel may still read it.  The tiles
+    compute exactly what they compute one after another; only their kernels interleave.  count <= 1 (or
+    a CPU device) runs the jobs in order on the caller's stream."""
+
+    def __init__(self, count: int):
+        self.count = max(1, int(count))
+        self._streams = {}
+
+    def run(self, jobs, device):
+        if self.count == 1 or device.type != "cuda":
+            return [job() for job in jobs]
+        streams = self._streams.get(device)
+        if streams is None:
+            streams = self._streams[device] = [torch.cuda.Stream(device=device) for _ in range(self.count)]
+        main = torch.cuda.current_stream(device)
+        results = []
+        for k, job in enumerate(jobs):
+            side = streams[k % self.count]
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                out = job()
+            out.record_stream(main)
+            results.append(out)
+        for side in streams:
+            main.wait_stream(side)
+        return results
+
+
 class _TileBatcher:
     """Replacement for the core's ``_run_tile_tasks``: decoder tiles go through ``forward_fn`` in
     groups of ``batch`` (0: 1 or 2 by free GPU memory).  Anything it does not batch (class-token
@@ -235,8 +268,9 @@ class _TileBatcher:
     RESERVE = 12 * 1024 ** 3      # kept free for the decoded video and other GPU users
     PER_TILE = 4 * 1024 ** 3
 
-    def __init__(self, core, own, batch):
+    def __init__(self, core, own, batch, streams=None):
         self.core, self.own, self.batch = core, own, int(batch)
+        self.streams = streams if streams is not None else _TileStreams(1)
 
     def _group_size(self, device):
         if self.batch:
@@ -252,11 +286,9 @@ class _TileBatcher:
         self.core._last_tile_batch = size
         if size == 1:
             return self.own(tiles, indices, forward_fn, stack_tiling, cls_agg)
-        results = []
-        for first in range(0, len(indices), size):
-            group = [tiles[i] for i in indices[first:first + size]]
-            results += list(forward_fn(torch.cat(group, dim=0)).split(1, dim=0))
-        return results
+        groups = [[tiles[i] for i in indices[first:first + size]] for first in range(0, len(indices), size)]
+        outs = self.streams.run([lambda g=g: forward_fn(torch.cat(g, dim=0)) for g in groups], tiles[0].device)
+        return [tile for out in outs for tile in out.split(1, dim=0)]
 
 
 class _CallTimer:
@@ -288,7 +320,7 @@ class H3VAEPyOptRuntime(torch.nn.Module):
                  tile_batch: int = 2, compile_decoder: bool = True, compile_encoder: bool = True, qk_rows: int = 8,
                  encoder_staged_batch: int = 4, log_calls: bool = True, encoder_tile_size: int = 0,
                  fast_linear: bool = False, int8_decode: bool = False, int8_encode: bool = False,
-                 decode_fusions: bool = False, *, core=None, config=None):
+                 decode_fusions: bool = False, *, core=None, config=None, tile_streams: int = 2):
         super().__init__()
         int8_decode, int8_encode = bool(int8_decode), bool(int8_encode)
         if fast_linear:
@@ -301,6 +333,10 @@ class H3VAEPyOptRuntime(torch.nn.Module):
             raise ValueError("encoder_tile_size must be 0 (auto) or a positive multiple of 16")
         if int(tile_batch) < 0:
             raise ValueError("tile_batch must be non-negative")
+        if int(tile_streams) < 1:
+            raise ValueError("tile_streams must be at least 1")
+        # independent encoder tiles and decoder tile groups run on this many streams at once
+        self.tile_streams = _TileStreams(tile_streams)
         if core is None:
             core, config = _load_klvae_core(model_code_dir)
             if encoder_tile_size and encoder_tile_size <= core.tile_overlap_min:
@@ -358,7 +394,7 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         core.decoder_tile_size = tile_size
         core.stack_tiling = False
         if tile_batch != 1:
-            self._install_batched_tiles(core, tile_batch)
+            self._install_batched_tiles(core, tile_batch, self.tile_streams)
 
     def _wire_encoder(self, core):
         """conv_in and every downsample conv with packed padding; the bias-fused prefix (residual-pack
@@ -390,9 +426,10 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         self.prefix, self.suffix = prefix, suffix
 
     @staticmethod
-    def _install_batched_tiles(core, batch: int):
-        """Batch decoder tiles per forward call (0 picks 1 or 2 from free memory; reference :452-483)."""
-        core._run_tile_tasks = _TileBatcher(core, core._run_tile_tasks, batch)
+    def _install_batched_tiles(core, batch: int, streams=None):
+        """Batch decoder tiles per forward call (0 picks 1 or 2 from free memory; reference :452-483); the
+        groups run on ``streams`` (a _TileStreams) in turn."""
+        core._run_tile_tasks = _TileBatcher(core, core._run_tile_tasks, batch, streams)
 
     # ---- small helpers --------------------------------------------------------------------------------
 
@@ -491,8 +528,10 @@ class H3VAEPyOptRuntime(torch.nn.Module):
         ys, hs, y_over = axis_tiles(x.shape[-2], tile_size, core.tile_overlap_min, core.vae_ratio)
         xs, ws, x_over = axis_tiles(x.shape[-1], tile_size, core.tile_overlap_min, core.vae_ratio)
         normed = self._normalize_pixels(x)
-        grid = [[self._encode_moments(normed[..., y:y + h, x0:x0 + w]) for x0, w in zip(xs, ws)]
-                for y, h in zip(ys, hs)]
+        jobs = [lambda y=y, h=h, x0=x0, w=w: self._encode_moments(normed[..., y:y + h, x0:x0 + w])
+                for y, h in zip(ys, hs) for x0, w in zip(xs, ws)]
+        flat = self.tile_streams.run(jobs, normed.device)
+        grid = [flat[i * len(xs):(i + 1) * len(xs)] for i in range(len(ys))]
         r = core.vae_ratio
         return stitch_tiles(grid, [o // r for o in y_over], [o // r for o in x_over], core.blend)
 

@@ -12,7 +12,9 @@ the core's own FP16 modules run through the same routines:
   restatement of the reference's nested blend loop (h3vae_runtime.py:609-639), within the same bounds;
 * decode: latent t = 1, 2, 7 and 12 (a 2-chunk video) over 2 x 2 tiles, tile batch 1 and 2, with and
   without decode_fusions: fp32 pixels within relative L2 0.05 of the core's FP16 decode finalised in
-  float32; a matching fp32 output_buffer is written in place and returned.
+  float32; a matching fp32 output_buffer is written in place and returned;
+* concurrent tile streams: encode (2 x 3 tiles, INT8) and decode (2 x 2 tiles in groups of 1 and 2,
+  decode_fusions) on 2 and 3 streams are bit-identical to the same runtime on one stream.
 """
 from __future__ import annotations
 
@@ -170,6 +172,32 @@ def test_runtime_decode_matches_fp16_model(rt, t, tile_batch, fusions):
         assert core._last_tile_batch == tile_batch
     rel = float((got - want).norm() / want.norm())
     assert rel < 0.05, rel
+
+
+@pytest.mark.parametrize("streams", [2, 3])
+def test_runtime_tile_streams_match_one_stream(rt, streams):
+    """The tiles (encode) and tile groups (decode) that run on side streams at once compute what they
+    compute one after another: outputs bit-identical to tile_streams=1 on the same core."""
+    print(f"runtime tile_streams={streams} vs 1", flush=True)
+    torch.manual_seed(19)
+    core = h3_arch.H3Core(h3_arch.H3Encoder(h3_arch.H3_ENCODER_STAGES),
+                          h3_arch.H3Decoder(dim=1024, hidden=2048, depth=2)).eval()
+    common = dict(device="cuda", dtype=torch.float16, int8_encode=True, int8_decode=True, decode_fusions=True,
+                  encoder_tile_size=128, encoder_staged_batch=4, decoder_tile_size=256, tile_batch=2,
+                  log_calls=False, config=_config())
+    one = rt.H3VAEPyOptRuntime(core=copy.deepcopy(core), tile_streams=1, **common)
+    many = rt.H3VAEPyOptRuntime(core=core, tile_streams=streams, **common)
+    gen = torch.Generator().manual_seed(23)
+    x = (torch.rand(1, 3, 22, 192, 256, generator=gen) * 2 - 1).half().to(DEV)     # 2 x 3 encoder tiles
+    z = torch.randn(1, 24, 7, 20, 20, generator=gen).half().to(DEV)                 # 2 x 2 decoder tiles
+    with torch.inference_mode():
+        lat1, lat2 = one.encode(x), many.encode(x)
+        pix1, pix2 = one.decode(z), many.decode(z)
+        torch.cuda.synchronize()
+    assert torch.isfinite(lat2).all() and torch.isfinite(pix2).all()
+    assert torch.equal(lat1, lat2)
+    assert torch.equal(pix1, pix2)
+    assert many.core._last_tile_batch == 2
 
 
 def test_runtime_decode_offload_frees_packed_and_int8_copies(rt):

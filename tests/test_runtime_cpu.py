@@ -93,6 +93,7 @@ def _bare_runtime(rt, core):
     r.int8_decode = r.int8_encode = False
     r.decode_fusions = False
     r.log_calls = False
+    r.tile_streams = rt._TileStreams(2)
     r._img_mean = torch.tensor(rt._IMG_MEAN).reshape(1, 3, 1, 1, 1)
     r._img_std = torch.tensor(rt._IMG_STD).reshape(1, 3, 1, 1, 1)
     return r
@@ -278,6 +279,19 @@ def test_runtime_rejects_before_loading(rt):
         rt.H3VAEPyOptRuntime(device="cpu", int8_decode=True)
     with pytest.raises(ValueError, match="model_code_dir"):
         rt.H3VAEPyOptRuntime(model_code_dir="", device="cpu")
+    assert params["tile_streams"].default == 2
+    with pytest.raises(ValueError, match="tile_streams"):
+        rt.H3VAEPyOptRuntime(device="cpu", tile_streams=0)
+
+
+def test_tile_streams_run_jobs_in_order_off_gpu(rt):
+    """Off the GPU (and with one stream) the tile jobs run in order on the caller's stream."""
+    seen = []
+    jobs = [lambda k=k: seen.append(k) or torch.full((1,), float(k)) for k in range(5)]
+    out = rt._TileStreams(3).run(jobs, torch.device("cpu"))
+    assert seen == [0, 1, 2, 3, 4] and [float(t) for t in out] == [0.0, 1.0, 2.0, 3.0, 4.0]
+    seen.clear()
+    assert [float(t) for t in rt._TileStreams(1).run(jobs, torch.device("cpu"))] == [0.0, 1.0, 2.0, 3.0, 4.0]
 
 
 # -- ComfyUI node -----------------------------------------------------------------------------------------
