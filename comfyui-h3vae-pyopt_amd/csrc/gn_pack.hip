@@ -10,11 +10,13 @@
 // counters to clear beforehand):
 //   gn_partial    grid (chunks, D): per 256-pixel chunk and group, avg and M2;
 //                 per chunk and channel max and min of the (pre-biased) input
-//                 (fp16, exact); block (0, 0) also zeroes the two counters of
-//                 absmax_lut
+//                 (fp16, exact).  Skipped by h3v_gn_norm_pack_i8_partials, whose
+//                 caller's window conv (h3v_conv3d_i8_gn) already wrote the same
+//                 three arrays for its 512-pixel output tiles
 //   gn_merge      grid (32, D): Chan merge of the chunks -> (mean, rstd); the
 //                 per-channel extremes over the chunks give the group's absmax
-//                 candidate (below), one word per (frame, group)
+//                 candidate (below), one word per (frame, group); block (0, 0)
+//                 also zeroes the two counters of absmax_lut
 //   absmax_lut    reduces the candidates, then builds the int8 code of every
 //                 fp16 pre-activation z under the final scale; when the candidate
 //                 cannot be proven exact it first runs the full absmax pass and
@@ -41,6 +43,8 @@
 // pixel lanes; lane pl owns pixels pl, pl+PL, ...; per pixel the group's
 // channels are summed left to right and added to the lane's running sum; the
 // lanes combine by the halving tree off = PL/2 .. 1; chunks merge sequentially.
+// The conv-epilogue partials follow their own fixed order (32 pixel lanes of a
+// 512-pixel tile, adjacent-pair tree), also restated by the oracle.
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
@@ -388,7 +392,7 @@ __device__ __forceinline__ void build_lut_range(float amax, int8_t* __restrict__
 // (almost always) the final scale is known at once: block 0 stores it and the first 256 blocks build 256
 // table entries each.  Otherwise every block runs its share of the full absmax pass into done[1]; the
 // last block to finish (counter done[0]) stores the final absmax and builds the whole table from it.
-// All blocks compute the same candidate, so all take the same branch.  gn_partial zeroed both counters.
+// All blocks compute the same candidate, so all take the same branch.  gn_merge zeroed both counters.
 // Grid: at least 256 blocks.
 template <int C, bool PRE_BIAS>
 __global__ __launch_bounds__(kNT) void absmax_lut(const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_bias,
