@@ -334,7 +334,11 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
             t_c = timed(lambda: call("h3v_conv3d_f16_ws", p(xs), p(wsp), p(bs), None, p(ys), b, cin, dp, hp, wp, cout, k,
                                      k, k, *stride, int(causal), p(wsf), floats, stream))
             flops = 2 * b * do * ho * wo * cout * k ** 3 * cin
-            res = {"h3v_conv3d_f16": fp16_mfma(t_c, flops)}
+            if k == 1:   # a 1x1x1 projection does 2 * Cin flops per output value: far below the fp16 ridge, HBM-bound
+                nbytes = 2 * (b * dp * hp * wp * cin + b * do * ho * wo * cout + cout * cin)
+                res = {"h3v_conv3d_f16": dict(hbm(t_c, nbytes), tflops=round(flops / t_c / 1e6, 1), flops=flops)}
+            else:
+                res = {"h3v_conv3d_f16": fp16_mfma(t_c, flops)}
             if vs_torch:
                 res["torch_conv3d"] = fp16_mfma(timed(lambda: F.conv3d(xs, ws, bs, stride=stride)), flops)
                 xn = xs.contiguous()
@@ -366,8 +370,13 @@ def config_measurements(torch, hip, kitchen, enc, stream, reps=20, vs_torch=Fals
                  stream)
 
         t_in = timed(conv_in)
+        # 2 * 81 flops per output value against its 2-byte store: HBM-bound.  Bytes: the 3-channel input read, the
+        # folded input written and read back, the weights, the fp16 output written
+        in_bytes = 2 * (17 * 256 * 256 * 3 + 2 * 19 * 256 * 256 * 32 + 128 * 96 + 17 * 256 * 256 * 128)
+        in_flops = 2 * 17 * 256 * 256 * 128 * 81
         out["conv_in_f16_3to128x17x256x256"] = {"tap_fold_pack_and_conv3d_f16":
-                                                fp16_mfma(t_in, 2 * 17 * 256 * 256 * 128 * 81)}
+                                                dict(hbm(t_in, in_bytes), tflops=round(in_flops / t_in / 1e6, 1),
+                                                     flops=in_flops)}
     torch.cuda.synchronize()
     return out
 
