@@ -195,7 +195,12 @@ class PackedConvWeight(nn.Module):
     with its owner (``.to()``, an offload of the runtime): no packed copy outlives the module or
     stays behind on a GPU, and a conv that never runs never holds one.  Each use compares the
     source weight with the stamp taken at packing and repacks when it changed (an in-place
-    state-dict load, a move of the model's weights)."""
+    state-dict load, a move of the model's weights).
+
+    The runtime runs encoder tiles on several streams at once, and the copy is shared by all of
+    them, so on a GPU (re)packing waits for the device twice: before, because another stream may
+    still read the old copy, and after, because the packing kernel runs on the current stream and
+    the next tile's convs on another stream must not read the copy before it is written."""
 
     def __init__(self, weight, fold=False):
         super().__init__()
@@ -207,8 +212,12 @@ class PackedConvWeight(nn.Module):
         stamp = _weight_stamp(weight)
         if self.packed is None or stamp != self._stamp:
             source = weight.detach()
+            if source.is_cuda:
+                torch.cuda.synchronize(source.device)
             self.packed = fold_conv_weight_f16(source) if self.fold else pack_conv_weight_f16(source)
             self._stamp = stamp
+            if source.is_cuda:
+                torch.cuda.synchronize(source.device)
         return self.packed
 
 
