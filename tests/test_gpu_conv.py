@@ -100,6 +100,22 @@ def test_conv_strided_pixel_shapes_sampled(ops, oracle, b, c, d, h, w, co, sampl
         assert np.array_equal(acc[bi:bi + 1, t:t + 1, :2 * rows], want), f"batch {bi} frame {t}"
 
 
+def test_conv_strided_pixel_partial_row_group(ops, oracle):
+    """The window kernel walks its tiles in groups of 8 / (weight tiles) row blocks; an output height of 40
+    (5 row blocks of 8 rows) leaves one partial group.  Exact int32 against the oracle on the first and the
+    last row block of sampled frames (130 tiles: the strided-pixel window kernel)."""
+    gen = _gen(4242)
+    qx = torch.randint(-127, 128, (1, 15, 42, 130, 128), generator=gen, dtype=torch.int8)
+    qx[:, :2] = 0
+    qw = torch.randint(-127, 128, (128, 3456), generator=gen, dtype=torch.int8)
+    print("strided-pixel window conv 1x128x15x42x130 -> 128 (partial row group)", flush=True)
+    acc = _conv_i32_gpu(ops, qx, qw, (3, 3, 3), (1, 1, 1), True)
+    for t in (0, 5, 12):
+        for r0 in (0, 32):
+            want = oracle.conv3d_acc(qx[:, t:t + 3, r0:r0 + 10].numpy(), qw.numpy(), (3, 3, 3), (1, 1, 1))
+            assert np.array_equal(acc[:, t:t + 1, r0:r0 + 8], want), f"frame {t} rows {r0}.."
+
+
 def test_conv_h3_stage0_shape_sampled(ops, oracle):
     """Real stage-0 layer: [1,128,19,258,258] int8 -> [1,17,256,256,128], causal skip; frames sampled."""
     gen = _gen(11)
