@@ -1319,8 +1319,8 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     // RBG = 8 / weight tiles, so the 32 workgroups an XCD runs at once cover 8 / RBG weight tiles x RBG
     // row blocks x 4 frames of one column block: the rows of neighbouring row blocks and the frames of
     // neighbouring output frames they share are read while that XCD's L2 still holds them.  Stage-0
-    // conv (one weight tile): input fetched from beyond L2 1.53x -> 0.98x the int8 bytes (frames, then
-    // column blocks, then row blocks: the previous order), 428.7 -> 394 us; 4 frames per group beat 2
+    // conv (one weight tile), against frames, then column blocks, then row blocks: input fetched from
+    // beyond L2 1.53x -> 0.98x the int8 bytes, 430.2 -> 410.6 us (same box); 4 frames per 32 tiles beat 2
     // and 8 on every window conv measured.
     int id = xcd_remap(blockIdx.x, gridDim.x);
     const int tn = id % p.tiles_n;
