@@ -431,17 +431,17 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                     const int q = j * 4 + q4;
 #pragma unroll
                     for (int i = 0; i < FM; ++i) {
-                        u16x4 v;
+                        float y[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
                             if constexpr (EP == Epi::F16Bias) {
                                 const float a = acc[i][j][q4 * 4 + e];
-                                v[e] = f2h(HB ? a + h2f(qb[q][e]) : a);
+                                y[e] = HB ? a + h2f(qb[q][e]) : a;
                             } else {
-                                v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]));
+                                y[e] = g1_reg<HB>(acc[i][j][q4 * 4 + e], sxr[i], qsw[q][e], qb[q][e]);
                             }
                         }
-                        put(trow(i), tc, v);
+                        put(trow(i), tc, f2h4(y[0], y[1], y[2], y[3]));
                     }
                 }
             }
@@ -1175,11 +1175,12 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
                     const int q = j * 4 + q4;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
-                        u16x4 v;
+                        float y[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = f2h(g1_reg<HB>(acc[i][j][q4 * 4 + e], sx[i], qsw[q][e], qb[q][e]));
+                        for (int e = 0; e < 4; ++e) y[e] = g1_reg<HB>(acc[i][j][q4 * 4 + e], sx[i], qsw[q][e], qb[q][e]);
                         const int r = i * 32 + frow;
-                        *reinterpret_cast<u16x4*>(stage + r * 128 + ((q ^ ((r >> 1) & 7)) << 4) + fhi * 8) = v;
+                        *reinterpret_cast<u16x4*>(stage + r * 128 + ((q ^ ((r >> 1) & 7)) << 4) + fhi * 8) =
+                            f2h4(y[0], y[1], y[2], y[3]);
                     }
                 }
         };

@@ -23,6 +23,14 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(f16, b); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (f16)f); }
 __device__ __forceinline__ float rt16(float f) { return (float)(f16)f; }
+// Four fp32 values to fp16 (round to nearest even, as f2h) with two v_cvt_pk_f16_f32; element-wise f2h
+// into a u16x4 compiles to single conversions plus packing instructions.
+__device__ __forceinline__ u16x4 f2h4(float a, float b, float c, float d) {
+    const f16x2 lo = __builtin_convertvector((f32x2){a, b}, f16x2);
+    const f16x2 hi = __builtin_convertvector((f32x2){c, d}, f16x2);
+    const uint2 w = {__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi)};
+    return __builtin_bit_cast(u16x4, w);
+}
 
 // A 16-byte load marked non-temporal (global_load ... nt): for streams read once whose lines need
 // not stay in the caches.  A large activation read this way (the GroupNorm producers' input, 285 MB
