@@ -20,7 +20,7 @@ import torch
 
 LIB_NAME = "libh3vae_hip.so"
 LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
-ABI_VERSION = 4
+ABI_VERSION = 5
 EINVAL = 1
 
 _P = ctypes.c_void_p
@@ -43,7 +43,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_tensor_quant_i8": [_P, _I64, _P, _P, _P, _I64, _P],
     "h3v_gn_norm_pack_i8": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "h3v_gn_norm_pack_i8_noalloc": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P],
-    "h3v_gn_norm_pack_i8_partials": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+    "h3v_gn_norm_pack_i8_partials": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
     "h3v_residual_norm1_quant": [_P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P, _P],
     "h3v_residual_rms_quant": [_P, _P, _P, _P, _F, _I64, _I64, _P, _P, _P, _P],
     "h3v_rms_fp16": [_P, _P, _F, _I64, _I64, _P, _P],
@@ -57,6 +57,7 @@ SIGNATURES: dict[str, list] = {
     "h3v_tap_fold_pack": [_P, _P] + [_I] * 7 + [_P],
     "h3v_conv3d_f16": [_P, _P, _P, _P, _P] + [_I] * 13 + [_P],
     "h3v_conv3d_f16_ws": [_P, _P, _P, _P, _P] + [_I] * 13 + [_P, _I64, _P],
+    "h3v_conv3d_f16_gn": [_P, _P, _P, _P] + [_I] * 12 + [_P, _P],
     "h3v_gn_norm_pack_f16": [_P, _P, _P, _P, _F, _I, _I, _I, _I, _I, _P, _P, _P, _P],
     "h3v_attention_d64": [_P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _F, _P],
 }

@@ -251,6 +251,10 @@ __device__ __forceinline__ void wait_stage(int ahead) {
 // i * 32 + r.  TILEW > 0: the tile is 512 / TILEW output rows of TILEW pixels each (a column block
 // of output rows p.Wo wide) starting at row m0, so tile row r is output row
 // m0 + (r / TILEW) * p.Wo + r % TILEW; 0: the tile's rows are consecutive from m0.
+// LDS past the operand rings that the chunk-statistics epilogue of the FP16 implicit-GEMM conv uses: the
+// lane sums [16][32], the group averages [32] and per wave of threads 0-255 the channel extremes [4][128][2].
+constexpr int kGnChunkLdsBytes = (16 * 32 + 32 + 4 * 128 * 2) * 4;
+
 template <int BM, int BN, int WGM, int WGN, int LDS_BYTES, Epi EP, int PADWO = 0, bool SROWS = false, int TILEW = 0,
           typename AccV>
 __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM / WGM / 32][BN / WGN / 32],
@@ -657,6 +661,120 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
 #pragma unroll
                     for (int e = 0; e < 8; ++e)
                         if (gcol + e < p.N) dst[e] = v[e];
+                }
+            }
+            // Chunk statistics (h3v_conv3d_f16_gn: 256 x 128 tiles of 8 waves, 128 output channels, every tile
+            // 256 consecutive pixels of one frame, batch one): the GroupNorm(32) partials of the tile exactly as
+            // the INT8 producer's statistics pass (gn_partial, C = 128) forms them for a 256-pixel chunk, from
+            // the staged tile instead of memory.  Threads 0-255: cv = tid % 16 owns channels 8 cv .. 8 cv + 7
+            // (groups 2 cv, 2 cv + 1) and pl = tid / 16 the pixels pl + 16 s (s = 0 .. 15); per pixel a group's
+            // four channels are summed left to right and added to the lane's running sum; the 16 pixel lanes
+            // combine by the halving tree off = 8, 4, 2, 1 (lane i += lane i + off); avg = sum / 1024, and M2
+            // the same sums of (v - avg)^2.  Channel maxima and minima are exact in any order.
+            if constexpr (EP == Epi::F16Bias && BM == 256 && OUTW == 128 && NW == 8 && !SROWS && TILEW == 0 &&
+                          PADWO == 0) {
+                if (p.gn_avg != nullptr) {
+                    constexpr int PL = 16, STEPS = 16, CG = 4;
+                    float* const sred = reinterpret_cast<float*>(smem + RING);   // [PL][32]
+                    float* const savg = sred + PL * 32;                         // [32]
+                    float* const sext = savg + 32;                              // [wave][128][2], waves 0-3
+                    const bool act = tid < 256;
+                    const int cv = tid & 15, pl = (tid >> 4) & 15;
+                    u16x8 xv[STEPS];
+                    float ls[2] = {0.0f, 0.0f}, vmx[8], vmn[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) { vmx[e] = -__builtin_inff(); vmn[e] = __builtin_inff(); }
+                    if (act) {
+#pragma unroll
+                        for (int st = 0; st < STEPS; ++st) {
+                            const int r = pl + st * PL;
+                            xv[st] = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((cv ^ skey(r)) << 4));
+                        }
+#pragma unroll
+                        for (int st = 0; st < STEPS; ++st) {
+                            float f[8];
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                f[e] = h2f(xv[st][e]);
+                                vmx[e] = __builtin_fmaxf(vmx[e], f[e]);
+                                vmn[e] = __builtin_fminf(vmn[e], f[e]);
+                            }
+#pragma unroll
+                            for (int gi = 0; gi < 2; ++gi) {
+                                float ps = f[gi * CG];
+#pragma unroll
+                                for (int i = 1; i < CG; ++i) ps = ps + f[gi * CG + i];
+                                ls[gi] = ls[gi] + ps;
+                            }
+                        }
+#pragma unroll
+                        for (int gi = 0; gi < 2; ++gi) sred[pl * 32 + cv * 2 + gi] = ls[gi];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            vmx[e] = __builtin_fmaxf(vmx[e], __shfl_xor(vmx[e], 16, 64));
+                            vmx[e] = __builtin_fmaxf(vmx[e], __shfl_xor(vmx[e], 32, 64));
+                            vmn[e] = __builtin_fminf(vmn[e], __shfl_xor(vmn[e], 16, 64));
+                            vmn[e] = __builtin_fminf(vmn[e], __shfl_xor(vmn[e], 32, 64));
+                        }
+                        if (lane < 16) {
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                sext[2 * (wave * 128 + cv * 8 + e)] = vmx[e];
+                                sext[2 * (wave * 128 + cv * 8 + e) + 1] = vmn[e];
+                            }
+                        }
+                    }
+                    const int hw = p.Ho * p.Wo;
+                    const int fr = m0 / hw, chunk = (m0 - fr * hw) / 256;
+                    // the halving tree of gn_partial over the lane sums of group g, in place
+                    auto tree = [&](int g) {
+                        for (int off = PL / 2; off >= 1; off >>= 1)
+                            for (int i = 0; i < off; ++i) sred[i * 32 + g] = sred[i * 32 + g] + sred[(i + off) * 32 + g];
+                        return sred[g];
+                    };
+                    lds_barrier();
+                    if (tid < 32) savg[tid] = tree(tid) / (float)(256 * CG);
+                    if (tid >= 256 && tid < 384) {
+                        const int c = tid - 256;
+                        float mx = sext[2 * c], mn = sext[2 * c + 1];
+#pragma unroll
+                        for (int w = 1; w < 4; ++w) {
+                            mx = __builtin_fmaxf(mx, sext[2 * (w * 128 + c)]);
+                            mn = __builtin_fminf(mn, sext[2 * (w * 128 + c) + 1]);
+                        }
+                        // the extremes are stored fp16 values: exact as fp16
+                        p.gn_ext[((int64_t)fr * p.gn_nchunk + chunk) * 128 + c] =
+                            (uint32_t)f2h(mx) | ((uint32_t)f2h(mn) << 16);
+                    }
+                    lds_barrier();
+                    float lm[2] = {0.0f, 0.0f};
+                    if (act) {
+                        const float a0 = savg[cv * 2], a1 = savg[cv * 2 + 1];
+#pragma unroll
+                        for (int st = 0; st < STEPS; ++st) {
+#pragma unroll
+                            for (int gi = 0; gi < 2; ++gi) {
+                                const float a = gi ? a1 : a0;
+                                float dv = h2f(xv[st][gi * CG]) - a;
+                                float pm = dv * dv;
+#pragma unroll
+                                for (int i = 1; i < CG; ++i) {
+                                    dv = h2f(xv[st][gi * CG + i]) - a;
+                                    pm = pm + dv * dv;
+                                }
+                                lm[gi] = lm[gi] + pm;
+                            }
+                        }
+#pragma unroll
+                        for (int gi = 0; gi < 2; ++gi) sred[pl * 32 + cv * 2 + gi] = lm[gi];
+                    }
+                    lds_barrier();
+                    if (tid < 32) {
+                        // group-major [frame][group][chunk], as gn_partial
+                        const int64_t dst = ((int64_t)fr * 32 + tid) * p.gn_nchunk + chunk;
+                        p.gn_m2[dst] = tree(tid);
+                        p.gn_avg[dst] = savg[tid];
+                    }
                 }
             }
         } else {
@@ -1670,11 +1788,16 @@ int launch_tiled(GemmParams p, hipStream_t stream, const char* what) {
     }
     constexpr size_t kLds = (size_t)(NSA * BM + NSB * BN) * BK;   // LDS rings (at most 160 KB on gfx950)
     static_assert(kLds <= 163840, "LDS rings exceed 160 KB");
-    const size_t lds = kLds;
+    // the chunk-statistics epilogue (h3v_conv3d_f16_gn) needs its reduction space past the rings
+    constexpr bool kChunkStats = EP == Epi::F16Bias && BM == 256 && BN == 128 && WGM * WGN == 8;
+    constexpr size_t kLdsMax = kLds + (kChunkStats ? kGnChunkLdsBytes : 0);
+    static_assert(kLdsMax <= 163840, "LDS exceeds 160 KB");
+    if (p.gn_avg != nullptr && !kChunkStats) return fail(H3V_EINVAL, "%s: no statistics epilogue for this tile", what);
+    const size_t lds = p.gn_avg != nullptr ? kLdsMax : kLds;
     auto kernel = &gemm_i8_mfma<BM, BN, BK, WGM, WGN, NSA, NSB, AM, EP>;
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, lds,
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsMax);
+    if (attr != hipSuccess) return fail(H3V_ELAUNCH, "%s: cannot reserve %zu bytes of LDS: %s", what, kLdsMax,
                                         hipGetErrorString(attr));
     const int splits = p.k_splits > 1 ? p.k_splits : 1;
     if ((p.K / BK) % splits != 0 || (splits > 1 && EP != Epi::F32Part))
@@ -2147,6 +2270,39 @@ int h3v_conv3d_f16_ws(const uint16_t* x, const uint16_t* w, const uint16_t* bias
                       hipStream_t stream) {
     return conv3d_f16_common(x, w, bias, residual, out, batch, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw,
                              causal_skip, workspace, workspace_floats, true, stream, "h3v_conv3d_f16_ws");
+}
+
+int h3v_conv3d_f16_gn(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int cin, int d,
+                      int h, int wd, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                      float* workspace, hipStream_t stream) {
+    const char* what = "h3v_conv3d_f16_gn";
+    H3V_REQUIRE(x && w && out && workspace, "%s: null pointer argument", what);
+    GemmParams p{};
+    int rc = fill_conv(p, what, 1, cin, d, h, wd, cout, kd, kh, kw, sd, sh, sw);
+    if (rc) return rc;
+    const int64_t hw = (int64_t)p.Ho * p.Wo;
+    H3V_REQUIRE(cout == 128 && hw % 256 == 0,
+                "%s: the chunk statistics need 128 output channels and an output frame of a multiple of 256 pixels "
+                "(got Cout %d, %d x %d)", what, cout, p.Ho, p.Wo);
+    H3V_REQUIRE(cin % 32 == 0 && aligned(x, 16) && aligned(w, 16) && aligned(out, 16) && aligned(workspace, 16),
+                "%s: requires Cin %% 32 == 0 and 16-byte aligned x, w, out and workspace (got Cin %d)", what, cin);
+    p.a = reinterpret_cast<const int8_t*>(x);
+    p.b = reinterpret_cast<const int8_t*>(w);
+    p.bias = bias;
+    p.out = out;
+    p.causal_skip = (causal_skip && kd == 3 && sd == 1) ? 1 : 0;
+    const GnWorkspace g = gn_workspace(workspace, p.Do, (int)hw, kGnSizingChunk);
+    p.gn_avg = g.avg;
+    p.gn_m2 = g.m2;
+    p.gn_ext = g.ext;
+    p.gn_nchunk = g.nchunk;
+    // the implicit GEMM on 256 x 128 tiles (one tile = one statistics chunk); these are the kernels
+    // h3v_conv3d_f16 itself runs for conv_in (64-byte K steps) and the stage-0 downsample
+    const bool k64 = (cin * 2) % 128 != 0;
+    p.C = cin * 2;
+    p.K = p.K * 2;
+    return k64 ? launch_tiled<256, 128, 64, 4, 2, 3, 2, AMode::Conv, Epi::F16Bias>(p, stream, what)
+               : launch_tiled<256, 128, 128, 4, 2, 2, 2, AMode::Conv, Epi::F16Bias>(p, stream, what);
 }
 
 int64_t h3v_conv3d_f16_workspace_floats(int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,

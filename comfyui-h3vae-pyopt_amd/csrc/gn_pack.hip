@@ -11,8 +11,10 @@
 //   gn_partial    grid (chunks, D): per 256-pixel chunk and group, avg and M2;
 //                 per chunk and channel max and min of the (pre-biased) input
 //                 (fp16, exact).  Skipped by h3v_gn_norm_pack_i8_partials, whose
-//                 caller's window conv (h3v_conv3d_i8_gn) already wrote the same
-//                 three arrays for its 512-pixel output tiles
+//                 caller's conv already wrote the same three arrays: the window
+//                 conv (h3v_conv3d_i8_gn) for its 512-pixel output tiles, or the
+//                 FP16 implicit-GEMM conv (h3v_conv3d_f16_gn) for 256-pixel
+//                 chunks in this pass's own order
 //   gn_merge      grid (32, D): Chan merge of the chunks -> (mean, rstd); the
 //                 per-channel extremes over the chunks give the group's absmax
 //                 candidate (below), one word per (frame, group); block (0, 0)
@@ -43,8 +45,10 @@
 // pixel lanes; lane pl owns pixels pl, pl+PL, ...; per pixel the group's
 // channels are summed left to right and added to the lane's running sum; the
 // lanes combine by the halving tree off = PL/2 .. 1; chunks merge sequentially.
-// The conv-epilogue partials follow their own fixed order (32 pixel lanes of a
-// 512-pixel tile, adjacent-pair tree), also restated by the oracle.
+// The window conv's epilogue partials follow their own fixed order (32 pixel
+// lanes of a 512-pixel tile, adjacent-pair tree), also restated by the oracle;
+// the FP16 implicit-GEMM conv's (h3v_conv3d_f16_gn) follow this pass's order on
+// 256-pixel chunks, so its partials are this pass's bit for bit.
 #include "h3v_common.hpp"
 #include "h3v_abi.hpp"
 
@@ -564,11 +568,11 @@ __global__ __launch_bounds__(kNT) void norm_pack_lut(const uint16_t* __restrict_
 // partial statistics of 512-pixel tiles, written by the window conv that produced x (h3v_conv3d_i8_gn).
 template <int C, bool PB>
 void launch_all(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma, const uint16_t* beta, float eps,
-                int d, int h, int w, int chunk, int8_t* q, float* scale, float* stats, float* ws, uint32_t* amax_bits,
-                hipStream_t stream) {
+                int d, int h, int w, int chunk, bool own_stats, int8_t* q, float* scale, float* stats, float* ws,
+                uint32_t* amax_bits, hipStream_t stream) {
     const int hw = h * w;
     const GnWorkspace g = gn_workspace(ws, d, hw, chunk);
-    if (chunk == kChunk)
+    if (own_stats)
         hipLaunchKernelGGL((gn_partial<C, PB>), dim3(g.nchunk, d), dim3(kNT), 0, stream, x, pre_bias, hw, g.nchunk,
                            g.avg, g.m2, g.ext);
     // block (0, 0) zeroes absmax_lut's counters; every candidate word is written
@@ -804,9 +808,11 @@ void launch_f16(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gam
 
 // ---------------------------------------------------------------------------
 // Checks and launch shared by h3v_gn_norm_pack_i8 and its no-allocation variant.
+// own_stats: run the statistics pass (gn_partial, 256-pixel chunks); otherwise the workspace already holds
+// the partials of `chunk`-pixel chunks, written by the conv that produced x.
 int run_norm_pack_i8(const char* what, const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
-                     const uint16_t* beta, float eps, int c, int d, int h, int w, int chunk, int8_t* q, float* scale,
-                     float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
+                     const uint16_t* beta, float eps, int c, int d, int h, int w, int chunk, bool own_stats, int8_t* q,
+                     float* scale, float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
     H3V_REQUIRE(x && gamma && beta && q && scale && stats, "%s: null pointer argument", what);
     H3V_REQUIRE(c == 128 || c == 256, "%s: C must be 128 or 256 (got %d)", what, c);
     H3V_REQUIRE(d >= 1 && h >= 2 && w >= 2, "%s: requires D >= 1 and H, W >= 2", what);
@@ -817,11 +823,11 @@ int run_norm_pack_i8(const char* what, const uint16_t* x, const uint16_t* pre_bi
                     aligned(q, 8),
                 "%s: x, gamma, beta, pre_bias need 16-byte and q 8-byte alignment", what);
     if (c == 128) {
-        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
-        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
+        if (pre_bias) launch_all<128, true>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, own_stats, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<128, false>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, own_stats, q, scale, stats, workspace, amax_scratch, stream);
     } else {
-        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
-        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, q, scale, stats, workspace, amax_scratch, stream);
+        if (pre_bias) launch_all<256, true>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, own_stats, q, scale, stats, workspace, amax_scratch, stream);
+        else launch_all<256, false>(x, pre_bias, gamma, beta, eps, d, h, w, chunk, own_stats, q, scale, stats, workspace, amax_scratch, stream);
     }
     return launch_status(what);
 }
@@ -866,20 +872,25 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
     const char* what = "h3v_gn_norm_pack_i8";
     H3V_REQUIRE(workspace && amax_scratch, "%s: null pointer argument", what);
     H3V_REQUIRE(aligned(workspace, 16), "%s: workspace needs 16-byte alignment", what);
-    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kChunk, q, scale, stats, workspace,
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kChunk, true, q, scale, stats, workspace,
                             amax_scratch, stream);
 }
 
 int h3v_gn_norm_pack_i8_partials(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
-                                 const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
-                                 float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream) {
+                                 const uint16_t* beta, float eps, int c, int d, int h, int w, int chunk, int8_t* q,
+                                 float* scale, float* stats, float* workspace, uint32_t* amax_scratch,
+                                 hipStream_t stream) {
     const char* what = "h3v_gn_norm_pack_i8_partials";
     H3V_REQUIRE(workspace && amax_scratch, "%s: null pointer argument", what);
     H3V_REQUIRE(aligned(workspace, 16), "%s: workspace needs 16-byte alignment", what);
-    H3V_REQUIRE(h >= 8 && ((int64_t)h * w) % kGnTileChunk == 0,
-                "%s: the partial statistics are those of %d-pixel conv tiles: H * W must be a multiple of %d and "
-                "H at least 8 (got %d x %d)", what, kGnTileChunk, kGnTileChunk, h, w);
-    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kGnTileChunk, q, scale, stats, workspace,
+    H3V_REQUIRE(chunk == kGnTileChunk || chunk == kChunk,
+                "%s: chunk must be %d (window-conv tiles) or %d (pixel runs of h3v_conv3d_f16_gn) (got %d)", what,
+                kGnTileChunk, kChunk, chunk);
+    H3V_REQUIRE(chunk == kChunk || h >= 8, "%s: %d-pixel tiles need H at least 8 (got %d)", what, kGnTileChunk, h);
+    H3V_REQUIRE(((int64_t)h * w) % chunk == 0,
+                "%s: the partial statistics are those of %d-pixel chunks: H * W must be a multiple of %d (got %d x %d)",
+                what, chunk, chunk, h, w);
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, chunk, false, q, scale, stats, workspace,
                             amax_scratch, stream);
 }
 
@@ -897,7 +908,7 @@ int h3v_gn_norm_pack_i8_noalloc(const uint16_t* x, const uint16_t* pre_bias, con
     const int rc = scratch_for_current_device(what, &base);
     if (rc != H3V_OK) return rc;
     // word 0: the absmax key; the workspace starts 256 bytes in (16-byte alignment kept)
-    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kChunk, q, scale, stats,
+    return run_norm_pack_i8(what, x, pre_bias, gamma, beta, eps, c, d, h, w, kChunk, true, q, scale, stats,
                             base + kScratchHeadFloats, reinterpret_cast<uint32_t*>(base), stream);
 }
 

@@ -21,7 +21,7 @@ kernel (``h3v_tap_fold_pack``), leaving a 3x1x1 conv with K = 96.
 """
 from __future__ import annotations
 
-from typing import List, Optional
+from typing import List, Optional, Tuple
 
 import torch
 import torch.nn.functional as F
@@ -120,6 +120,48 @@ def _fake_conv(x, w_packed, bias, kernel_size, stride, causal_skip, residual=Non
     _check_conv(x, w_packed, bias, kernel_size, stride, residual)
     return torch.empty(_out_shape(x, w_packed, kernel_size, stride), device=x.device, dtype=x.dtype,
                        memory_format=torch.channels_last_3d)
+
+
+def conv3d_f16_gn_fits(x, w_packed, kernel_size, stride):
+    """Whether ``conv3d_f16_gn`` takes this conv: one clip, 128 output channels, output frames of a multiple
+    of 256 pixels, Cin % 32 == 0."""
+    if x.ndim != 5 or w_packed.ndim != 2:
+        return False
+    b, c, _, _, _ = x.shape
+    _, _, do, ho, wo = _out_shape(x, w_packed, kernel_size, stride)
+    return b == 1 and c % 32 == 0 and w_packed.shape[0] == 128 and do >= 1 and (ho * wo) % 256 == 0
+
+
+@torch.library.custom_op("h3vae_encoder::conv3d_f16_gn", mutates_args=(), device_types="cuda")
+def conv3d_f16_gn(x: torch.Tensor, w_packed: torch.Tensor, bias: Optional[torch.Tensor], kernel_size: List[int],
+                  stride: List[int], causal_skip: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``conv3d_f16`` (no residual) that also writes the GroupNorm(32) partial statistics of its output for the
+    INT8 producer that normalises it next (``h3v_conv3d_f16_gn``): -> (out, workspace), the workspace in that
+    producer's layout over 256-pixel chunks, in the order of its own statistics pass, so the producer's
+    results are bit-identical to those of its own pass.  ``conv3d_f16_gn_fits`` geometry only."""
+    _check_conv(x, w_packed, bias, kernel_size, stride)
+    if not conv3d_f16_gn_fits(x, w_packed, kernel_size, stride):
+        raise ValueError(f"conv3d_f16_gn: input {tuple(x.shape)}, Cout {w_packed.shape[0]} is outside its gate "
+                         "(one clip, Cout 128, output frames of a multiple of 256 pixels)")
+    _hip.require_gfx950(x.device, "conv3d_f16_gn")
+    if not x.is_contiguous(memory_format=torch.channels_last_3d):
+        x = x.contiguous(memory_format=torch.channels_last_3d)
+    _, c, d, h, w = x.shape
+    shape = _out_shape(x, w_packed, kernel_size, stride)
+    out = torch.empty(shape, device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d)
+    floats = int(_hip.lib().h3v_gn_norm_pack_workspace_floats(*shape[2:]))
+    ws = torch.empty(floats, device=x.device, dtype=torch.float32)
+    _hip.call("h3v_conv3d_f16_gn", _hip.ptr(x), _hip.ptr(w_packed), _hip.ptr(bias), _hip.ptr(out), c, d, h, w,
+              w_packed.shape[0], *kernel_size, *stride, int(bool(causal_skip)), _hip.ptr(ws), _hip.stream(x.device))
+    return out, ws
+
+
+@conv3d_f16_gn.register_fake
+def _fake_conv_gn(x, w_packed, bias, kernel_size, stride, causal_skip):
+    _check_conv(x, w_packed, bias, kernel_size, stride)
+    shape = _out_shape(x, w_packed, kernel_size, stride)
+    return (torch.empty(shape, device=x.device, dtype=x.dtype, memory_format=torch.channels_last_3d),
+            x.new_empty((0,), dtype=torch.float32))
 
 
 def _check_pack(x, front, pads):
@@ -255,6 +297,21 @@ class NativeConv(nn.Module):
         return conv3d_f16(x, self.packed_weight(self.weight), self.bias if with_bias else None, kernel,
                           list(self.stride), skip, residual)
 
+    def forward_partials(self, x, *, causal_skip=False):
+        """``(forward(x), partials)``: where ``conv3d_f16_gn`` takes the geometry, the conv also writes the
+        GroupNorm statistics of its output (``GnPartials`` over 256-pixel chunks) for the INT8 norm that reads
+        it next; otherwise ``(forward(x), None)``."""
+        _require_native(x, "FP16 encoder convolution")
+        kernel = list(self.weight.shape[2:])
+        packed = self.packed_weight(self.weight)
+        if not conv3d_f16_fits(x, self.weight, self.stride) or not conv3d_f16_gn_fits(x, packed, kernel,
+                                                                                      self.stride):
+            return self.forward(x, causal_skip=causal_skip), None
+        from .encoder_int8_norm import PIXEL_CHUNK, GnPartials
+        skip = bool(causal_skip) and kernel[0] == 3 and self.stride[0] == 1
+        out, ws = conv3d_f16_gn(x, packed, self.bias, kernel, list(self.stride), skip)
+        return out, GnPartials(ws, PIXEL_CHUNK)
+
 
 class PointwiseConv(nn.Module):
     """A 1x1x1 ``nn.Conv3d`` over channels-last-3d activations.
@@ -333,17 +390,30 @@ class PaddedCausalConv(nn.Module):
             self.conv = NativeConv(weight, bias, stride)
 
     def forward(self, x, front):
+        return self.forward_partials(x, front, want=False)[0]
+
+    def forward_partials(self, x, front, want=True):
+        """``(forward(x, front), partials)``: with ``want`` and where ``conv3d_f16_gn`` takes the conv, it also
+        writes the GroupNorm statistics of its output (``GnPartials``, 256-pixel chunks) for the INT8 norm that
+        reads it next; otherwise partials is None."""
         _require_native(x, "padded causal convolution")
         if self.folded:
             if min(x.shape[3:]) < 2:
                 raise ValueError("conv_in requires H, W >= 2")
-            return conv3d_f16(tap_fold_pack(x, front), self.packed_weight(self.weight), self.bias, [3, 1, 1],
-                              [1, 1, 1], front == 2)
+            folded, packed = tap_fold_pack(x, front), self.packed_weight(self.weight)
+            if want and conv3d_f16_gn_fits(folded, packed, [3, 1, 1], [1, 1, 1]):
+                from .encoder_int8_norm import PIXEL_CHUNK, GnPartials
+                out, ws = conv3d_f16_gn(folded, packed, self.bias, [3, 1, 1], [1, 1, 1], front == 2)
+                return out, GnPartials(ws, PIXEL_CHUNK)
+            return conv3d_f16(folded, packed, self.bias, [3, 1, 1], [1, 1, 1], front == 2), None
         top, bottom, left, right = self.border
         written = padded_input_of(x, front, self.border)
-        if written is not None:   # the producing conv already wrote this conv's padded input
-            return self.conv(written, causal_skip=front == 2)
-        if x.shape[1] % 8 or max(top, bottom) >= x.shape[3] or max(left, right) >= x.shape[4]:
-            raise ValueError(f"padded causal convolution: input {tuple(x.shape)} needs C % 8 == 0 and a reflect "
-                             f"border {self.border} smaller than H, W")
-        return self.conv(causal_reflect_pack(x, front, top, bottom, left, right), causal_skip=front == 2)
+        if written is None:
+            if x.shape[1] % 8 or max(top, bottom) >= x.shape[3] or max(left, right) >= x.shape[4]:
+                raise ValueError(f"padded causal convolution: input {tuple(x.shape)} needs C % 8 == 0 and a "
+                                 f"reflect border {self.border} smaller than H, W")
+            written = causal_reflect_pack(x, front, top, bottom, left, right)
+        # (else the producing conv already wrote this conv's padded input)
+        if want:
+            return self.conv.forward_partials(written, causal_skip=front == 2)
+        return self.conv(written, causal_skip=front == 2), None

@@ -125,25 +125,26 @@ def int8_norm_conv3d_residual_padded(x: torch.Tensor, norm_weight: torch.Tensor,
                                      weight_scale: torch.Tensor, bias: torch.Tensor | None,
                                      residual: torch.Tensor | None, residual_bias: torch.Tensor | None,
                                      front: int, border: list[int],
-                                     x_partials: torch.Tensor | None) -> torch.Tensor:
+                                     x_partials: torch.Tensor | None, x_chunk: int) -> torch.Tensor:
     """The last conv of an encoder stage written as the padded input of the stage's causal stride-2
     downsample: ``[B, Cout, D + front, H + top + bottom, W + left + right]``, zero leading frames, a reflect
     border (top, bottom, left, right) of 0 or 1 per side.  The
     residual add is that of ``int8_norm_conv3d_residual``, or with ``residual_bias`` the stage-1 residual
     pack's ``residual + (out + bias)`` (opt/encoder_fused_residual_pack.py:12-33); the pack kernel that
     would re-read the conv output (there, or ``causal_reflect_pack`` before the stage-0 downsample) is
-    not run.  ``x_partials``: GroupNorm tile statistics of ``x`` as in ``int8_norm_conv3d_tiles``."""
+    not run.  ``x_partials``, ``x_chunk``: GroupNorm statistics of ``x`` as in ``int8_norm_conv3d_tiles``."""
     from .encoder_int8 import _conv3d_from_quantized_padded
-    from .encoder_int8_norm import quantized_temporal_norm_pad
+    from .encoder_int8_norm import GnPartials, quantized_temporal_norm_pad
 
-    qx, scale = quantized_temporal_norm_pad(x, norm_weight, norm_bias, eps, pre_bias=pre_bias, partials=x_partials)
+    partials = None if x_partials is None else GnPartials(x_partials, int(x_chunk))
+    qx, scale = quantized_temporal_norm_pad(x, norm_weight, norm_bias, eps, pre_bias=pre_bias, partials=partials)
     return _conv3d_from_quantized_padded(qx, scale, qweight, weight_scale, bias=bias, residual=residual,
                                          residual_bias=residual_bias, front=int(front), border=border)
 
 
 @int8_norm_conv3d_residual_padded.register_fake
 def _int8_norm_conv3d_residual_padded_fake(x, norm_weight, norm_bias, pre_bias, eps, qweight, weight_scale, bias,
-                                           residual, residual_bias, front, border, x_partials):
+                                           residual, residual_bias, front, border, x_partials, x_chunk):
     b, _, d, h, w = x.shape
     top, bottom, left, right = border
     return torch.empty((b, qweight.shape[0], d + int(front), h + top + bottom, w + left + right), device=x.device,
@@ -154,17 +155,19 @@ def _int8_norm_conv3d_residual_padded_fake(x, norm_weight, norm_bias, pre_bias, 
 def int8_norm_conv3d_tiles(x: torch.Tensor, norm_weight: torch.Tensor, norm_bias: torch.Tensor,
                            pre_bias: torch.Tensor | None, eps: float, qweight: torch.Tensor,
                            weight_scale: torch.Tensor, bias: torch.Tensor | None, residual: torch.Tensor | None,
-                           x_partials: torch.Tensor | None, emit: bool,
+                           x_partials: torch.Tensor | None, x_chunk: int, emit: bool,
                            partials_bias: torch.Tensor | None) -> tuple[torch.Tensor, torch.Tensor]:
-    """``int8_norm_conv3d`` (or ``_residual``) with GroupNorm tile statistics on either side: the producer
-    reads those of ``x`` from ``x_partials`` (written by the conv that produced ``x``, with ``pre_bias`` as
-    its statistics bias; the workspace is reused by the producer) instead of its own statistics pass, and
-    with ``emit`` the conv writes those of its output plus ``partials_bias`` into the returned workspace
-    (``gn_stats_fits`` geometry; without ``emit`` the second output is empty)."""
+    """``int8_norm_conv3d`` (or ``_residual``) with GroupNorm statistics on either side: the producer reads
+    those of ``x`` from ``x_partials`` (written by the conv that produced ``x`` over ``x_chunk``-pixel chunks,
+    with ``pre_bias`` as its statistics bias; the workspace is reused by the producer) instead of its own
+    statistics pass, and with ``emit`` the conv writes those of its output's 512-pixel tiles plus
+    ``partials_bias`` into the returned workspace (``gn_stats_fits`` geometry; without ``emit`` the second
+    output is empty)."""
     from .encoder_int8 import gn_workspace_floats
-    from .encoder_int8_norm import quantized_temporal_norm_pad
+    from .encoder_int8_norm import GnPartials, quantized_temporal_norm_pad
 
-    qx, scale = quantized_temporal_norm_pad(x, norm_weight, norm_bias, eps, pre_bias=pre_bias, partials=x_partials)
+    partials = None if x_partials is None else GnPartials(x_partials, int(x_chunk))
+    qx, scale = quantized_temporal_norm_pad(x, norm_weight, norm_bias, eps, pre_bias=pre_bias, partials=partials)
     ws = None
     if emit:
         ws = torch.empty((gn_workspace_floats(*x.shape[2:]),), device=x.device, dtype=torch.float32)
@@ -177,7 +180,7 @@ def int8_norm_conv3d_tiles(x: torch.Tensor, norm_weight: torch.Tensor, norm_bias
 
 @int8_norm_conv3d_tiles.register_fake
 def _int8_norm_conv3d_tiles_fake(x, norm_weight, norm_bias, pre_bias, eps, qweight, weight_scale, bias, residual,
-                                 x_partials, emit, partials_bias):
+                                 x_partials, x_chunk, emit, partials_bias):
     out = torch.empty((x.shape[0], qweight.shape[0], *x.shape[2:]), device=x.device, dtype=x.dtype,
                       memory_format=torch.channels_last_3d)
     return out, x.new_empty((0,), dtype=torch.float32)
@@ -235,11 +238,11 @@ class Int8FusedValidConv3d(nn.Module):
         ``pad_front`` and ``pad_border`` (with ``residual_bias`` optional) return the padded input of the
         stage's downsample instead (``int8_norm_conv3d_residual_padded``).
 
-        GroupNorm tile statistics (``int8_norm_conv3d_tiles``): ``x_partials`` holds those of ``x``, written
-        by the conv that produced ``x`` with ``pre_bias`` as its statistics bias; with ``emit_partials``
-        the call returns ``(out, partials)``, ``partials`` the statistics of ``out`` plus ``partials_bias``
-        for the norm that reads ``out``, or None where the conv's geometry has no statistics epilogue
-        (``gn_stats_fits``)."""
+        GroupNorm statistics (``int8_norm_conv3d_tiles``): ``x_partials`` (``GnPartials``) holds those of ``x``,
+        written by the conv that produced ``x`` with ``pre_bias`` as its statistics bias; with
+        ``emit_partials`` the call returns ``(out, partials)``, ``partials`` the tile statistics of ``out``
+        plus ``partials_bias`` for the norm that reads ``out``, or None where the conv's geometry has no
+        statistics epilogue (``gn_stats_fits``)."""
         if not self.fuse_norm:
             raise RuntimeError("INT8 norm fusion is not enabled for this convolution")
         if x.dtype != torch.float16:
@@ -247,12 +250,14 @@ class Int8FusedValidConv3d(nn.Module):
         if x.device != self.qweight.device:
             raise RuntimeError("INT8 encoder activation and qweight must be on the same device")
         bias = self.bias if self.apply_bias else None
+        from .encoder_int8_norm import TILE_CHUNK, GnPartials
+        x_ws, x_chunk = (None, TILE_CHUNK) if x_partials is None else x_partials
         if pad_front is not None:
             if emit_partials:
                 raise ValueError("the padded form writes no tile statistics")
             return int8_norm_conv3d_residual_padded(x, norm_weight, norm_bias, pre_bias, eps, self.qweight,
                                                     self.weight_scale, bias, residual, residual_bias, int(pad_front),
-                                                    [int(v) for v in pad_border], x_partials)
+                                                    [int(v) for v in pad_border], x_ws, int(x_chunk))
         if residual_bias is not None:
             raise ValueError("residual_bias is only taken with pad_front")
         if x_partials is not None or emit_partials:
@@ -261,9 +266,11 @@ class Int8FusedValidConv3d(nn.Module):
             emit = bool(emit_partials) and gn_stats_fits(self.config.in_channels, self.config.out_channels, d, h, w,
                                                          batch=b)
             out, partials = int8_norm_conv3d_tiles(x, norm_weight, norm_bias, pre_bias, eps, self.qweight,
-                                                   self.weight_scale, bias, residual, x_partials, emit,
+                                                   self.weight_scale, bias, residual, x_ws, int(x_chunk), emit,
                                                    partials_bias if emit else None)
-            return (out, partials if emit else None) if emit_partials else out
+            if not emit_partials:
+                return out
+            return out, (GnPartials(partials, TILE_CHUNK) if emit else None)
         if partials_bias is not None:
             raise ValueError("partials_bias is only taken with emit_partials")
         if residual is not None:

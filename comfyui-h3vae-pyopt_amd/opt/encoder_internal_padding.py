@@ -17,11 +17,17 @@ downsample conv of the prefix and of the suffix stages the same way.
 """
 from __future__ import annotations
 
+import contextlib
 from dataclasses import dataclass
 
 import torch
 
 from .encoder_fp16_conv import PaddedCausalConv
+
+
+@dataclass
+class _PartialsSlot:
+    partials: object = None
 
 
 def _reflect_border(conv):
@@ -50,9 +56,32 @@ class ImplicitTemporalPadConv3d(torch.nn.Module):
         # zero frames in front of a clip / of a single image
         self.front_video, self.front_image = 2 * self.padding[0], self.kernel_size[0] - 1
         self.native = PaddedCausalConv(self.weight, self.bias, self.stride, _reflect_border(original))
+        self._partials_slot = None
 
     def forward(self, x):
-        return self.native(x, self.front_video if x.shape[2] > 1 else self.front_image)
+        front = self.front_video if x.shape[2] > 1 else self.front_image
+        slot = self._partials_slot
+        if slot is not None:
+            out, slot.partials = self.native.forward_partials(x, front)
+            return out
+        return self.native(x, front)
+
+    def forward_partials(self, x):
+        """``(forward(x), partials)``: the conv also writes the GroupNorm statistics of its output for the INT8
+        norm that reads it next (``GnPartials``), or None where its geometry has no statistics epilogue."""
+        return self.native.forward_partials(x, self.front_video if x.shape[2] > 1 else self.front_image)
+
+    @contextlib.contextmanager
+    def partials_requested(self):
+        """Inside the block, a call of this conv by the module that owns it (the model's downsample module
+        calls it as ``self.conv(x)``) also forms the statistics of ``forward_partials`` and leaves them in the
+        yielded slot's ``partials``."""
+        slot = _PartialsSlot()
+        self._partials_slot = slot
+        try:
+            yield slot
+        finally:
+            self._partials_slot = None
 
     def padded_input_form(self, x):
         """(front, border) of the padded input this conv builds for ``x`` when its reflect border is 0 or 1

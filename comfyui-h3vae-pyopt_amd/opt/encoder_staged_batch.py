@@ -22,21 +22,39 @@ _VALIDATED = ((1, 1), (1, 2), (2, 1), (2, 2), (2, 4))
 _CL3D = torch.channels_last_3d
 
 
-def _run_stages(stages, h):
+def _reads_partials(stage):
+    """Whether the first block of ``stage`` normalises its input through the INT8 producer, which can take the
+    input's GroupNorm statistics from the conv that wrote it instead of its own statistics pass."""
+    blocks = getattr(stage, "block", None)
+    if not blocks or getattr(blocks[0], "forward_partials", None) is None:
+        return False
+    first = getattr(blocks[0], "int8_first", None)
+    return first is not None and bool(getattr(first, "fuse_norm", False))
+
+
+def _run_stages(stages, h, partials=None):
     """Every residual block of each stage in order, then the stage's downsample if it has one.  Blocks with
-    ``forward_partials`` (the INT8 prefix blocks) hand the GroupNorm tile statistics of their output,
-    written by their last conv, to the next block's first norm."""
-    for stage in stages:
-        partials = None
+    ``forward_partials`` (the INT8 prefix blocks) hand the GroupNorm statistics of their output, written by
+    their last conv, to the next block's first norm.  ``partials``: the statistics of ``h`` (written by
+    conv_in) for the first block; a downsample conv forms those of its output when the next stage's first
+    block reads them."""
+    for i, stage in enumerate(stages):
         for block in stage.block:
             step = getattr(block, "forward_partials", None)
             if step is not None:
                 h, partials = step(h, partials)
             else:
                 h, partials = block(h), None
+        partials = None
         downsample = getattr(stage, "downsample", None)
         if downsample is not None:
-            h = downsample(h)
+            request = getattr(getattr(downsample, "conv", None), "partials_requested", None)
+            if request is not None and i + 1 < len(stages) and _reads_partials(stages[i + 1]):
+                with request() as slot:
+                    h = downsample(h)
+                partials = slot.partials
+            else:
+                h = downsample(h)
     return h
 
 
@@ -53,7 +71,13 @@ class EncoderPrefix(torch.nn.Module):
         self.stages = torch.nn.ModuleList(encoder.down[i] for i in range(cut))
 
     def forward(self, x):
-        return _run_stages(self.stages, self.conv_in(x.contiguous(memory_format=_CL3D)))
+        x = x.contiguous(memory_format=_CL3D)
+        step = getattr(self.conv_in, "forward_partials", None)
+        if step is not None and len(self.stages) and _reads_partials(self.stages[0]):
+            h, partials = step(x)
+        else:
+            h, partials = self.conv_in(x), None
+        return _run_stages(self.stages, h, partials)
 
 
 class EncoderSuffix(torch.nn.Module):

@@ -24,7 +24,7 @@
 extern "C" {
 #endif
 
-#define H3V_ABI_VERSION 4
+#define H3V_ABI_VERSION 5
 
 #define H3V_OK 0
 #define H3V_EINVAL 1   /* shape / dtype / alignment / contract violation */
@@ -119,6 +119,20 @@ int h3v_conv3d_f16_ws(const uint16_t* x, const uint16_t* w, const uint16_t* bias
  * does not split, -1 for an invalid geometry (h3v_last_error says why). */
 int64_t h3v_conv3d_f16_workspace_floats(int batch, int cin, int d, int h, int wd, int cout, int kd, int kh, int kw,
                                         int sd, int sh, int sw);
+
+/* h3v_conv3d_f16 (batch one, no residual, 128 output channels, an output
+ * frame of a multiple of 256 pixels) that also writes the GroupNorm(32)
+ * partial statistics of its output for the INT8 producer that normalises it
+ * next: `workspace` (h3v_gn_norm_pack_workspace_floats of the output's
+ * [d, h, w], 16-byte aligned) receives, per 256-pixel chunk of a frame, the
+ * group averages and M2 and the channel max / min, in the order of that
+ * producer's own statistics pass; hand it to h3v_gn_norm_pack_i8_partials
+ * with chunk = 256 and no pre_bias.  Replaces the `_partial` launch of
+ * _norm_statistics (opt/encoder_int8_norm.py:16-50) that follows conv_in and
+ * the stage-0 downsample (the model's convs at opt/encoder_internal_padding.py:34). */
+int h3v_conv3d_f16_gn(const uint16_t* x, const uint16_t* w, const uint16_t* bias, uint16_t* out, int cin, int d,
+                      int h, int wd, int cout, int kd, int kh, int kw, int sd, int sh, int sw, int causal_skip,
+                      float* workspace, hipStream_t stream);
 
 /* ---- decoder attention (head_dim 64) --------------------------------------
  * Replaces the model's `perform_attention` (flash attention) called from
@@ -281,16 +295,21 @@ int h3v_gn_norm_pack_i8(const uint16_t* x, const uint16_t* pre_bias, const uint1
                         float eps, int c, int d, int h, int w, int8_t* q, float* scale, float* stats,
                         float* workspace, uint32_t* amax_scratch, hipStream_t stream);
 
-/* h3v_gn_norm_pack_i8 on an input written by h3v_conv3d_i8_gn: `workspace`
- * holds the partial statistics of x's 512-pixel tiles (h * w a multiple of
- * 512, h >= 8), summed over x + pre_bias with the same pre_bias; the
- * statistics pass is skipped and the tiles merge in order (8-row bands of
- * 64-column blocks).  Same outputs as h3v_gn_norm_pack_i8 up to the
- * summation order of the statistics.  Replaces quantized_temporal_norm_pad
- * (opt/encoder_int8_norm.py:77-110) after the fused conv. */
+/* h3v_gn_norm_pack_i8 on an input whose producing conv wrote its GroupNorm
+ * partial statistics into `workspace` (summed over x + pre_bias with the same
+ * pre_bias); the statistics pass is skipped and the chunks merge in order.
+ * chunk = 512: the 512-pixel tiles of h3v_conv3d_i8_gn (h * w a multiple of
+ * 512, h >= 8; 8-row bands of 64-column blocks), the same outputs as
+ * h3v_gn_norm_pack_i8 up to the summation order of the statistics;
+ * chunk = 256: the 256-pixel chunks of h3v_conv3d_f16_gn (h * w a multiple
+ * of 256), written in the statistics pass's own order, so the outputs are
+ * bit-identical to h3v_gn_norm_pack_i8's.  Replaces
+ * quantized_temporal_norm_pad (opt/encoder_int8_norm.py:77-110) after the
+ * fused conv. */
 int h3v_gn_norm_pack_i8_partials(const uint16_t* x, const uint16_t* pre_bias, const uint16_t* gamma,
-                                 const uint16_t* beta, float eps, int c, int d, int h, int w, int8_t* q, float* scale,
-                                 float* stats, float* workspace, uint32_t* amax_scratch, hipStream_t stream);
+                                 const uint16_t* beta, float eps, int c, int d, int h, int w, int chunk, int8_t* q,
+                                 float* scale, float* stats, float* workspace, uint32_t* amax_scratch,
+                                 hipStream_t stream);
 
 /* h3v_gn_norm_pack_i8 without a workspace argument and without allocating:
  * no counterpart in the reference.  It is for callers that cannot allocate

@@ -171,7 +171,7 @@ def test_encoder_fake_shapes(ops):
     y = integ.int8_norm_conv3d_residual_padded(x, torch.empty(128, dtype=torch.float16, device="meta"),
                                                torch.empty(128, dtype=torch.float16, device="meta"), None, 1e-6, qw,
                                                torch.empty(256, device="meta"), None, None, None, 2, [0, 1, 0, 1],
-                                               None)
+                                               None, 512)
     assert tuple(y.shape) == (1, 256, 7, 9, 11)      # two leading frames, one reflected row and column
     assert y.is_contiguous(memory_format=torch.channels_last_3d)
 

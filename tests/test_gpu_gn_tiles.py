@@ -127,7 +127,7 @@ def test_norm_pack_partials_matches_oracle(ops, oracle, c, d, h, w, pre):
     stats = torch.empty((d, 32, 2), device=DEV)
     scratch = torch.empty(1, dtype=torch.int32, device=DEV)
     hip.call("h3v_gn_norm_pack_i8_partials", hip.ptr(xd), hip.ptr(pbd), hip.ptr(gd), hip.ptr(bd), 1e-6, c, d, h, w,
-             hip.ptr(q), hip.ptr(scale), hip.ptr(stats), hip.ptr(ws), hip.ptr(scratch), hip.stream(DEV))
+             512, hip.ptr(q), hip.ptr(scale), hip.ptr(stats), hip.ptr(ws), hip.ptr(scratch), hip.stream(DEV))
     torch.cuda.synchronize()
     rstats = oracle.gn_stats_tiled(xn, 1e-6, pbn)
     assert np.array_equal(np_(stats).view(np.uint32), rstats.view(np.uint32)), "stats"
@@ -143,7 +143,13 @@ def test_norm_pack_partials_rejects_untiled_frames(ops):
     z = torch.zeros(16, device=DEV)
     with pytest.raises(ValueError, match="multiple of 512"):
         hip.call("h3v_gn_norm_pack_i8_partials", hip.ptr(z), None, hip.ptr(z), hip.ptr(z), 1e-6, 128, 1, 8, 40,
-                 hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.stream(DEV))
+                 512, hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.stream(DEV))
+    with pytest.raises(ValueError, match="multiple of 256"):
+        hip.call("h3v_gn_norm_pack_i8_partials", hip.ptr(z), None, hip.ptr(z), hip.ptr(z), 1e-6, 128, 1, 8, 40,
+                 256, hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.stream(DEV))
+    with pytest.raises(ValueError, match="chunk must be"):
+        hip.call("h3v_gn_norm_pack_i8_partials", hip.ptr(z), None, hip.ptr(z), hip.ptr(z), 1e-6, 128, 1, 8, 64,
+                 128, hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.ptr(z), hip.stream(DEV))
 
 
 # -- the encoder blocks ----------------------------------------------------------------------------------
