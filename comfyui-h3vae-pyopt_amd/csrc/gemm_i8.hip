@@ -1308,6 +1308,30 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
         uint16_t* out = static_cast<uint16_t*>(p.out);
         const int c8 = lane & 7;
         const int gcol = cbase + c8 * 8;
+        if (p.vec_out && cbase + 64 <= p.N && p.ldo <= (1 << 20)) {
+            // The wave's 64 columns lie inside N (every decoder GEMM): all 16 row pieces are read from LDS
+            // first, then stored from one wave-uniform base with 32-bit offsets, so no store waits for its
+            // own LDS read and no per-row 64-bit address is formed.  Rows past M (the last row of tiles)
+            // are skipped.
+            u16x8 v[16];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                const int r = t * 8 + (lane >> 3);
+                v[t] = *reinterpret_cast<const u16x8*>(stage + r * 128 + ((c8 ^ ((r >> 1) & 7)) << 4));
+            }
+            uint16_t* const base = out + (int64_t)rbase * p.ldo + cbase;   // wave-uniform
+            const int rows = p.M - rbase;   // wave-uniform; 128 or fewer in the last row of tiles (even <= 0)
+            const int off = (lane >> 3) * (int)p.ldo + c8 * 8;
+            if (rows >= 128) {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) *reinterpret_cast<u16x8*>(base + off + t * 8 * (int)p.ldo) = v[t];
+            } else {
+#pragma unroll
+                for (int t = 0; t < 16; ++t)
+                    if (t * 8 + (lane >> 3) < rows) *reinterpret_cast<u16x8*>(base + off + t * 8 * (int)p.ldo) = v[t];
+            }
+            return;
+        }
 #pragma unroll 4
         for (int t = 0; t < 16; ++t) {
             const int r = t * 8 + (lane >> 3);
