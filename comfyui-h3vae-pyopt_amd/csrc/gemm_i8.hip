@@ -531,13 +531,16 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 }
                 u16x8 gb{};
                 if (p.gn_bias) gb = *reinterpret_cast<const u16x8*>(p.gn_bias + gcol);
+                // tile row r is output row m0 + (r / TILEW) * Wo + r % TILEW: 32-bit element offsets from the
+                // tile's first row (at most 8 * 256 rows of 256 channels)
+                uint16_t* const tile_out = out + (int64_t)m0 * p.ldo + gcol;
                 lds_barrier();   // the output tile is complete in LDS
 #pragma unroll
                 for (int k = 0; k < PER; ++k) {
                     const int r = (tid >> 4) + 32 * k;
                     u16x8 y = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
                     if (p.res != nullptr) y = add_f16x8(v[k], y);   // fp16(res + y), one rounding
-                    *reinterpret_cast<u16x8*>(out + (int64_t)gidx(r) * p.ldo + gcol) = y;
+                    *reinterpret_cast<u16x8*>(tile_out + ((r / TILEW) * p.Wo + r % TILEW) * (int)p.ldo) = y;
                     v[k] = p.gn_bias ? add_f16x8(y, gb) : y;
                 }
                 const int fpix = p.Ho * p.Wo;
@@ -648,19 +651,44 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
         }
         if (p.res == nullptr) {
             lds_barrier();   // the output tile is complete in LDS
-#pragma unroll 4
-            for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
-                const int r = idx / RCH, ch = idx - r * RCH;
-                const int grow = gidx(r), gcol = gcol0 + ch * 8;
-                if (grow >= p.M || gcol >= p.N) continue;
-                const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
-                if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
-                    store_chunk(r, grow, gcol, v);
-                } else {
-                    uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+            constexpr int NT = NW * 64;
+            if (PADWO == 0 && (BM * RCH) % NT == 0 && NT % RCH == 0 && p.vec_out && gcol0 + OUTW <= p.N &&
+                p.ldo <= 65536) {
+                // Every column of the tile lies inside N: a thread keeps one 8-column chunk for all its rows,
+                // reads all its pieces from LDS first and stores them from the tile's first output row with
+                // 32-bit element offsets (the tile spans at most 512 consecutive rows, or 8 rows of a frame at
+                // most 256 wide); rows past M (the last tile of a GEMM) are skipped.
+                constexpr int PER = BM * RCH / NT;
+                const int ch = tid % RCH;
+                uint16_t* const tile_out = out + (int64_t)m0 * p.ldo + gcol0 + ch * 8;
+                u16x8 v[PER];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e)
-                        if (gcol + e < p.N) dst[e] = v[e];
+                for (int k = 0; k < PER; ++k) {
+                    const int r = (tid + k * NT) / RCH;
+                    v[k] = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
+                }
+                const int rows = p.M - m0;
+#pragma unroll
+                for (int k = 0; k < PER; ++k) {
+                    const int r = (tid + k * NT) / RCH;
+                    const int orow = TILEW ? (r / (TILEW ? TILEW : 1)) * p.Wo + r % (TILEW ? TILEW : 1) : r;
+                    if (TILEW || r < rows) *reinterpret_cast<u16x8*>(tile_out + orow * (int)p.ldo) = v[k];
+                }
+            } else {
+#pragma unroll 4
+                for (int idx = tid; idx < BM * RCH; idx += NW * 64) {
+                    const int r = idx / RCH, ch = idx - r * RCH;
+                    const int grow = gidx(r), gcol = gcol0 + ch * 8;
+                    if (grow >= p.M || gcol >= p.N) continue;
+                    const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
+                    if (PADWO > 0 || (p.vec_out && gcol + 8 <= p.N)) {
+                        store_chunk(r, grow, gcol, v);
+                    } else {
+                        uint16_t* dst = out + (int64_t)grow * p.ldo + gcol;
+#pragma unroll
+                        for (int e = 0; e < 8; ++e)
+                            if (gcol + e < p.N) dst[e] = v[e];
+                    }
                 }
             }
             // Chunk statistics (h3v_conv3d_f16_gn: 256 x 128 tiles of 8 waves, 128 output channels, every tile
