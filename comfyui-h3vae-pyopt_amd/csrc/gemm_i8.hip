@@ -535,13 +535,18 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                 // tile's first row (at most 8 * 256 rows of 256 channels)
                 uint16_t* const tile_out = out + (int64_t)m0 * p.ldo + gcol;
                 lds_barrier();   // the output tile is complete in LDS
+                // all pieces from LDS first (with the residual added), then the stores
 #pragma unroll
                 for (int k = 0; k < PER; ++k) {
                     const int r = (tid >> 4) + 32 * k;
-                    u16x8 y = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
-                    if (p.res != nullptr) y = add_f16x8(v[k], y);   // fp16(res + y), one rounding
-                    *reinterpret_cast<u16x8*>(tile_out + ((r / TILEW) * p.Wo + r % TILEW) * (int)p.ldo) = y;
-                    v[k] = p.gn_bias ? add_f16x8(y, gb) : y;
+                    const u16x8 y = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
+                    v[k] = p.res != nullptr ? add_f16x8(v[k], y) : y;   // fp16(res + y), one rounding
+                }
+#pragma unroll
+                for (int k = 0; k < PER; ++k) {
+                    const int r = (tid >> 4) + 32 * k;
+                    *reinterpret_cast<u16x8*>(tile_out + ((r / TILEW) * p.Wo + r % TILEW) * (int)p.ldo) = v[k];
+                    if (p.gn_bias) v[k] = add_f16x8(v[k], gb);
                 }
                 const int fpix = p.Ho * p.Wo;
                 const int fr = m0 / fpix, rem = m0 - fr * fpix;
@@ -821,6 +826,35 @@ __device__ __forceinline__ void write_tile(const GemmParams& p, AccV (&acc)[BM /
                     rv[i] = *reinterpret_cast<const u16x8*>(p.res + (int64_t)grow * p.ldo + gcol);
             }
             lds_barrier();   // the output tile is complete in LDS
+            if (NT % RCH == 0 && (PADWO > 0 || (p.vec_out && gcol0 + OUTW <= p.N))) {
+                // every piece is a whole 16-byte chunk and a thread keeps one chunk column: all pieces from
+                // LDS with the residual added first, then the stores
+                const int gcol = gcol0 + (tid % RCH) * 8;
+                u16x8 rb{};
+                if (p.res_bias) rb = *reinterpret_cast<const u16x8*>(p.res_bias + gcol);
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    const int idx = tid + i * NT;
+                    if (idx >= BM * RCH) continue;
+                    const int r = idx / RCH, ch = idx - r * RCH;
+                    const u16x8 v = *reinterpret_cast<const u16x8*>(ep + r * (OUTW * 2) + ((ch ^ skey(r)) << 4));
+                    if (p.res_bias) {   // fp16(res + (y + b)): both adds in fp32, one rounding
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) rv[i][e] = f2h(h2f(rv[i][e]) + (h2f(v[e]) + h2f(rb[e])));
+                    } else {
+                        rv[i] = add_f16x8(rv[i], v);   // fp16(res + y), one rounding
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < PER; ++i) {
+                    const int idx = tid + i * NT;
+                    const int r = idx / RCH;
+                    const int grow = gidx(r);
+                    if (idx >= BM * RCH || grow >= p.M) continue;
+                    store_chunk(r, grow, gcol, rv[i]);
+                }
+                return;
+            }
 #pragma unroll
             for (int i = 0; i < PER; ++i) {
                 const int idx = tid + i * NT;
