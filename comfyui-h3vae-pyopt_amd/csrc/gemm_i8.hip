@@ -1617,10 +1617,18 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     }
 
     Acc acc[FM][FN];
+    // zero accumulators; the empty asm pins the moves where this is called (otherwise they sink to just
+    // before the first MFMA, after the first wait and barrier)
+    auto zero_acc = [&]() {
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
+        for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = Acc{};
+            for (int j = 0; j < FN; ++j) {
+                Acc z = {};
+                asm volatile("" : "+v"(z));
+                acc[i][j] = z;
+            }
+    };
 
     // stage s covers depth tap kd0 + s / CQ and channel slice s % CQ; the issue
     // position is kept as a running (kd, cq) pair
@@ -1655,6 +1663,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
         };
         issue_next(0);
         issue_next(1);
+        zero_acc();                                           // while the first two stages are in flight
         wait_vmcnt<NH + NWT>();                               // stage 0 landed, stage 1 may be in flight
         lds_barrier();
 #pragma unroll
@@ -1766,6 +1775,7 @@ __global__ __launch_bounds__(512) void conv3_halo_i8(GemmParams p) {
     v4i fa[2][FM], fb[2][FN];
     issue_next(0);
     issue_next(1);
+    zero_acc();                                               // while the first two stages are in flight
     wait_vmcnt<NH + NWT>();                                   // stage 0 landed, stage 1 may be in flight
     lds_barrier();
     load_frags(0, 0, fa[0], fb[0]);
