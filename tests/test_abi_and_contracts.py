@@ -2,6 +2,7 @@
 
 * libh3vae_hip.so loads and exports every entry point declared in
   include/h3vae_hip.h, and the ctypes table covers them all;
+* bench.py refuses --gpus above 1 with a message;
 * the reference's CPU contract tests, adapted: shape/dtype/layout guards on
   meta tensors, fake (meta) op outputs, weight-quantizer validation with an
   injected quantize function, explicit failure on CPU tensors (no fallback).
@@ -275,3 +276,13 @@ def test_tile_policy(ops):
     assert resolve(64, "128x64x64") == "128x64x64"
     with pytest.raises(ValueError):
         resolve(64, "auto")
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says so, before torch is imported."""
+    import subprocess
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2", "--steps", "1", "--warmup", "0"],
+                          capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert proc.returncode == 2
+    assert "measures one MI355X" in proc.stderr and "--gpus 1" in proc.stderr
+    assert proc.stdout == ""
