@@ -1165,9 +1165,11 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
     // MFMAs of their empty rows and finish early, so the CUs that ran them start their full tiles out of
     // step with the rest and the tiles' ends (128 KB of stores each) spread out instead of all falling
     // together: H3 FFN-up (64 tail tiles, then 7 rounds of full ones) 243.5 -> 235.5 us against the tail
-    // tiles last.  The full tiles are mapped as in the other GEMMs (per-XCD contiguous ranges, grouped by
-    // 8 row blocks; the tail count is a multiple of 8 for the decoder widths, so each full tile keeps its
-    // XCD).
+    // tiles last.  The full tiles are mapped as in the other GEMMs: per-XCD contiguous ranges, grouped by
+    // row blocks (the tail count is a multiple of 8 for the decoder widths, so each full tile keeps its
+    // XCD).  Groups of 4 row blocks for outputs of 16 or more column tiles, else 8: H3 QKV 98.4 -> 96.6 us
+    // and FFN-up 231.6 -> 228.5 us with 4, attention-out 33.7 -> 34.4 us (mean of four same-box A/B runs,
+    // bit-identical); 16 was slower on every shape.
     int tm, tn;
     const int ntail = p.M % BM ? p.tiles_n : 0;
     const int nfull = p.tiles_m * p.tiles_n - ntail;
@@ -1175,7 +1177,8 @@ __global__ __launch_bounds__(512) void gemm_i8_pingpong(GemmParams p) {
         tm = p.tiles_m - 1;
         tn = blockIdx.x;
     } else {
-        grouped_tile(xcd_remap(blockIdx.x - ntail, nfull), p.tiles_m - (ntail ? 1 : 0), p.tiles_n, 8, tm, tn);
+        grouped_tile(xcd_remap(blockIdx.x - ntail, nfull), p.tiles_m - (ntail ? 1 : 0), p.tiles_n,
+                     p.tiles_n >= 16 ? 4 : 8, tm, tn);
     }
     const int m0 = tm * BM, n0 = tn * BN;
     const int nk = p.K / BK;
